@@ -1,0 +1,84 @@
+// Device-side MoE dispatch: routing bookkeeping between the router and the grouped expert kernels, with every
+// routing-dependent size kept on the device (consumers launch for the maximum and read the real extents from
+// MoePlan / ntiles_dev). Drop-in for src/kernels/moe_dispatch.hpp of the reference (single-device subset).
+//
+// The permutation is deterministic: rows of expert e are its tokens in ascending token order (the reference's
+// host path, src/model/forward_ref.hip:1302-1328), computed with scans instead of the reference device path's
+// atomic arrival order (moe_dispatch.hip:9-10). The combine follows pidx, so results never depend on it.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "unholy/kernels/exl3_moe.hpp"
+
+namespace unholy::kernels {
+
+struct MoePlan {  // ref moe_dispatch.hpp:14-20
+  int P;
+  int remote0;
+  int n_local_tiles;
+  int n_remote_tiles;
+  int n_remote_tokens;
+};
+
+// count[e] += picks of e (count zero on entry; moe_plan clears it again); hist[e] += the same. Ref :26.
+void moe_count(const int32_t* sel, int T, int K, int32_t* count, int E, hipStream_t st, uint32_t* hist = nullptr);
+// Offsets (resident experts first, then the others, each ascending), tiles of <= tile_rows rows, plan; clears
+// fill and count. resident may be null (all resident). E <= 1024. Ref :29-31.
+void moe_plan(int32_t* count, const uint8_t* resident, int E, int P, MoePlan* plan, Exl3Tile* local_tiles,
+              Exl3Tile* remote_tiles, int32_t* off, int32_t* fill, int max_tiles, hipStream_t st,
+              int tile_rows = kExl3TileRows);
+// Per token: its K picks sorted by expert id, pick j of token t -> pair row off[e] + (its rank among e's tokens).
+// eidx[p] = token, ewt[p] = weight, row_expert[p] = e, pidx[t][j] = p. fill is not used. E is taken from the
+// largest expert id present; the kernel scans sel per expert. Ref :32-33.
+void moe_scatter(const int32_t* sel, const float* wt, int T, int K, const int32_t* off, int32_t* fill, int32_t* eidx,
+                 float* ewt, int32_t* row_expert, int32_t* pidx, hipStream_t st);
+// The same outputs as moe_scatter when the expert count is known (the kernel needs E; moe_scatter derives it).
+void moe_scatter_e(const int32_t* sel, const float* wt, int T, int K, int E, const int32_t* off, int32_t* eidx,
+                   float* ewt, int32_t* row_expert, int32_t* pidx, hipStream_t st);
+
+// count + plan + scatter (optionally routing first) for steps of up to kMoeSmallMaxTokens tokens in one
+// single-block launch. Ref :79-124. The remote-side fields (remote, qin, tok2u, u2t, p2u_dst, u2p_dst, plan_dst,
+// tiles_dst, w_dst, e_dst, x_dst, q_dst, req_flag) belong to the cross-device transport: this single-GPU
+// library rejects them set (all experts must be resident).
+constexpr int kMoeSmallMaxTokens = 32;
+struct MoeSmallArgs {
+  const int32_t* sel;
+  const float* wt;
+  int T, K;
+  uint32_t* hist;
+  const uint8_t* resident;
+  int E, P, max_tiles, tile_rows;
+  MoePlan* plan;
+  Exl3Tile *lt, *rtl;
+  int32_t* eidx;
+  float* ewt;
+  int32_t *row_expert, *pidx;
+  bool remote, qin;
+  int32_t *tok2u, *u2t, *p2u_dst, *u2p_dst;
+  MoePlan* plan_dst;
+  Exl3Tile* tiles_dst;
+  float* w_dst;
+  int32_t* e_dst;
+  const float* route_logits = nullptr;  // GLM sigmoid routing in the launch
+  const float* route_bias = nullptr;
+  float route_scale = 0.0f;
+  const uint16_t* x = nullptr;
+  int dim = 0;
+  uint16_t* x_dst = nullptr;
+  const float* ds_logits = nullptr;  // DSV4 sqrt-softplus routing in the launch
+  const float* ds_bias = nullptr;
+  const float* ds_bias_vl = nullptr;
+  const int32_t* ds_tid2eid = nullptr;
+  const int32_t* ids = nullptr;
+  int vocab = 0;
+  uint8_t* q_dst = nullptr;
+  uint8_t* qs_dst = nullptr;
+  uint32_t* req_flag = nullptr;
+  uint32_t req_value = 0;
+};
+void moe_dispatch_small(const MoeSmallArgs& a, hipStream_t st);
+
+}  // namespace unholy::kernels

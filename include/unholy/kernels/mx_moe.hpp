@@ -1,0 +1,118 @@
+// MXFP4 routed-expert kernels for gfx950. Drop-in for the reference's src/kernels/mx_moe.hpp (same names,
+// signatures, weight/scale layouts and pointer-table semantics; cited per entry point below).
+//
+// Weights: e2m1 codes (two per byte, low nibble = even input) with one e8m0 scale per 32 inputs, repacked at
+// load into the tile-major layout: for 64-input slab kt and 16-output tile nt, chunk kt * (N/16) + nt holds
+// 512 code bytes (output n's 32 bytes at (n % 16) * 32) and 32 scale bytes (n's two 32-blocks at (n % 16) * 2)
+// (mx_moe.hpp:11-14 of the reference). Tables are [w1, w3, w2] x [codes, scales] x E device pointers; a null
+// entry means the expert is not on this device and its rows are skipped (mx_moe.hpp:8-9).
+//
+// Arithmetic: each expert product is sum over 32-blocks of (sum of e4m3(x) * e2m1(w)) * sa * sw with sa the
+// activation row's e8m0 scale per 128 inputs and sw the weight's per 32 (the reference's act_quant_fp8 +
+// gemm_a8w4, ref_gemm.hip:180-183). Here it runs on the CDNA4 block-scaled MFMA
+// (v_mfma_scale_f32_16x16x128_f8f6f4: A = e4m3 activation codes, B = e2m1 weight codes, per-32 e8m0 scales
+// on both operands) with fp32 accumulation: the same exact products summed in another fp32 order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "unholy/kernels/exl3_moe.hpp"
+#include "unholy/kernels/moe_dispatch.hpp"
+
+namespace unholy::kernels {
+
+using bf16 = uint16_t;
+
+// [N, K/2] codes + [N, K/32] scales -> tile-major, in place (tmp: N*K/2 + N*K/32 bytes). Ref mx_moe.hpp:27.
+void mx_repack(uint8_t* w, uint8_t* s, int N, int K, uint8_t* tmp, hipStream_t st);
+// The same permutation into separate buffers. Ref mx_moe.hpp:29.
+void mx_repack_to(const uint8_t* w, const uint8_t* s, uint8_t* tw, uint8_t* ts, int N, int K, hipStream_t st);
+
+// xa[r] = bf16(fq8_128(x[x_rows ? x_rows[r] : r])) for rows whose expert is resident. Ref mx_moe.hpp:33-34.
+void mx_xform_in(const bf16* x, int ldx, const int32_t* row_expert, const uint8_t* const* s_tab, bf16* xa, int P,
+                 int K, hipStream_t st, const int32_t* x_rows = nullptr);
+// hh[r] = bf16(fq8_128(bf16(w[r] * silu(min(g, lim)) * clamp(u, +-lim)))). Ref mx_moe.hpp:41-42.
+void mx_swiglu(const bf16* g, const bf16* u, const float* w, const int32_t* row_expert, const uint8_t* const* s_tab,
+               bf16* hh, int P, int I, float limit, hipStream_t st);
+
+// out[r] = xa[r] @ W[e]^T over each tile's rows; second projection (w3) of the same rows with w_tab2/s_tab2/out2.
+// Ref mx_moe.hpp:49-52. Preconditions: K % 128 == 0, N % 16 == 0 (looser than the reference's K % 64, N % 128
+// only where the MFMA step needs 128 inputs).
+void mx_grouped_gemm(const bf16* xa, int K, const Exl3Tile* tiles, int ntiles, const uint8_t* const* w_tab,
+                     const uint8_t* const* s_tab, bf16* out, int ldo, int N, hipStream_t st,
+                     const int* ntiles_dev = nullptr, const uint8_t* const* w_tab2 = nullptr,
+                     const uint8_t* const* s_tab2 = nullptr, bf16* out2 = nullptr, int max_rows = kExl3TileRows);
+bool mx_skinny_enabled();
+// Register-B tiles are a gfx11 design of the reference (mx_moe.hpp:54-58): false here; the setters are no-ops.
+bool mx_gemm_rb();
+void mx_gemm_force_rb(int on);
+void mx_gemm_rb_double_buffer(int on);
+// Exhaustive check of the MFMA's block-scaled decode against the closed forms: every e2m1 code x every e8m0
+// scale on the weight operand, every e4m3 code x every scale on the activation operand. Returns the
+// mismatches among results that are normal fp32 numbers (*total: how many were compared). Ref mx_moe.hpp:61
+// (there: the v_perm dequant against the LDS table).
+unsigned long long mx_check_dequant(unsigned long long* total);
+
+constexpr int kMxGemvTileRows = 8;  // ref mx_moe.hpp:67
+int mx_gemv_max_tokens();           // UNHOLY_MX_GEMV_TOKENS, default 8 (ref mx_moe.hpp:70)
+inline bool mx_use_gemv(int tokens) { return tokens <= mx_gemv_max_tokens(); }
+
+// SwiGLU (+ fake quant) in the w1/w3 launch: hh [P, N] written for every row of every tile. Ref mx_moe.hpp:74-81.
+// counters is accepted for signature compatibility and not used (one workgroup holds both projections of its
+// 128 outputs). hq / hs (extension): also (or instead) write hh as e4m3 codes [P, N] + e8m0 scales [P, N/128].
+struct MxGlu {
+  const float* w = nullptr;
+  const int32_t* row_expert = nullptr;
+  const uint8_t* const* s_tab = nullptr;
+  bf16* hh = nullptr;
+  float limit = 0.0f;
+  uint32_t* counters = nullptr;
+  uint8_t* hq = nullptr;
+  uint8_t* hs = nullptr;
+};
+bool mx_gemm_glu();
+void mx_gemm_force_glu(int on);
+// Remote token sums (ref mx_moe.hpp:90-96) belong to the cross-device transport, which this single-GPU library
+// does not implement: a non-null dst is rejected.
+struct MxSums {
+  const int32_t* u2p = nullptr;
+  const MoePlan* plan = nullptr;
+  int K = 0;
+  bf16* dst = nullptr;
+  uint32_t* counters = nullptr;
+};
+// w1 and w3 with the SwiGLU epilogue in one launch. Ref mx_moe.hpp:97-99.
+void mx_grouped_gemm_glu(const bf16* xa, int K, const Exl3Tile* tiles, int ntiles, const uint8_t* const* w1_tab,
+                         const uint8_t* const* s1_tab, const uint8_t* const* w3_tab, const uint8_t* const* s3_tab, int N,
+                         const MxGlu& glu, hipStream_t st, const int* ntiles_dev = nullptr);
+// Ref mx_moe.hpp:100-104.
+void mx_grouped_gemv(const bf16* xa, int K, const Exl3Tile* tiles, int ntiles, const uint8_t* const* w_tab,
+                     const uint8_t* const* s_tab, bf16* out, int ldo, int N, hipStream_t st,
+                     const int* ntiles_dev = nullptr, const uint8_t* const* w_tab2 = nullptr,
+                     const uint8_t* const* s_tab2 = nullptr, bf16* out2 = nullptr, int max_rows = kMxGemvTileRows,
+                     const MxGlu& glu = {}, const MxSums& sums = {});
+
+// ---- native fp8-activation forms (no reference counterpart: the activations stay as e4m3 codes + e8m0 scales
+// per 128, the operand format of the block-scaled MFMA, instead of fake-quantized bf16) -----------------------------
+// q [P, K] e4m3 + qs [P, K/128] e8m0: act_quant_fp8 of x[x_rows[r]] per 128 (rows of non-resident experts skipped).
+void mx_xform_in_fp8(const bf16* x, int ldx, const int32_t* row_expert, const uint8_t* const* s_tab, uint8_t* q,
+                     uint8_t* qs, int P, int K, hipStream_t st, const int32_t* x_rows = nullptr);
+// mx_grouped_gemv / gemm / gemm_glu with the activations as (q, qs).
+void mx_grouped_gemv_q(const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles, int ntiles,
+                       const uint8_t* const* w_tab, const uint8_t* const* s_tab, bf16* out, int ldo, int N,
+                       hipStream_t st, const int* ntiles_dev = nullptr, const uint8_t* const* w_tab2 = nullptr,
+                       const uint8_t* const* s_tab2 = nullptr, bf16* out2 = nullptr, int max_rows = kMxGemvTileRows,
+                       const MxGlu& glu = {});
+// The GEMV with fp32 outputs (no bf16 rounding): for accuracy checks against an fp64 oracle.
+void mx_grouped_gemv_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles, int ntiles,
+                              const uint8_t* const* w_tab, const uint8_t* const* s_tab, float* out, int ldo, int N,
+                              hipStream_t st, const int* ntiles_dev = nullptr, int max_rows = kMxGemvTileRows);
+void mx_grouped_gemm_q(const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles, int ntiles,
+                       const uint8_t* const* w_tab, const uint8_t* const* s_tab, bf16* out, int ldo, int N,
+                       hipStream_t st, const int* ntiles_dev = nullptr, const uint8_t* const* w_tab2 = nullptr,
+                       const uint8_t* const* s_tab2 = nullptr, bf16* out2 = nullptr, int max_rows = kExl3TileRows,
+                       const MxGlu& glu = {});
+
+}  // namespace unholy::kernels

@@ -1,0 +1,182 @@
+/* C ABI of the gfx950 quantized-MoE library (libunholy_amd.so).
+ *
+ * Each kernel entry point wraps the C++ drop-in of the same name in namespace unholy::kernels
+ * (the headers under include/unholy/kernels/), which keeps the reference's signatures, weight/scale layouts and pointer-table
+ * semantics; the reference declaration each one replaces is cited per function (paths in the reference tree
+ * ewtodd/unholy). Conventions: plain pointers and sizes; device pointers unless named h_*; bf16 = uint16_t;
+ * e4m3 / e2m1 codes and e8m0 scale exponents = uint8_t; `stream` is a hipStream_t (NULL = the null stream).
+ * Every function returns 0 on success and -1 on failure (invalid shape, HIP error); uh_last_error() then
+ * holds the message of the calling thread's last failure. Launches are asynchronous: device faults surface at
+ * the next synchronizing call.
+ */
+#ifndef UNHOLY_AMD_H
+#define UNHOLY_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- runtime (no reference counterpart: src/rt/hip.hpp's DeviceBuffer / UH_CHECK play this role there) ---- */
+const char* uh_last_error(void);
+int uh_version(void); /* the library version (a value, not a status) */
+int uh_device_count(int* n);
+int uh_set_device(int dev);
+int uh_device_name(char* buf, int len);
+int uh_malloc(void** p, size_t bytes);
+int uh_free(void* p);
+int uh_memcpy_h2d(void* dst, const void* h_src, size_t bytes);
+int uh_memcpy_d2h(void* h_dst, const void* src, size_t bytes);
+int uh_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+int uh_memset(void* dst, int value, size_t bytes, void* stream);
+int uh_synchronize(void);
+int uh_stream_create(void** stream);
+int uh_stream_destroy(void* stream);
+int uh_stream_synchronize(void* stream);
+int uh_event_create(void** ev);
+int uh_event_destroy(void* ev);
+int uh_event_record(void* ev, void* stream);
+int uh_event_synchronize(void* ev);
+int uh_event_elapsed_ms(float* ms, void* start, void* stop);
+/* Synthetic data on the device: n bytes of a splitmix64 stream (seed), each byte mapped to lo + (v % (hi-lo+1)). */
+int uh_fill_random_bytes(void* dst, size_t n, uint64_t seed, uint32_t lo, uint32_t hi, void* stream);
+
+/* ---- MXFP4 layout and activation transforms (src/kernels/mx_moe.hpp) ---- */
+/* mx_moe.hpp:27 */
+int uh_mx_repack(uint8_t* w, uint8_t* s, int N, int K, uint8_t* tmp, void* stream);
+/* mx_moe.hpp:29 */
+int uh_mx_repack_to(const uint8_t* w, const uint8_t* s, uint8_t* tw, uint8_t* ts, int N, int K, void* stream);
+/* mx_moe.hpp:33-34 (x_rows may be NULL) */
+int uh_mx_xform_in(const uint16_t* x, int ldx, const int32_t* row_expert, const uint8_t* const* s_tab, uint16_t* xa,
+                   int P, int K, void* stream, const int32_t* x_rows);
+/* No reference counterpart: mx_xform_in emitting e4m3 codes [P, K] + e8m0 scales [P, K/128] (the MFMA operand). */
+int uh_mx_xform_in_fp8(const uint16_t* x, int ldx, const int32_t* row_expert, const uint8_t* const* s_tab,
+                       uint8_t* q, uint8_t* qs, int P, int K, void* stream, const int32_t* x_rows);
+/* mx_moe.hpp:41-42 */
+int uh_mx_swiglu(const uint16_t* g, const uint16_t* u, const float* w, const int32_t* row_expert,
+                 const uint8_t* const* s_tab, uint16_t* hh, int P, int I, float limit, void* stream);
+/* mx_moe.hpp:61: exhaustive MFMA block-scaled decode check; *bad = mismatches among normal results. */
+int uh_mx_check_dequant(unsigned long long* bad, unsigned long long* total);
+
+/* ---- grouped expert GEMV / GEMM (src/kernels/mx_moe.hpp). tiles: int32 triples {expert, row0, rows}.
+ * glu_*: the MxGlu epilogue (glu_hh / glu_hq NULL: none); glu_hq + glu_hs: hh as e4m3 codes + e8m0 scales. ---- */
+/* mx_moe.hpp:100-104 */
+int uh_mx_grouped_gemv(const uint16_t* xa, int K, const int32_t* tiles, int ntiles, const uint8_t* const* w_tab,
+                       const uint8_t* const* s_tab, uint16_t* out, int ldo, int N, void* stream,
+                       const int* ntiles_dev, const uint8_t* const* w_tab2, const uint8_t* const* s_tab2,
+                       uint16_t* out2, int max_rows, const float* glu_w, const int32_t* glu_row_expert,
+                       const uint8_t* const* glu_s_tab, uint16_t* glu_hh, float glu_limit, uint32_t* glu_counters);
+/* mx_moe.hpp:49-52 */
+int uh_mx_grouped_gemm(const uint16_t* xa, int K, const int32_t* tiles, int ntiles, const uint8_t* const* w_tab,
+                       const uint8_t* const* s_tab, uint16_t* out, int ldo, int N, void* stream,
+                       const int* ntiles_dev, const uint8_t* const* w_tab2, const uint8_t* const* s_tab2,
+                       uint16_t* out2, int max_rows);
+/* mx_moe.hpp:97-99 */
+int uh_mx_grouped_gemm_glu(const uint16_t* xa, int K, const int32_t* tiles, int ntiles, const uint8_t* const* w1_tab,
+                           const uint8_t* const* s1_tab, const uint8_t* const* w3_tab, const uint8_t* const* s3_tab,
+                           int N, const float* glu_w, const int32_t* glu_row_expert, const uint8_t* const* glu_s_tab,
+                           uint16_t* glu_hh, float glu_limit, void* stream, const int* ntiles_dev);
+/* No reference counterpart: the GEMV / GEMM on e4m3 activation codes q [P, K] + e8m0 qs [P, K/128]. */
+int uh_mx_grouped_gemv_q(const uint8_t* q, const uint8_t* qs, int K, const int32_t* tiles, int ntiles,
+                         const uint8_t* const* w_tab, const uint8_t* const* s_tab, uint16_t* out, int ldo, int N,
+                         void* stream, const int* ntiles_dev, const uint8_t* const* w_tab2,
+                         const uint8_t* const* s_tab2, uint16_t* out2, int max_rows, const float* glu_w,
+                         const int32_t* glu_row_expert, const uint8_t* const* glu_s_tab, uint16_t* glu_hh,
+                         uint8_t* glu_hq, uint8_t* glu_hs, float glu_limit);
+/* No reference counterpart: uh_mx_grouped_gemv_q with fp32 outputs (before bf16 rounding), for accuracy checks. */
+int uh_mx_grouped_gemv_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const int32_t* tiles, int ntiles,
+                                const uint8_t* const* w_tab, const uint8_t* const* s_tab, float* out, int ldo, int N,
+                                void* stream, const int* ntiles_dev, int max_rows);
+int uh_mx_grouped_gemm_q(const uint8_t* q, const uint8_t* qs, int K, const int32_t* tiles, int ntiles,
+                         const uint8_t* const* w_tab, const uint8_t* const* s_tab, uint16_t* out, int ldo, int N,
+                         void* stream, const int* ntiles_dev, const uint8_t* const* w_tab2,
+                         const uint8_t* const* s_tab2, uint16_t* out2, int max_rows, const float* glu_w,
+                         const int32_t* glu_row_expert, const uint8_t* const* glu_s_tab, uint16_t* glu_hh,
+                         uint8_t* glu_hq, uint8_t* glu_hs, float glu_limit);
+
+/* ---- routing and dispatch (src/kernels/ref.hpp, src/kernels/moe_dispatch.hpp). plan: int32[5]
+ * {P, remote0, n_local_tiles, n_remote_tiles, n_remote_tokens}. ---- */
+/* ref.hpp:243-245 */
+int uh_route(const float* logits, const float* bias, const int32_t* tid2eid, const int32_t* ids, int32_t* sel,
+             float* weights, int T, int E, int K, float route_scale, void* stream, const float* bias_vl, int vocab);
+/* ref.hpp:247-249 */
+int uh_route_fast(const float* logits, const float* bias, const int32_t* tid2eid, const int32_t* ids, int32_t* sel,
+                  float* weights, int T, int E, int K, float route_scale, void* stream, const float* bias_vl,
+                  int vocab);
+/* moe_dispatch.hip:308-356 (route_token_wave, GLM sigmoid routing) */
+int uh_route_glm(const float* logits, const float* bias, int32_t* sel, float* weights, int T, int E, int K,
+                 float route_scale, void* stream);
+/* No reference counterpart: the synthetic workload's softmax top-K, renormalised over the picks. */
+int uh_route_softmax(const float* logits, int32_t* sel, float* weights, int T, int E, int K, void* stream);
+/* moe_dispatch.hpp:26 */
+int uh_moe_count(const int32_t* sel, int T, int K, int32_t* count, int E, void* stream, uint32_t* hist);
+/* moe_dispatch.hpp:29-31 (resident may be NULL: all resident) */
+int uh_moe_plan(int32_t* count, const uint8_t* resident, int E, int P, int32_t* plan, int32_t* local_tiles,
+                int32_t* remote_tiles, int32_t* off, int32_t* fill, int max_tiles, void* stream, int tile_rows);
+/* moe_dispatch.hpp:32-33 (deterministic: rows of an expert in ascending token order) */
+int uh_moe_scatter(const int32_t* sel, const float* wt, int T, int K, const int32_t* off, int32_t* fill,
+                   int32_t* eidx, float* ewt, int32_t* row_expert, int32_t* pidx, void* stream);
+/* moe_dispatch.hpp:124 (MoeSmallArgs without the remote-side fields; ds_* or route_* logits: routing in-launch) */
+int uh_moe_dispatch_small(const int32_t* sel, const float* wt, int T, int K, int E, int P, int max_tiles,
+                          int tile_rows, int32_t* plan, int32_t* tiles, int32_t* eidx, float* ewt,
+                          int32_t* row_expert, int32_t* pidx, uint32_t* hist, const float* route_logits,
+                          const float* route_bias, float route_scale, const float* ds_logits, const float* ds_bias,
+                          const float* ds_bias_vl, const int32_t* ds_tid2eid, const int32_t* ids, int vocab,
+                          void* stream);
+/* ref.hpp:251-252 */
+int uh_swiglu(const uint16_t* gate, const uint16_t* up, const float* w, uint16_t* h, int rows, int dim, float limit,
+              void* stream);
+/* ref.hpp:254 */
+int uh_scatter_add(const uint16_t* src, const int32_t* rows_idx, float* y, int n, int dim, void* stream);
+/* ref.hpp:255 */
+int uh_gather_rows(const uint16_t* src, const int32_t* rows_idx, uint16_t* dst, int n, int dim, void* stream);
+/* ref.hpp:258-259 (shared may be NULL: zero) */
+int uh_moe_combine(const uint16_t* pair_out, const int32_t* pidx, const uint16_t* shared, uint16_t* out, int T, int K,
+                   int dim, void* stream);
+
+/* ---- quantization and dense fp8 (src/kernels/ref.hpp, gemv.hpp, gemm_wmma.hpp) ---- */
+/* ref.hpp:128 */
+int uh_act_quant_fp8(const uint16_t* x, int ldx, uint8_t* q, uint8_t* s, int rows, int cols, int block, void* stream);
+/* ref.hpp:130 */
+int uh_fake_quant_fp8(uint16_t* x, int ldx, int rows, int cols, int block, void* stream);
+/* tools/ref/oracle/kernel.py:43-55 with scale_fmt=None (fp32 scales) */
+int uh_act_quant_fp8_f32s(const uint16_t* x, int ldx, uint8_t* q, float* s, int rows, int cols, int block,
+                          void* stream);
+/* ref.hpp:135-136 */
+int uh_gemm_w8a8(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, uint16_t* c, int ldc,
+                 int M, int N, int K, void* stream);
+/* gemm_wmma.hpp:15-16 */
+int uh_gemm_w8a8_wmma(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, uint16_t* c, int ldc,
+                      int M, int N, int K, void* stream);
+/* gemv.hpp:23-24 */
+int uh_gemv_w8a8(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, uint16_t* c, int ldc,
+                 int M, int N, int K, void* stream);
+/* kernel.py fp8_gemm with fp32 scales (scale_fmt=None); gemm_wmma.hip:89-100's fold */
+int uh_gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw, uint16_t* c, int ldc,
+                     int M, int N, int K, void* stream);
+/* ref.hpp:139-140 and :142-143: the reference-order (bit-exact) a8w4 GEMMs */
+int uh_gemm_a8w4(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, uint16_t* c, int ldc,
+                 int M, int N, int K, void* stream);
+int uh_gemm_a8w4_tiled(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, uint16_t* c, int ldc,
+                       int M, int N, int K, void* stream);
+/* No reference counterpart (checkpoint-side preparation): e4m3 codes of fp32 weights [N, K] with one fp32 scale per
+ * 128 x 128 block, s = max(amax, 1e-4) / 448 (fp32, times fp32(1/448)). */
+int uh_quant_weight_fp8_f32s(const float* w, uint8_t* q, float* s, int N, int K, void* stream);
+
+/* ---- the routed-expert FFN in one call (src/model/forward_ref.hip:449-474 native branch + moe_device_dispatch
+ * :1052-1156 + moe_combine): router logits [T, E] -> softmax top-K -> dispatch -> xform (fp8) -> w1/w3 + SwiGLU ->
+ * w2 -> combine into out [T, D]. tab: device table of 6 * E pointers {w1 codes, w1 scales, w3 codes, w3 scales,
+ * w2 codes, w2 scales} x E (tile-major), the layout of the reference's exl3_ptrs(m, f, E). ws: device workspace of
+ * uh_mx_moe_workspace_size bytes. sel / wt (may be NULL): the routing is also written there. ---- */
+size_t uh_mx_moe_workspace_size(int T, int K, int E, int D, int I);
+int uh_mx_moe_forward(const uint16_t* x, const float* logits, int T, int K, int E, int D, int I,
+                      const uint8_t* const* tab, float limit, void* ws, size_t ws_bytes, uint16_t* out, int32_t* sel,
+                      float* wt, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UNHOLY_AMD_H */

@@ -1,0 +1,84 @@
+"""GPU parity of the fp8 e4m3 block-scaled dense GEMM / GEMV and the reference-order a8w4 GEMM."""
+import numpy as np
+import pytest
+
+import oracle
+from tests.helpers import from_bf16, max_rel, mx_weights, randn_bf16, rel_l2
+from unholy_amd import call
+from unholy_amd.device import DeviceBuffer
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return DeviceBuffer.from_array(np.ascontiguousarray(a))
+
+
+def _weights_f32s(rng, N, K):
+    w = (rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    dw = dev(w)
+    q, s = DeviceBuffer(N * K), DeviceBuffer(((N + 127) // 128) * (K // 128) * 4)
+    call("uh_quant_weight_fp8_f32s", dw, q, s, N, K, None)
+    return q.download((N, K), np.uint8), s.download(((N + 127) // 128, K // 128), np.float32), w
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (5, 384, 1024), (64, 512, 1024), (300, 256, 512)])
+def test_fp8_f32_scales(M, N, K):
+    """BASELINE config 4 form: A bf16 -> e4m3 per 1x128 with fp32 scales; W e4m3 with fp32 128x128 scales."""
+    rng = np.random.default_rng(M + N)
+    x = randn_bf16(rng, (M, K))
+    wq, ws, w = _weights_f32s(rng, N, K)
+    # the weight quantizer against its definition: s = max(amax, 1e-4) * fp32(1/448), codes e4m3(w / s)
+    blk = np.abs(w[:128, :128]).max()
+    assert ws[0, 0] == np.float32(max(blk, np.float32(1e-4))) * np.float32(1.0 / 448.0)
+    q, sa = DeviceBuffer(M * K), DeviceBuffer(M * (K // 128) * 4)
+    call("uh_act_quant_fp8_f32s", dev(x), K, q, sa, M, K, 128, None)
+    q_ref, sa_ref = oracle.act_quant_fp8_f32s(x)
+    assert np.array_equal(q.download((M, K), np.uint8), q_ref)
+    assert np.array_equal(sa.download((M, K // 128), np.float32), sa_ref)
+    c = DeviceBuffer(M * N * 2)
+    call("uh_gemm_fp8_f32s", q, sa, dev(wq), dev(ws), c, N, M, N, K, None)
+    got = from_bf16(c.download((M, N), np.uint16))
+    ref16, _ = oracle.gemm_w8a8(q_ref, sa_ref, wq, ws)
+    ref64 = oracle.gemm_w8a8_f64(q_ref, sa_ref, wq, ws)
+    mr = max_rel(got, from_bf16(ref16))
+    print(f"fp8 f32s M={M}: max_rel {mr:.3e} rel_l2 {rel_l2(got, from_bf16(ref16)):.3e} "
+          f"vs f64 {max_rel(got, ref64):.3e}")
+    assert mr <= 1e-2
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (8, 1024, 512), (33, 256, 1024), (200, 512, 512)])
+def test_fp8_e8m0_scales(M, N, K):
+    """The reference's W8A8 contract (gemm_w8a8 / gemv_w8a8 / gemm_w8a8_wmma): e8m0 scales on both sides."""
+    rng = np.random.default_rng(M * 3 + K)
+    x = randn_bf16(rng, (M, K))
+    q_ref, sa_ref = oracle.act_quant_fp8(x)
+    wq = rng.integers(0, 256, (N, K), dtype=np.uint8)
+    wq[(wq & 0x7F) == 0x7F] = 0  # no NaN codes
+    sw = rng.integers(118, 126, ((N + 127) // 128, K // 128), dtype=np.uint8)
+    ref16, _ = oracle.gemm_w8a8(q_ref, sa_ref, wq, sw)
+    ref = from_bf16(ref16)
+    names = ["uh_gemm_w8a8", "uh_gemm_w8a8_wmma"] + (["uh_gemv_w8a8"] if M <= 32 else [])
+    outs = []
+    for name in names:
+        c = DeviceBuffer(M * N * 2)
+        call(name, dev(q_ref), dev(sa_ref), dev(wq), dev(sw), c, N, M, N, K, None)
+        outs.append(c.download((M, N), np.uint16))
+        assert max_rel(from_bf16(outs[-1]), ref) <= 1e-2, name
+    for o in outs[1:]:  # every W8A8 entry point gives the same values (a row's result does not depend on M)
+        assert np.array_equal(o, outs[0])
+
+
+@pytest.mark.parametrize("tiled", [False, True])
+def test_gemm_a8w4_reference_order_bit_exact(tiled):
+    rng = np.random.default_rng(9)
+    M, N, K = 7, 256, 512
+    x = randn_bf16(rng, (M, K))
+    q, qs = oracle.act_quant_fp8(x)
+    w, s = mx_weights(rng, N, K)
+    if tiled:
+        w, s = oracle.repack(w, s, N, K)
+    ref16, _ = oracle.gemm_a8w4(q, qs, w, s, N, tiled=tiled)
+    c = DeviceBuffer(M * N * 2)
+    call("uh_gemm_a8w4_tiled" if tiled else "uh_gemm_a8w4", dev(q), dev(qs), dev(w), dev(s), c, N, M, N, K, None)
+    assert np.array_equal(c.download((M, N), np.uint16), ref16)

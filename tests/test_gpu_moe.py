@@ -1,0 +1,158 @@
+"""GPU parity of routing, dispatch, combine and the whole routed-expert FFN against the CPU oracle."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.helpers import from_bf16, max_rel, mx_weights, randn_bf16, rel_l2
+from unholy_amd import call
+from unholy_amd.device import DeviceBuffer, pointer_table, synchronize
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return DeviceBuffer.from_array(np.ascontiguousarray(a))
+
+
+@pytest.mark.parametrize("T,E,K", [(8, 256, 6), (64, 256, 6), (300, 64, 8), (5, 1000, 3)])
+def test_route_softmax(T, E, K):
+    rng = np.random.default_rng(T)
+    logits = rng.standard_normal((T, E), dtype=np.float32)
+    logits[0, 5] = logits[0, 9] = 9.0  # a tie: the lower id first
+    sel_ref, wt_ref = oracle.route_softmax(logits, K)
+    sel, wt = DeviceBuffer(T * K * 4), DeviceBuffer(T * K * 4)
+    call("uh_route_softmax", dev(logits), sel.ptr, wt.ptr, T, E, K, None)
+    assert np.array_equal(sel.download((T, K), np.int32), sel_ref)
+    assert sel_ref[0, 0] == 5 and sel_ref[0, 1] == 9
+    np.testing.assert_allclose(wt.download((T, K), np.float32), wt_ref, rtol=2e-6, atol=0)
+
+
+@pytest.mark.parametrize("T", [1, 7, 32])
+def test_route_ds_and_glm(T):
+    rng = np.random.default_rng(11)
+    E, K = 256, 6
+    logits = rng.standard_normal((T, E), dtype=np.float32) * 3
+    bias = rng.standard_normal(E, dtype=np.float32) * 0.1
+    sel_ref, wt_ref = oracle.route_ds(logits, bias, K, 2.5)
+    for name in ("uh_route", "uh_route_fast"):
+        sel, wt = DeviceBuffer(T * K * 4), DeviceBuffer(T * K * 4)
+        call(name, dev(logits), dev(bias), None, None, sel.ptr, wt.ptr, T, E, K, 2.5, None, None, 0)
+        assert np.array_equal(sel.download((T, K), np.int32), sel_ref), name
+        np.testing.assert_allclose(wt.download((T, K), np.float32), wt_ref, rtol=1e-5)
+    gsel_ref, gwt_ref = oracle.route_glm(logits, bias, K, 1.5)
+    sel, wt = DeviceBuffer(T * K * 4), DeviceBuffer(T * K * 4)
+    call("uh_route_glm", dev(logits), dev(bias), sel.ptr, wt.ptr, T, E, K, 1.5, None)
+    assert np.array_equal(sel.download((T, K), np.int32), gsel_ref)
+    np.testing.assert_allclose(wt.download((T, K), np.float32), gwt_ref, rtol=1e-5)
+
+
+def _check_dispatch(ref, eidx, ewt, row_expert, pidx, tiles, plan, ntiles):
+    assert np.array_equal(eidx, ref["eidx"])
+    assert np.array_equal(ewt, ref["ewt"])
+    assert np.array_equal(row_expert, ref["row_expert"])
+    assert np.array_equal(pidx, ref["pidx"])
+    assert plan[0] == ref["plan"][0] and plan[2] == ref["plan"][2] == ntiles
+    assert np.array_equal(tiles[:ntiles], ref["tiles"][:ntiles])
+
+
+@pytest.mark.parametrize("T,E,K,tile_rows", [(8, 256, 6, 16), (32, 64, 8, 4), (1, 16, 2, 8)])
+def test_dispatch_small(T, E, K, tile_rows):
+    rng = np.random.default_rng(T + E)
+    sel = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    wt = rng.random((T, K)).astype(np.float32)
+    P = T * K
+    ref = oracle.dispatch(sel, wt, E, tile_rows)
+    max_tiles = P + E
+    bufs = dict(plan=DeviceBuffer(20), tiles=DeviceBuffer(max_tiles * 12), eidx=DeviceBuffer(P * 4),
+                ewt=DeviceBuffer(P * 4), row_expert=DeviceBuffer(P * 4), pidx=DeviceBuffer(P * 4))
+    call("uh_moe_dispatch_small", dev(sel), dev(wt), T, K, E, P, max_tiles, tile_rows, bufs["plan"].ptr,
+         bufs["tiles"].ptr, bufs["eidx"].ptr, bufs["ewt"].ptr, bufs["row_expert"].ptr, bufs["pidx"].ptr, None,
+         None, None, 0.0, None, None, None, None, None, 0, None)
+    plan = bufs["plan"].download(5, np.int32)
+    _check_dispatch(ref, bufs["eidx"].download(P, np.int32), bufs["ewt"].download(P, np.float32),
+                    bufs["row_expert"].download(P, np.int32), bufs["pidx"].download((T, K), np.int32),
+                    bufs["tiles"].download((max_tiles, 3), np.int32), plan, plan[2])
+
+
+@pytest.mark.parametrize("T,E,K,tile_rows", [(4096, 256, 6, 128), (100, 16, 4, 8), (33, 1024, 8, 128)])
+def test_dispatch_multi_kernel(T, E, K, tile_rows):
+    rng = np.random.default_rng(T)
+    sel = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    wt = rng.random((T, K)).astype(np.float32)
+    P = T * K
+    ref = oracle.dispatch(sel, wt, E, tile_rows)
+    max_tiles = P // tile_rows + E + 1
+    count = DeviceBuffer(E * 4)
+    count.zero()
+    off, fill, plan = DeviceBuffer(E * 4), DeviceBuffer(E * 4), DeviceBuffer(20)
+    tiles = DeviceBuffer(max_tiles * 12)
+    eidx, ewt, rex, pidx = (DeviceBuffer(P * 4) for _ in range(4))
+    dsel, dwt = dev(sel), dev(wt)
+    call("uh_moe_count", dsel.ptr, T, K, count.ptr, E, None, None)
+    call("uh_moe_plan", count.ptr, None, E, P, plan.ptr, tiles.ptr, None, off.ptr, fill.ptr, max_tiles, None,
+         tile_rows)
+    call("uh_moe_scatter", dsel.ptr, dwt.ptr, T, K, off.ptr, fill.ptr, eidx.ptr, ewt.ptr, rex.ptr, pidx.ptr, None)
+    p = plan.download(5, np.int32)
+    assert np.array_equal(off.download(E, np.int32), ref["off"])
+    assert not count.download(E, np.int32).any()  # cleared for the next step
+    _check_dispatch(ref, eidx.download(P, np.int32), ewt.download(P, np.float32), rex.download(P, np.int32),
+                    pidx.download((T, K), np.int32), tiles.download((max_tiles, 3), np.int32), p, p[2])
+
+
+def test_combine():
+    rng = np.random.default_rng(4)
+    T, K, D = 19, 6, 4096
+    P = T * K
+    pair = randn_bf16(rng, (P, D))
+    pidx = rng.permutation(P).reshape(T, K).astype(np.int32)
+    shared = randn_bf16(rng, (T, D))
+    for sh in (None, shared):
+        out = DeviceBuffer(T * D * 2)
+        call("uh_moe_combine", dev(pair), dev(pidx), None if sh is None else dev(sh), out.ptr, T, K, D,
+             None)
+        assert np.array_equal(out.download((T, D), np.uint16), oracle.moe_combine(pair, pidx, sh))
+
+
+def _moe_case(rng, T, E, K, D, I, bias_scale=0.0):
+    experts, bufs = [], []
+    for _ in range(E):
+        ex = {}
+        for (wn, sn), (n, kk) in ((("w1", "s1"), (I, D)), (("w3", "s3"), (I, D)), (("w2", "s2"), (D, I))):
+            w, s = mx_weights(rng, n, kk)
+            ex[wn], ex[sn] = oracle.repack(w, s, n, kk)
+        experts.append(ex)
+    order = ("w1", "s1", "w3", "s3", "w2", "s2")
+    for key in order:
+        bufs.append([dev(ex[key]) for ex in experts])
+    flat = [b for key_bufs in bufs for b in key_bufs]
+    tab = pointer_table(flat)
+    x = randn_bf16(rng, (T, D))
+    logits = rng.standard_normal((T, E), dtype=np.float32)
+    if bias_scale:
+        logits = logits + rng.standard_normal(E, dtype=np.float32) * np.float32(bias_scale)
+    return experts, bufs, tab, x, logits
+
+
+@pytest.mark.parametrize("T,E,K,D,I,bias", [(8, 32, 6, 1024, 512, 0.0), (64, 64, 6, 512, 256, 0.5),
+                                            (200, 16, 4, 512, 256, 0.0)])
+def test_moe_forward_vs_oracle(T, E, K, D, I, bias):
+    rng = np.random.default_rng(T * 7 + E)
+    limit = 10.0
+    experts, bufs, tab, x, logits = _moe_case(rng, T, E, K, D, I, bias)
+    sel_ref, wt_ref = oracle.route_softmax(logits, K)
+    out_ref, _ = oracle.moe_forward(x, sel_ref, wt_ref, experts, D, I, limit)
+    ws_bytes = call("uh_mx_moe_workspace_size", T, K, E, D, I)
+    ws = DeviceBuffer(ws_bytes)
+    out = DeviceBuffer(T * D * 2)
+    sel, wt = DeviceBuffer(T * K * 4), DeviceBuffer(T * K * 4)
+    call("uh_mx_moe_forward", dev(x), dev(logits), T, K, E, D, I, tab.ptr, limit, ws.ptr, ws_bytes, out.ptr,
+         sel.ptr, wt.ptr, None)
+    synchronize()
+    assert np.array_equal(sel.download((T, K), np.int32), sel_ref)
+    got = from_bf16(out.download((T, D), np.uint16))
+    ref = from_bf16(out_ref)
+    mr = max_rel(got, ref)
+    print(f"moe T={T} E={E}: max_rel {mr:.3e}, rel_l2 {rel_l2(got, ref):.3e}")
+    assert mr <= 1e-2

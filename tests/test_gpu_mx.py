@@ -1,0 +1,210 @@
+"""GPU parity of the MXFP4 expert path against the CPU oracle, through the C ABI.
+
+Bar: bit-exact for layout, quantization codes/scales, routing and permutation; bf16 outputs of the expert GEMMs
+within max-rel 1e-2 (denominator floored at 2^-8 rms) of the oracle's reference-order fp32 path, and the GEMV's fp32
+outputs within 1e-3 max-rel of the fp64 oracle on the same quantized operands.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.helpers import from_bf16, max_rel, mx_weights, randn_bf16, rel_l2
+from unholy_amd import call
+from unholy_amd.device import DeviceBuffer, pointer_table, synchronize
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return DeviceBuffer.from_array(np.ascontiguousarray(a))
+
+
+def test_check_dequant_exhaustive():
+    bad = ctypes.c_ulonglong(0)
+    total = ctypes.c_ulonglong(0)
+    call("uh_mx_check_dequant", ctypes.byref(bad), ctypes.byref(total))
+    print(f"MFMA decode check: {bad.value} mismatches of {total.value}")
+    assert total.value > 200_000
+    assert bad.value == 0
+
+
+@pytest.mark.parametrize("N,K", [(16, 64), (64, 256), (2048, 4096)])
+def test_repack_matches_oracle(N, K):
+    rng = np.random.default_rng(1)
+    w, s = mx_weights(rng, N, K, 0, 254)
+    tw_ref, ts_ref = oracle.repack(w, s, N, K)
+    dw, ds = dev(w), dev(s)
+    tw, ts = DeviceBuffer(w.nbytes), DeviceBuffer(s.nbytes)
+    call("uh_mx_repack_to", dw.ptr, ds.ptr, tw.ptr, ts.ptr, N, K, None)
+    assert np.array_equal(tw.download(tw_ref.shape, np.uint8), tw_ref)
+    assert np.array_equal(ts.download(ts_ref.shape, np.uint8), ts_ref)
+    # in place, with the caller's tmp
+    tmp = DeviceBuffer(w.nbytes + s.nbytes)
+    call("uh_mx_repack", dw.ptr, ds.ptr, N, K, tmp.ptr, None)
+    assert np.array_equal(dw.download(tw_ref.shape, np.uint8), tw_ref)
+    assert np.array_equal(ds.download(ts_ref.shape, np.uint8), ts_ref)
+
+
+@pytest.mark.parametrize("block", [32, 64, 128])
+def test_act_quant_bit_exact(block):
+    rng = np.random.default_rng(2)
+    x = randn_bf16(rng, (37, 1024), 3.0)
+    x[0, :block] = 0  # amax floor
+    x[1, :block] = randn_bf16(rng, (block,), 1e-7)  # tiny block
+    q_ref, s_ref = oracle.act_quant_fp8(x, block)
+    dx = dev(x)
+    q, s = DeviceBuffer(q_ref.nbytes), DeviceBuffer(s_ref.nbytes)
+    call("uh_act_quant_fp8", dx.ptr, 1024, q.ptr, s.ptr, 37, 1024, block, None)
+    assert np.array_equal(q.download(q_ref.shape, np.uint8), q_ref)
+    assert np.array_equal(s.download(s_ref.shape, np.uint8), s_ref)
+    call("uh_fake_quant_fp8", dx.ptr, 1024, 37, 1024, block, None)
+    assert np.array_equal(dx.download(x.shape, np.uint16), oracle.fake_quant_fp8(x, block))
+    q32_ref, s32_ref = oracle.act_quant_fp8_f32s(x, block)
+    dx.upload(x)
+    s32 = DeviceBuffer(s32_ref.nbytes)
+    call("uh_act_quant_fp8_f32s", dx.ptr, 1024, q.ptr, s32.ptr, 37, 1024, block, None)
+    assert np.array_equal(q.download(q32_ref.shape, np.uint8), q32_ref)
+    assert np.array_equal(s32.download(s32_ref.shape, np.float32), s32_ref)
+
+
+def test_xform_in_gathered_rows():
+    rng = np.random.default_rng(3)
+    T, K, P, E = 9, 512, 20, 4
+    x = randn_bf16(rng, (T, K))
+    x_rows = rng.integers(0, T, P).astype(np.int32)
+    row_expert = rng.integers(0, E, P).astype(np.int32)
+    present = DeviceBuffer(16)
+    tab = pointer_table([present, None, present, present])  # expert 1 not resident: its rows skipped
+    gathered = x[x_rows]
+    fq_ref = oracle.fake_quant_fp8(gathered)
+    q_ref, s_ref = oracle.act_quant_fp8(gathered)
+    dx, dr, de = dev(x), dev(x_rows), dev(row_expert)
+    xa = DeviceBuffer(P * K * 2)
+    xa.zero()
+    call("uh_mx_xform_in", dx.ptr, K, de.ptr, tab.ptr, xa.ptr, P, K, None, dr.ptr)
+    q, s = DeviceBuffer(P * K), DeviceBuffer(P * K // 128)
+    q.zero()
+    s.zero()
+    call("uh_mx_xform_in_fp8", dx.ptr, K, de.ptr, tab.ptr, q.ptr, s.ptr, P, K, None, dr.ptr)
+    got, gq, gs = xa.download((P, K), np.uint16), q.download((P, K), np.uint8), s.download((P, K // 128), np.uint8)
+    live = row_expert != 1
+    assert np.array_equal(got[live], fq_ref[live])
+    assert np.array_equal(gq[live], q_ref[live]) and np.array_equal(gs[live], s_ref[live])
+    assert not got[~live].any() and not gq[~live].any()
+
+
+def _expert_tables(experts, keys):
+    bufs = {k: [dev(ex[k]) if ex is not None else None for ex in experts] for k in keys}
+    tabs = {k: pointer_table(bufs[k]) for k in keys}
+    return bufs, tabs
+
+
+def _make_experts(rng, E, N, K, names=("w", "s")):
+    out = []
+    for _ in range(E):
+        w, s = mx_weights(rng, N, K)
+        tw, ts = oracle.repack(w, s, N, K)
+        out.append({names[0]: tw, names[1]: ts})
+    return out
+
+
+def test_single_gemv_config0():
+    """x [1, 4096] ~ N(0,1), W [2048, 4096] MXFP4 with e8m0 in [119, 125], seed 0."""
+    rng = np.random.default_rng(0)
+    N, K = 2048, 4096
+    x = randn_bf16(rng, (1, K))
+    w, s = mx_weights(rng, N, K)
+    tw, ts = oracle.repack(w, s, N, K)
+    q, qs = oracle.act_quant_fp8(x)
+    ref16, ref32 = oracle.gemm_a8w4(q, qs, w, s, N)
+    ref64 = oracle.gemm_a8w4_f64(q, qs, w, s, N)
+    dq, dqs, dw, ds = dev(q), dev(qs), dev(tw), dev(ts)
+    wt, st = pointer_table([dw]), pointer_table([ds])
+    tiles = dev(np.array([[0, 0, 1]], np.int32))
+    out = DeviceBuffer(N * 2)
+    call("uh_mx_grouped_gemv_q", dq.ptr, dqs.ptr, K, tiles.ptr, 1, wt.ptr, st.ptr, out.ptr, N, N, None, None,
+         None, None, None, 1, None, None, None, None, None, None, 0.0)
+    out32 = DeviceBuffer(N * 4)
+    call("uh_mx_grouped_gemv_q_f32out", dq.ptr, dqs.ptr, K, tiles.ptr, 1, wt.ptr, st.ptr, out32.ptr, N, N, None,
+         None, 1)
+    got = from_bf16(out.download((1, N), np.uint16))
+    got32 = out32.download((1, N), np.float32)
+    mr, mr64 = max_rel(got, from_bf16(ref16)), max_rel(got32, ref64)
+    print(f"config0: max_rel vs ref {mr:.3e}, rel_l2 {rel_l2(got, from_bf16(ref16)):.3e}, fp32 vs fp64 {mr64:.3e}, "
+          f"bit-identical {np.mean(out.download((1, N), np.uint16) == ref16):.4f}")
+    assert mr <= 1e-2
+    assert mr64 <= 1e-3
+    # the drop-in form: bf16 fake-quantized xa -> the same MFMA operands
+    xa = DeviceBuffer(K * 2)
+    call("uh_mx_xform_in", dev(x), K, dev(np.zeros(1, np.int32)), st.ptr, xa.ptr, 1, K, None, None)
+    out2 = DeviceBuffer(N * 2)
+    call("uh_mx_grouped_gemv", xa.ptr, K, tiles.ptr, 1, wt.ptr, st.ptr, out2.ptr, N, N, None, None, None, None, None,
+         8, None, None, None, None, 0.0, None)
+    assert np.array_equal(out2.download((1, N), np.uint16), out.download((1, N), np.uint16))
+
+
+@pytest.mark.parametrize("abf16", [False, True])
+def test_grouped_gemv_glu(abf16):
+    """Tiles of 1-16 rows over several experts, w1 and w3 in one launch with the SwiGLU epilogue."""
+    rng = np.random.default_rng(5)
+    E, K, N, limit = 5, 1024, 512, 10.0
+    rows = [3, 16, 1, 0, 11]
+    P = sum(rows)
+    tiles, row_expert, r0 = [], [], 0
+    for e, c in enumerate(rows):
+        if c:
+            tiles.append([e, r0, c])
+        row_expert += [e] * c
+        r0 += c
+    tiles.append([2, 0, 0])  # an empty tile past the live count
+    ntiles_live = len(tiles) - 1
+    row_expert = np.array(row_expert, np.int32)
+    w1 = _make_experts(rng, E, N, K)
+    w3 = _make_experts(rng, E, N, K)
+    w1raw = [oracle.unrepack(ex["w"], ex["s"], N, K) for ex in w1]
+    w3raw = [oracle.unrepack(ex["w"], ex["s"], N, K) for ex in w3]
+    x = randn_bf16(rng, (P, K))
+    q, qs = oracle.act_quant_fp8(x)
+    rw = rng.random(P).astype(np.float32)
+    g_ref = np.zeros((P, N), np.uint16)
+    u_ref = np.zeros((P, N), np.uint16)
+    for t in tiles[:ntiles_live]:
+        e, a, c = t
+        g_ref[a:a + c] = oracle.gemm_a8w4(q[a:a + c], qs[a:a + c], *w1raw[e], N)[0]
+        u_ref[a:a + c] = oracle.gemm_a8w4(q[a:a + c], qs[a:a + c], *w3raw[e], N)[0]
+    b1, t1 = _expert_tables(w1, ("w", "s"))
+    b3, t3 = _expert_tables(w3, ("w", "s"))
+    dtiles = dev(np.array(tiles, np.int32))
+    ntd = dev(np.array([ntiles_live], np.int32))
+    g, u, hh = DeviceBuffer(P * N * 2), DeviceBuffer(P * N * 2), DeviceBuffer(P * N * 2)
+    de, drw = dev(row_expert), dev(rw)
+    if abf16:
+        xa = dev(oracle.fake_quant_fp8(x))
+        call("uh_mx_grouped_gemv", xa.ptr, K, dtiles.ptr, len(tiles), t1["w"].ptr, t1["s"].ptr, g.ptr, N, N, None,
+             ntd.ptr, t3["w"].ptr, t3["s"].ptr, u.ptr, 16, drw.ptr, de.ptr, t1["s"].ptr, hh.ptr, limit, None)
+    else:
+        hq, hs = DeviceBuffer(P * N), DeviceBuffer(P * N // 128)
+        call("uh_mx_grouped_gemv_q", dev(q), dev(qs), K, dtiles.ptr, len(tiles), t1["w"].ptr, t1["s"].ptr,
+             g.ptr, N, N, None, ntd.ptr, t3["w"].ptr, t3["s"].ptr, u.ptr, 16, drw.ptr, de.ptr, t1["s"].ptr, hh.ptr,
+             hq.ptr, hs.ptr, limit)
+    synchronize()
+    gg, uu, hgot = (b.download((P, N), np.uint16) for b in (g, u, hh))
+    assert max_rel(from_bf16(gg), from_bf16(g_ref)) <= 1e-2
+    assert max_rel(from_bf16(uu), from_bf16(u_ref)) <= 1e-2
+    # The epilogue on the kernel's own g / u: swiglu + fake quant as the reference's mx_swiglu.
+    h_ref = oracle.fake_quant_fp8(oracle.swiglu(gg, uu, rw, limit))
+    frac = np.mean(hgot == h_ref)
+    print(f"glu abf16={abf16}: hh bit-identical fraction {frac:.6f}")
+    assert max_rel(from_bf16(hgot), from_bf16(h_ref)) <= 1e-2
+    assert frac > 0.999
+    if not abf16:
+        # codes x scales are exactly the fake-quantized values (the codes themselves are act_quant's of the
+        # SwiGLU output, so for rows where it is bit-identical they equal the oracle's codes too)
+        codes, scales = hq.download((P, N), np.uint8), hs.download((P, N // 128), np.uint8)
+        deq = oracle.e4m3_to_f32(codes) * np.ldexp(1.0, scales.astype(np.int32) - 127).repeat(128, axis=1)
+        assert np.array_equal(deq.astype(np.float32), from_bf16(hgot))
+        q2, s2 = oracle.act_quant_fp8(oracle.swiglu(gg, uu, rw, limit))
+        same = (hgot == h_ref).all(axis=1)
+        assert np.array_equal(codes[same], q2[same]) and np.array_equal(scales[same], s2[same])

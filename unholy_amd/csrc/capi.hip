@@ -1,0 +1,456 @@
+// The C ABI (include/unholy_amd.h): exception-to-status wrappers over the C++ entry points, device memory and
+// stream helpers for hosts without a HIP binding (the Python package binds this library with ctypes), the
+// synthetic-data generator and the one-call routed-expert FFN.
+#include <cstring>
+#include <string>
+
+#include "common.hpp"
+#include "numerics.hpp"
+#include "unholy/kernels/gemm_wmma.hpp"
+#include "unholy/kernels/gemv.hpp"
+#include "unholy/kernels/moe_dispatch.hpp"
+#include "unholy/kernels/mx_moe.hpp"
+#include "unholy/kernels/ref.hpp"
+#include "unholy_amd.h"
+
+namespace k = unholy::kernels;
+using uh::bf16;
+
+namespace {
+
+thread_local std::string g_err;
+
+template <class F>
+int guard(F&& f) {
+  try {
+    f();
+    return 0;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+  } catch (...) {
+    g_err = "unknown error";
+  }
+  return -1;
+}
+
+inline hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
+inline const k::Exl3Tile* T3(const int32_t* p) { return reinterpret_cast<const k::Exl3Tile*>(p); }
+
+__global__ void fill_random_kernel(uint8_t* dst, size_t n, uint64_t seed, uint32_t lo, uint32_t span) {
+  for (size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x; i < (n + 7) / 8; i += size_t(gridDim.x) * blockDim.x) {
+    uint64_t z = seed + 0x9e3779b97f4a7c15ull * (i + 1);  // splitmix64
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    z ^= z >> 31;
+    for (int b = 0; b < 8 && i * 8 + b < n; ++b) dst[i * 8 + b] = uint8_t(lo + uint32_t((z >> (8 * b)) & 0xff) % span);
+  }
+}
+
+// Weight quantization for the dense fp8 workload: a block per 128 x 128 tile, amax over the tile.
+__global__ __launch_bounds__(256) void quant_weight_kernel(const float* w, uint8_t* q, float* s, int N, int K) {
+  __shared__ float red[4];
+  const int bn = blockIdx.y, bk = blockIdx.x, kb = K / 128;
+  float am = 0.0f;
+  for (int i = threadIdx.x; i < 128 * 128; i += 256) {
+    const int r = bn * 128 + i / 128, c = bk * 128 + i % 128;
+    if (r < N) am = fmaxf(am, fabsf(w[size_t(r) * K + c]));
+  }
+  am = uh::wave_max(am);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = am;
+  __syncthreads();
+  am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float sc = fmaxf(am, 1e-4f) * (1.0f / 448.0f);
+  for (int i = threadIdx.x; i < 128 * 128; i += 256) {
+    const int r = bn * 128 + i / 128, c = bk * 128 + i % 128;
+    if (r < N) q[size_t(r) * K + c] = uh::fp8_code(w[size_t(r) * K + c], sc);
+  }
+  if (threadIdx.x == 0) s[size_t(bn) * kb + bk] = sc;
+}
+
+// Workspace carve-up of uh_mx_moe_forward.
+struct MoeWs {
+  int32_t *count, *off, *fill, *plan, *tiles, *eidx, *row_expert, *pidx, *sel;
+  float *ewt, *wt;
+  uint8_t *xq, *xs, *hq, *hs;
+  bf16* pair_out;
+  size_t bytes;
+  int max_tiles, tile_rows;
+};
+MoeWs carve(char* base, int T, int K, int E, int D, int I) {
+  MoeWs w{};
+  const size_t P = size_t(T) * K;
+  w.tile_rows = T <= 64 ? 16 : k::kExl3TileRows;
+  w.max_tiles = int(std::min<size_t>(P, size_t(E) + P / size_t(w.tile_rows) + 1));
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    char* p = base ? base + o : nullptr;
+    o += (bytes + 255) / 256 * 256;
+    return p;
+  };
+  w.count = reinterpret_cast<int32_t*>(take(size_t(E) * 4));
+  w.off = reinterpret_cast<int32_t*>(take(size_t(E) * 4));
+  w.fill = reinterpret_cast<int32_t*>(take(size_t(E) * 4));
+  w.plan = reinterpret_cast<int32_t*>(take(sizeof(k::MoePlan)));
+  w.tiles = reinterpret_cast<int32_t*>(take(size_t(w.max_tiles) * sizeof(k::Exl3Tile)));
+  w.eidx = reinterpret_cast<int32_t*>(take(P * 4));
+  w.row_expert = reinterpret_cast<int32_t*>(take(P * 4));
+  w.pidx = reinterpret_cast<int32_t*>(take(P * 4));
+  w.sel = reinterpret_cast<int32_t*>(take(P * 4));
+  w.ewt = reinterpret_cast<float*>(take(P * 4));
+  w.wt = reinterpret_cast<float*>(take(P * 4));
+  w.xq = reinterpret_cast<uint8_t*>(take(P * D));
+  w.xs = reinterpret_cast<uint8_t*>(take(P * (D / 128)));
+  w.hq = reinterpret_cast<uint8_t*>(take(P * I));
+  w.hs = reinterpret_cast<uint8_t*>(take(P * (I / 128)));
+  w.pair_out = reinterpret_cast<bf16*>(take(P * D * 2));
+  w.bytes = o;
+  return w;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* uh_last_error(void) { return g_err.c_str(); }
+int uh_version(void) { return 1; }
+int uh_device_count(int* n) {
+  return guard([&] { UH_CHECK(hipGetDeviceCount(n)); });
+}
+int uh_set_device(int dev) {
+  return guard([&] { UH_CHECK(hipSetDevice(dev)); });
+}
+int uh_device_name(char* buf, int len) {
+  return guard([&] {
+    int dev = 0;
+    UH_CHECK(hipGetDevice(&dev));
+    hipDeviceProp_t p{};
+    UH_CHECK(hipGetDeviceProperties(&p, dev));
+    std::snprintf(buf, size_t(len), "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
+  });
+}
+int uh_malloc(void** p, size_t bytes) {
+  return guard([&] { UH_CHECK(hipMalloc(p, bytes ? bytes : 1)); });
+}
+int uh_free(void* p) {
+  return guard([&] { UH_CHECK(hipFree(p)); });
+}
+int uh_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+  return guard([&] { UH_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice)); });
+}
+int uh_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+  return guard([&] { UH_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost)); });
+}
+int uh_memcpy_d2d(void* dst, const void* src, size_t bytes, void* st) {
+  return guard([&] { UH_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, S(st))); });
+}
+int uh_memset(void* dst, int value, size_t bytes, void* st) {
+  return guard([&] { UH_CHECK(hipMemsetAsync(dst, value, bytes, S(st))); });
+}
+int uh_synchronize(void) {
+  return guard([&] { UH_CHECK(hipDeviceSynchronize()); });
+}
+int uh_stream_create(void** st) {
+  return guard([&] {
+    hipStream_t s;
+    UH_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *st = s;
+  });
+}
+int uh_stream_destroy(void* st) {
+  return guard([&] { UH_CHECK(hipStreamDestroy(S(st))); });
+}
+int uh_stream_synchronize(void* st) {
+  return guard([&] { UH_CHECK(hipStreamSynchronize(S(st))); });
+}
+int uh_event_create(void** ev) {
+  return guard([&] {
+    hipEvent_t e;
+    UH_CHECK(hipEventCreate(&e));
+    *ev = e;
+  });
+}
+int uh_event_destroy(void* ev) {
+  return guard([&] { UH_CHECK(hipEventDestroy(static_cast<hipEvent_t>(ev))); });
+}
+int uh_event_record(void* ev, void* st) {
+  return guard([&] { UH_CHECK(hipEventRecord(static_cast<hipEvent_t>(ev), S(st))); });
+}
+int uh_event_synchronize(void* ev) {
+  return guard([&] { UH_CHECK(hipEventSynchronize(static_cast<hipEvent_t>(ev))); });
+}
+int uh_event_elapsed_ms(float* ms, void* a, void* b) {
+  return guard([&] { UH_CHECK(hipEventElapsedTime(ms, static_cast<hipEvent_t>(a), static_cast<hipEvent_t>(b))); });
+}
+int uh_fill_random_bytes(void* dst, size_t n, uint64_t seed, uint32_t lo, uint32_t hi, void* st) {
+  return guard([&] {
+    if (hi < lo || hi > 255) throw std::runtime_error("uh_fill_random_bytes: need lo <= hi <= 255");
+    if (!n) return;
+    const unsigned grid = unsigned(std::min<size_t>(uh::cdiv((n + 7) / 8, 256), 65536));
+    fill_random_kernel<<<grid, 256, 0, S(st)>>>(static_cast<uint8_t*>(dst), n, seed, lo, hi - lo + 1);
+    UH_CHECK_LAUNCH();
+  });
+}
+
+int uh_mx_repack(uint8_t* w, uint8_t* s, int N, int K, uint8_t* tmp, void* st) {
+  return guard([&] { k::mx_repack(w, s, N, K, tmp, S(st)); });
+}
+int uh_mx_repack_to(const uint8_t* w, const uint8_t* s, uint8_t* tw, uint8_t* ts, int N, int K, void* st) {
+  return guard([&] { k::mx_repack_to(w, s, tw, ts, N, K, S(st)); });
+}
+int uh_mx_xform_in(const uint16_t* x, int ldx, const int32_t* row_expert, const uint8_t* const* s_tab, uint16_t* xa,
+                   int P, int K, void* st, const int32_t* x_rows) {
+  return guard([&] { k::mx_xform_in(x, ldx, row_expert, s_tab, xa, P, K, S(st), x_rows); });
+}
+int uh_mx_xform_in_fp8(const uint16_t* x, int ldx, const int32_t* row_expert, const uint8_t* const* s_tab,
+                       uint8_t* q, uint8_t* qs, int P, int K, void* st, const int32_t* x_rows) {
+  return guard([&] { k::mx_xform_in_fp8(x, ldx, row_expert, s_tab, q, qs, P, K, S(st), x_rows); });
+}
+int uh_mx_swiglu(const uint16_t* g, const uint16_t* u, const float* w, const int32_t* row_expert,
+                 const uint8_t* const* s_tab, uint16_t* hh, int P, int I, float limit, void* st) {
+  return guard([&] { k::mx_swiglu(g, u, w, row_expert, s_tab, hh, P, I, limit, S(st)); });
+}
+int uh_mx_check_dequant(unsigned long long* bad, unsigned long long* total) {
+  return guard([&] { *bad = k::mx_check_dequant(total); });
+}
+
+int uh_mx_grouped_gemv(const uint16_t* xa, int K, const int32_t* tiles, int ntiles, const uint8_t* const* w_tab,
+                       const uint8_t* const* s_tab, uint16_t* out, int ldo, int N, void* st, const int* ntiles_dev,
+                       const uint8_t* const* w_tab2, const uint8_t* const* s_tab2, uint16_t* out2, int max_rows,
+                       const float* glu_w, const int32_t* glu_row_expert, const uint8_t* const* glu_s_tab,
+                       uint16_t* glu_hh, float glu_limit, uint32_t* glu_counters) {
+  return guard([&] {
+    k::MxGlu glu{glu_w, glu_row_expert, glu_s_tab, glu_hh, glu_limit, glu_counters};
+    k::mx_grouped_gemv(xa, K, T3(tiles), ntiles, w_tab, s_tab, out, ldo, N, S(st), ntiles_dev, w_tab2, s_tab2, out2,
+                       max_rows, glu);
+  });
+}
+int uh_mx_grouped_gemm(const uint16_t* xa, int K, const int32_t* tiles, int ntiles, const uint8_t* const* w_tab,
+                       const uint8_t* const* s_tab, uint16_t* out, int ldo, int N, void* st, const int* ntiles_dev,
+                       const uint8_t* const* w_tab2, const uint8_t* const* s_tab2, uint16_t* out2, int max_rows) {
+  return guard([&] {
+    k::mx_grouped_gemm(xa, K, T3(tiles), ntiles, w_tab, s_tab, out, ldo, N, S(st), ntiles_dev, w_tab2, s_tab2, out2,
+                       max_rows);
+  });
+}
+int uh_mx_grouped_gemm_glu(const uint16_t* xa, int K, const int32_t* tiles, int ntiles, const uint8_t* const* w1_tab,
+                           const uint8_t* const* s1_tab, const uint8_t* const* w3_tab, const uint8_t* const* s3_tab,
+                           int N, const float* glu_w, const int32_t* glu_row_expert, const uint8_t* const* glu_s_tab,
+                           uint16_t* glu_hh, float glu_limit, void* st, const int* ntiles_dev) {
+  return guard([&] {
+    k::MxGlu glu{glu_w, glu_row_expert, glu_s_tab, glu_hh, glu_limit, nullptr};
+    k::mx_grouped_gemm_glu(xa, K, T3(tiles), ntiles, w1_tab, s1_tab, w3_tab, s3_tab, N, glu, S(st), ntiles_dev);
+  });
+}
+int uh_mx_grouped_gemv_q(const uint8_t* q, const uint8_t* qs, int K, const int32_t* tiles, int ntiles,
+                         const uint8_t* const* w_tab, const uint8_t* const* s_tab, uint16_t* out, int ldo, int N,
+                         void* st, const int* ntiles_dev, const uint8_t* const* w_tab2, const uint8_t* const* s_tab2,
+                         uint16_t* out2, int max_rows, const float* glu_w, const int32_t* glu_row_expert,
+                         const uint8_t* const* glu_s_tab, uint16_t* glu_hh, uint8_t* glu_hq, uint8_t* glu_hs,
+                         float glu_limit) {
+  return guard([&] {
+    k::MxGlu glu{glu_w, glu_row_expert, glu_s_tab, glu_hh, glu_limit, nullptr, glu_hq, glu_hs};
+    k::mx_grouped_gemv_q(q, qs, K, T3(tiles), ntiles, w_tab, s_tab, out, ldo, N, S(st), ntiles_dev, w_tab2, s_tab2,
+                         out2, max_rows, glu);
+  });
+}
+int uh_mx_grouped_gemv_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const int32_t* tiles, int ntiles,
+                                const uint8_t* const* w_tab, const uint8_t* const* s_tab, float* out, int ldo, int N,
+                                void* st, const int* ntiles_dev, int max_rows) {
+  return guard([&] {
+    k::mx_grouped_gemv_q_f32out(q, qs, K, T3(tiles), ntiles, w_tab, s_tab, out, ldo, N, S(st), ntiles_dev, max_rows);
+  });
+}
+int uh_mx_grouped_gemm_q(const uint8_t* q, const uint8_t* qs, int K, const int32_t* tiles, int ntiles,
+                         const uint8_t* const* w_tab, const uint8_t* const* s_tab, uint16_t* out, int ldo, int N,
+                         void* st, const int* ntiles_dev, const uint8_t* const* w_tab2, const uint8_t* const* s_tab2,
+                         uint16_t* out2, int max_rows, const float* glu_w, const int32_t* glu_row_expert,
+                         const uint8_t* const* glu_s_tab, uint16_t* glu_hh, uint8_t* glu_hq, uint8_t* glu_hs,
+                         float glu_limit) {
+  return guard([&] {
+    k::MxGlu glu{glu_w, glu_row_expert, glu_s_tab, glu_hh, glu_limit, nullptr, glu_hq, glu_hs};
+    k::mx_grouped_gemm_q(q, qs, K, T3(tiles), ntiles, w_tab, s_tab, out, ldo, N, S(st), ntiles_dev, w_tab2, s_tab2,
+                         out2, max_rows, glu);
+  });
+}
+
+int uh_route(const float* logits, const float* bias, const int32_t* tid2eid, const int32_t* ids, int32_t* sel,
+             float* weights, int T, int E, int K, float route_scale, void* st, const float* bias_vl, int vocab) {
+  return guard([&] { k::route(logits, bias, tid2eid, ids, sel, weights, T, E, K, route_scale, S(st), bias_vl, vocab); });
+}
+int uh_route_fast(const float* logits, const float* bias, const int32_t* tid2eid, const int32_t* ids, int32_t* sel,
+                  float* weights, int T, int E, int K, float route_scale, void* st, const float* bias_vl, int vocab) {
+  return guard(
+      [&] { k::route_fast(logits, bias, tid2eid, ids, sel, weights, T, E, K, route_scale, S(st), bias_vl, vocab); });
+}
+int uh_route_glm(const float* logits, const float* bias, int32_t* sel, float* weights, int T, int E, int K,
+                 float route_scale, void* st) {
+  return guard([&] { k::route_glm(logits, bias, sel, weights, T, E, K, route_scale, S(st)); });
+}
+int uh_route_softmax(const float* logits, int32_t* sel, float* weights, int T, int E, int K, void* st) {
+  return guard([&] { k::route_softmax(logits, sel, weights, T, E, K, S(st)); });
+}
+int uh_moe_count(const int32_t* sel, int T, int K, int32_t* count, int E, void* st, uint32_t* hist) {
+  return guard([&] { k::moe_count(sel, T, K, count, E, S(st), hist); });
+}
+int uh_moe_plan(int32_t* count, const uint8_t* resident, int E, int P, int32_t* plan, int32_t* local_tiles,
+                int32_t* remote_tiles, int32_t* off, int32_t* fill, int max_tiles, void* st, int tile_rows) {
+  return guard([&] {
+    k::moe_plan(count, resident, E, P, reinterpret_cast<k::MoePlan*>(plan), reinterpret_cast<k::Exl3Tile*>(local_tiles),
+                reinterpret_cast<k::Exl3Tile*>(remote_tiles), off, fill, max_tiles, S(st), tile_rows);
+  });
+}
+int uh_moe_scatter(const int32_t* sel, const float* wt, int T, int K, const int32_t* off, int32_t* fill,
+                   int32_t* eidx, float* ewt, int32_t* row_expert, int32_t* pidx, void* st) {
+  return guard([&] { k::moe_scatter(sel, wt, T, K, off, fill, eidx, ewt, row_expert, pidx, S(st)); });
+}
+int uh_moe_dispatch_small(const int32_t* sel, const float* wt, int T, int K, int E, int P, int max_tiles,
+                          int tile_rows, int32_t* plan, int32_t* tiles, int32_t* eidx, float* ewt,
+                          int32_t* row_expert, int32_t* pidx, uint32_t* hist, const float* route_logits,
+                          const float* route_bias, float route_scale, const float* ds_logits, const float* ds_bias,
+                          const float* ds_bias_vl, const int32_t* ds_tid2eid, const int32_t* ids, int vocab,
+                          void* st) {
+  return guard([&] {
+    k::MoeSmallArgs a{};
+    a.sel = sel;
+    a.wt = wt;
+    a.T = T;
+    a.K = K;
+    a.hist = hist;
+    a.E = E;
+    a.P = P;
+    a.max_tiles = max_tiles;
+    a.tile_rows = tile_rows;
+    a.plan = reinterpret_cast<k::MoePlan*>(plan);
+    a.lt = reinterpret_cast<k::Exl3Tile*>(tiles);
+    a.eidx = eidx;
+    a.ewt = ewt;
+    a.row_expert = row_expert;
+    a.pidx = pidx;
+    a.route_logits = route_logits;
+    a.route_bias = route_bias;
+    a.route_scale = route_scale;
+    a.ds_logits = ds_logits;
+    a.ds_bias = ds_bias;
+    a.ds_bias_vl = ds_bias_vl;
+    a.ds_tid2eid = ds_tid2eid;
+    a.ids = ids;
+    a.vocab = vocab;
+    k::moe_dispatch_small(a, S(st));
+  });
+}
+int uh_swiglu(const uint16_t* gate, const uint16_t* up, const float* w, uint16_t* h, int rows, int dim, float limit,
+              void* st) {
+  return guard([&] { k::swiglu(gate, up, w, h, rows, dim, limit, S(st)); });
+}
+int uh_scatter_add(const uint16_t* src, const int32_t* rows_idx, float* y, int n, int dim, void* st) {
+  return guard([&] { k::scatter_add(src, rows_idx, y, n, dim, S(st)); });
+}
+int uh_gather_rows(const uint16_t* src, const int32_t* rows_idx, uint16_t* dst, int n, int dim, void* st) {
+  return guard([&] { k::gather_rows(src, rows_idx, dst, n, dim, S(st)); });
+}
+int uh_moe_combine(const uint16_t* pair_out, const int32_t* pidx, const uint16_t* shared, uint16_t* out, int T, int K,
+                   int dim, void* st) {
+  return guard([&] { k::moe_combine(pair_out, pidx, shared, out, T, K, dim, S(st)); });
+}
+
+int uh_act_quant_fp8(const uint16_t* x, int ldx, uint8_t* q, uint8_t* s, int rows, int cols, int block, void* st) {
+  return guard([&] { k::act_quant_fp8(x, ldx, q, s, rows, cols, block, S(st)); });
+}
+int uh_fake_quant_fp8(uint16_t* x, int ldx, int rows, int cols, int block, void* st) {
+  return guard([&] { k::fake_quant_fp8(x, ldx, rows, cols, block, S(st)); });
+}
+int uh_act_quant_fp8_f32s(const uint16_t* x, int ldx, uint8_t* q, float* s, int rows, int cols, int block, void* st) {
+  return guard([&] { k::act_quant_fp8_f32s(x, ldx, q, s, rows, cols, block, S(st)); });
+}
+int uh_gemm_w8a8(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, uint16_t* c, int ldc,
+                 int M, int N, int K, void* st) {
+  return guard([&] { k::gemm_w8a8(a, sa, w, sw, c, ldc, M, N, K, S(st)); });
+}
+int uh_gemm_w8a8_wmma(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, uint16_t* c, int ldc,
+                      int M, int N, int K, void* st) {
+  return guard([&] { k::gemm_w8a8_wmma(a, sa, w, sw, c, ldc, M, N, K, S(st)); });
+}
+int uh_gemv_w8a8(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, uint16_t* c, int ldc,
+                 int M, int N, int K, void* st) {
+  return guard([&] { k::gemv_w8a8(a, sa, w, sw, c, ldc, M, N, K, S(st)); });
+}
+int uh_gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw, uint16_t* c, int ldc,
+                     int M, int N, int K, void* st) {
+  return guard([&] { k::gemm_fp8_f32s(a, sa, w, sw, c, ldc, M, N, K, S(st)); });
+}
+int uh_gemm_a8w4(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, uint16_t* c, int ldc,
+                 int M, int N, int K, void* st) {
+  return guard([&] { k::gemm_a8w4(a, sa, w, sw, c, ldc, M, N, K, S(st)); });
+}
+int uh_gemm_a8w4_tiled(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, uint16_t* c, int ldc,
+                       int M, int N, int K, void* st) {
+  return guard([&] { k::gemm_a8w4_tiled(a, sa, w, sw, c, ldc, M, N, K, S(st)); });
+}
+int uh_quant_weight_fp8_f32s(const float* w, uint8_t* q, float* s, int N, int K, void* st) {
+  return guard([&] {
+    if (K % 128 || N <= 0) throw std::runtime_error("uh_quant_weight_fp8_f32s: K % 128");
+    quant_weight_kernel<<<dim3(unsigned(K / 128), uh::cdiv(size_t(N), 128)), 256, 0, S(st)>>>(w, q, s, N, K);
+    UH_CHECK_LAUNCH();
+  });
+}
+
+size_t uh_mx_moe_workspace_size(int T, int K, int E, int D, int I) { return carve(nullptr, T, K, E, D, I).bytes; }
+
+int uh_mx_moe_forward(const uint16_t* x, const float* logits, int T, int K, int E, int D, int I,
+                      const uint8_t* const* tab, float limit, void* ws, size_t ws_bytes, uint16_t* out, int32_t* sel,
+                      float* wt, void* stream) {
+  return guard([&] {
+    if (T <= 0) return;
+    const MoeWs w = carve(static_cast<char*>(ws), T, K, E, D, I);
+    if (ws_bytes < w.bytes) throw std::runtime_error("uh_mx_moe_forward: workspace too small");
+    if (D % 128 || I % 128) throw std::runtime_error("uh_mx_moe_forward: D % 128, I % 128");
+    const hipStream_t st = S(stream);
+    const int P = T * K;
+    int32_t* s_sel = sel ? sel : w.sel;
+    float* s_wt = wt ? wt : w.wt;
+    const auto t = [&](int m, int f) { return tab + size_t(2 * m + f) * E; };
+    k::route_softmax(logits, s_sel, s_wt, T, E, K, st);
+    const int* ntd = &reinterpret_cast<const k::MoePlan*>(w.plan)->n_local_tiles;
+    k::Exl3Tile* tiles = reinterpret_cast<k::Exl3Tile*>(w.tiles);
+    if (T <= k::kMoeSmallMaxTokens) {
+      k::MoeSmallArgs a{};
+      a.sel = s_sel;
+      a.wt = s_wt;
+      a.T = T;
+      a.K = K;
+      a.E = E;
+      a.P = P;
+      a.max_tiles = w.max_tiles;
+      a.tile_rows = w.tile_rows;
+      a.plan = reinterpret_cast<k::MoePlan*>(w.plan);
+      a.lt = tiles;
+      a.eidx = w.eidx;
+      a.ewt = w.ewt;
+      a.row_expert = w.row_expert;
+      a.pidx = w.pidx;
+      k::moe_dispatch_small(a, st);
+    } else {
+      UH_CHECK(hipMemsetAsync(w.count, 0, size_t(E) * 4, st));
+      k::moe_count(s_sel, T, K, w.count, E, st);
+      k::moe_plan(w.count, nullptr, E, P, reinterpret_cast<k::MoePlan*>(w.plan), tiles, nullptr, w.off, w.fill,
+                  w.max_tiles, st, w.tile_rows);
+      k::moe_scatter_e(s_sel, s_wt, T, K, E, w.off, w.eidx, w.ewt, w.row_expert, w.pidx, st);
+    }
+    k::mx_xform_in_fp8(x, D, w.row_expert, t(0, 1), w.xq, w.xs, P, D, st, w.eidx);
+    const k::MxGlu glu{w.ewt, w.row_expert, t(2, 1), nullptr, limit, nullptr, w.hq, w.hs};
+    if (T <= 64) {
+      k::mx_grouped_gemv_q(w.xq, w.xs, D, tiles, w.max_tiles, t(0, 0), t(0, 1), nullptr, I, I, st, ntd, t(1, 0), t(1, 1),
+                           nullptr, w.tile_rows, glu);
+      k::mx_grouped_gemv_q(w.hq, w.hs, I, tiles, w.max_tiles, t(2, 0), t(2, 1), w.pair_out, D, D, st, ntd, nullptr,
+                           nullptr, nullptr, w.tile_rows);
+    } else {
+      k::mx_grouped_gemm_q(w.xq, w.xs, D, tiles, w.max_tiles, t(0, 0), t(0, 1), nullptr, I, I, st, ntd, t(1, 0), t(1, 1),
+                           nullptr, w.tile_rows, glu);
+      k::mx_grouped_gemm_q(w.hq, w.hs, I, tiles, w.max_tiles, t(2, 0), t(2, 1), w.pair_out, D, D, st, ntd, nullptr,
+                           nullptr, nullptr, w.tile_rows);
+    }
+    k::moe_combine(w.pair_out, w.pidx, nullptr, out, T, K, D, st);
+  });
+}
+
+}  // extern "C"

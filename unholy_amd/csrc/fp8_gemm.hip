@@ -1,0 +1,302 @@
+// Activation quantization and the fp8 e4m3 block-scaled dense GEMM/GEMV on gfx950, plus the reference-order
+// a8w4 GEMM. Interfaces: include/unholy/kernels/ref.hpp, gemv.hpp, gemm_wmma.hpp.
+//
+// Dense fp8: C[M,N] = sum over 128-input blocks kb of raw_kb * scale(m, n, kb), raw_kb the exact fp8 dot over the
+// block, fp32, bf16 out (ref_gemm.hip:130-137 with e8m0 scales; gemm_wmma.hip:89-100's fold for fp32 scales).
+// On gfx950 raw_kb is four bf16 MFMAs (16x16x32) per 16 x 16 output tile on operands dequantized exactly in
+// registers (the block-scaled f8f6f4 MFMA's internal sums are not fp32-accurate; see common.hpp).
+#include <algorithm>
+
+#include "common.hpp"
+#include "numerics.hpp"
+#include "unholy/kernels/gemm_wmma.hpp"
+#include "unholy/kernels/gemv.hpp"
+#include "unholy/kernels/ref.hpp"
+#include "fp8_internal.hpp"
+
+namespace unholy::kernels {
+
+using namespace uh;
+
+namespace {
+
+// act_quant per block of B values (B in {32, 64, 128}): a group of B/2 lanes, two values per lane.
+// MODE 0: codes + e8m0 scale; 1: fake quant in place; 2: codes + fp32 scale (kernel.py scale_fmt=None).
+template <int B, int MODE>
+__global__ __launch_bounds__(256) void act_quant_kernel(const bf16* __restrict__ x, int ldx, uint8_t* __restrict__ q,
+                                                        void* __restrict__ s, int rows, int cols) {
+  constexpr int G = B / 2;
+  const int nb = cols / B;
+  const size_t gi = (blockIdx.x * size_t(blockDim.x) + threadIdx.x) / G;
+  const int l = threadIdx.x % G;
+  const bool valid = gi < size_t(rows) * nb;  // uniform per group of G lanes
+  const int r = valid ? int(gi / nb) : 0, b = valid ? int(gi % nb) : 0;
+  bf16* xr = const_cast<bf16*>(x) + size_t(r) * ldx + size_t(b) * B + 2 * l;
+  float v0 = 0.0f, v1 = 0.0f;
+  if (valid) {
+    v0 = bf16_to_f32(xr[0]);
+    v1 = bf16_to_f32(xr[1]);
+  }
+  const float am = group_max<G>(fmaxf(fabsf(v0), fabsf(v1)));
+  if (!valid) return;
+  uint8_t c0, c1;
+  if constexpr (MODE == 2) {
+    const float sc = fmaxf(am, 1e-4f) * (1.0f / 448.0f);
+    c0 = fp8_code(v0, sc);
+    c1 = fp8_code(v1, sc);
+    if (l == 0) static_cast<float*>(s)[size_t(r) * nb + b] = sc;
+  } else {
+    const Fp8Block blk = fp8_block_scale(am);
+    c0 = fp8_code(v0, blk.sc);
+    c1 = fp8_code(v1, blk.sc);
+    if constexpr (MODE == 1) {
+      xr[0] = f32_to_bf16(e4m3_to_f32(c0) * blk.sc);
+      xr[1] = f32_to_bf16(e4m3_to_f32(c1) * blk.sc);
+      return;
+    }
+    if (l == 0) static_cast<uint8_t*>(s)[size_t(r) * nb + b] = blk.se;
+  }
+  *reinterpret_cast<uint16_t*>(q + size_t(r) * cols + size_t(b) * B + 2 * l) = uint16_t(c0 | uint32_t(c1) << 8);
+}
+
+template <int MODE>
+void launch_act_quant(const bf16* x, int ldx, uint8_t* q, void* s, int rows, int cols, int block, hipStream_t st) {
+  if (rows <= 0) return;
+  if (block != 32 && block != 64 && block != 128) throw std::runtime_error("act_quant: block in {32, 64, 128}");
+  if (cols % block) throw std::runtime_error("act_quant: cols % block");
+  const size_t threads = size_t(rows) * (cols / block) * (block / 2);
+  const unsigned grid = cdiv(threads, 256);
+  if (block == 32) act_quant_kernel<32, MODE><<<grid, 256, 0, st>>>(x, ldx, q, s, rows, cols);
+  else if (block == 64) act_quant_kernel<64, MODE><<<grid, 256, 0, st>>>(x, ldx, q, s, rows, cols);
+  else act_quant_kernel<128, MODE><<<grid, 256, 0, st>>>(x, ldx, q, s, rows, cols);
+  UH_CHECK_LAUNCH();
+}
+
+// ---- reference-order a8w4 GEMM ----------------------------------------------------------------------------------
+// A thread per output: per 32-block the exact partial sum in k order, scaled by sa[m][k/128] * sw[n][k/32] and
+// added in block order -- the operation order of the reference's gemm_a8w4 (ref_gemm.hip:26-58, G = 32), so the
+// fp32 results are the reference's bit for bit. Not a fast path: a pinned twin of the MFMA kernels.
+template <bool TILED>
+__global__ __launch_bounds__(256) void gemm_a8w4_ref_kernel(const uint8_t* a, const uint8_t* sa, const uint8_t* w,
+                                                            const uint8_t* sw, bf16* c, int ldc, int M, int N, int K) {
+  const int n = blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
+  if (n >= N) return;
+  float acc = 0.0f;
+  for (int kb = 0; kb < K / 32; ++kb) {
+    float part = 0.0f;
+    for (int k = kb * 32; k < kb * 32 + 32; ++k) {
+      uint8_t byte;
+      if constexpr (TILED) byte = w[(size_t(k / 64) * (N / 16) + n / 16) * 512 + (n % 16) * 32 + (k % 64) / 2];
+      else byte = w[size_t(n) * (K / 2) + k / 2];
+      part = fmaf(e4m3_to_f32(a[size_t(m) * K + k]), e2m1_to_f32((k & 1) ? (byte >> 4) : (byte & 0xf)), part);
+    }
+    uint8_t sb;
+    if constexpr (TILED) sb = sw[(size_t(kb / 2) * (N / 16) + n / 16) * 32 + (n % 16) * 2 + kb % 2];
+    else sb = sw[size_t(n) * (K / 32) + kb];
+    acc += part * (e8m0_to_f32(sa[size_t(m) * (K / 128) + kb / 4]) * e8m0_to_f32(sb));
+  }
+  c[size_t(m) * ldc + n] = f32_to_bf16(acc);
+}
+
+// ---- fp8 dense, skinny (rows in groups of <= 16 staged in LDS) -------------------------------------------------------
+// A workgroup = 4 waves x DN_TN 16-column tiles. Per 128-input step lane l takes 32 code bytes of weight row
+// n0 + l % 16 at inputs 32 (l / 16) .. + 31 (four lanes cover one row's 128 contiguous bytes), dequantizes them and
+// the matching activation inputs exactly to bf16 and issues four bf16 MFMAs per column tile. e8m0 scales are
+// folded into the conversions (exact) and the MFMA accumulates across blocks; with fp32 scales each 128-block's
+// MFMA chain starts from zero and is folded as acc += raw * (sa * sw), the reference's order of scaling.
+constexpr int DN_NT = 256, DN_WAVES = 4, DN_TN = 2, DN_PAD = 16, DN_MAXROWS = 16;
+
+template <bool F32S>
+__global__ __launch_bounds__(DN_NT) void fp8_skinny_kernel(Fp8GemmArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int K = a.K, N = a.N, KS = K / 128, ldA = K + DN_PAD, ntn = (N + 15) / 16;
+  uint8_t* sA = smem;
+  float* sSf = reinterpret_cast<float*>(smem + size_t(a.rows_cap) * ldA);
+  uint8_t* sSb = smem + size_t(a.rows_cap) * ldA;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nl = lane & 15, g = lane >> 4;
+  int nt[DN_TN];
+#pragma unroll
+  for (int j = 0; j < DN_TN; ++j) nt[j] = blockIdx.x * (DN_WAVES * DN_TN) + wave * DN_TN + j;
+  const int rg = blockIdx.y * a.rows_cap, M = min(a.rows_cap, a.M - rg);
+  for (int i = tid; i < M * (K / 16); i += DN_NT) {
+    const int m = i / (K / 16), c = (i % (K / 16)) * 16;
+    *reinterpret_cast<uint4*>(sA + m * ldA + c) = *reinterpret_cast<const uint4*>(a.a + size_t(rg + m) * K + c);
+  }
+  for (int i = tid; i < M * KS; i += DN_NT) {
+    if constexpr (F32S) sSf[i] = a.sa32[size_t(rg) * KS + i];
+    else sSb[i] = a.sa8[size_t(rg) * KS + i];
+  }
+  __syncthreads();
+  const bool arow = nl < M;
+  const uint8_t* ap = sA + nl * ldA + g * 32;
+  v4f acc[DN_TN];
+#pragma unroll
+  for (int j = 0; j < DN_TN; ++j) acc[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  // Weight row of this lane in each column tile (rows past N read row N - 1 and are not stored).
+  const uint8_t* wrow[DN_TN];
+#pragma unroll
+  for (int j = 0; j < DN_TN; ++j) wrow[j] = a.w + size_t(min(nt[j] * 16 + nl, N - 1)) * K + g * 32;
+#pragma unroll 2
+  for (int s = 0; s < KS; ++s) {
+    v4i b[DN_TN][2];
+#pragma unroll
+    for (int j = 0; j < DN_TN; ++j)
+      if (nt[j] < ntn) {
+        b[j][0] = *reinterpret_cast<gptr<v4i>>(as_global(wrow[j] + s * 128));
+        b[j][1] = *reinterpret_cast<gptr<v4i>>(as_global(wrow[j] + s * 128 + 16));
+      }
+    // Activation inputs 32g .. 32g + 31 of row nl (scale folded in for e8m0, 1.0 for fp32 scales).
+    bf16x8 af[4];
+    if (arow) {
+      const v4i lo = *reinterpret_cast<const v4i*>(ap + s * 128), hi = *reinterpret_cast<const v4i*>(ap + s * 128 + 16);
+      const float sc = F32S ? 1.0f : e8m0_to_f32(sSb[nl * KS + s]);
+      af[0] = fp8x8_to_bf16(lo[0], lo[1], sc);
+      af[1] = fp8x8_to_bf16(lo[2], lo[3], sc);
+      af[2] = fp8x8_to_bf16(hi[0], hi[1], sc);
+      af[3] = fp8x8_to_bf16(hi[2], hi[3], sc);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) af[t] = bf16x8{};
+    }
+    if constexpr (F32S) {
+      float sa_i[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sa_i[i] = (4 * g + i) < M ? sSf[(4 * g + i) * KS + s] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < DN_TN; ++j)
+        if (nt[j] < ntn) {
+          v4f raw = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            raw = mfma_bf16(af[t], fp8x8_to_bf16(uint32_t(b[j][t / 2][2 * (t % 2)]), uint32_t(b[j][t / 2][2 * (t % 2) + 1]), 1.0f), raw);
+          const float swv = a.sw32[size_t(min(nt[j] * 16 + nl, N - 1) / 128) * KS + s];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[j][i] += raw[i] * (sa_i[i] * swv);
+        }
+    } else {
+#pragma unroll
+      for (int j = 0; j < DN_TN; ++j)
+        if (nt[j] < ntn) {
+          const float sc = e8m0_to_f32(a.sw8[size_t(min(nt[j] * 16 + nl, N - 1) / 128) * KS + s]);
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            acc[j] = mfma_bf16(af[t], fp8x8_to_bf16(uint32_t(b[j][t / 2][2 * (t % 2)]), uint32_t(b[j][t / 2][2 * (t % 2) + 1]), sc), acc[j]);
+        }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < DN_TN; ++j) {
+    const int n = nt[j] * 16 + nl;
+    if (nt[j] >= ntn || n >= N) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * g + i;
+      if (r < M) a.c[size_t(rg + r) * a.ldc + n] = f32_to_bf16(acc[j][i]);
+    }
+  }
+}
+
+}  // namespace
+
+void launch_fp8_skinny(const Fp8GemmArgs& a0, hipStream_t st) {
+  Fp8GemmArgs a = a0;
+  if (a.M <= 0) return;
+  if (a.K % 128 || a.K <= 0 || a.N <= 0) throw std::runtime_error("fp8 gemm: K % 128");
+  if (!a.a || !a.w || !a.c) throw std::runtime_error("fp8 gemm: null operand");
+  const bool f32s = a.sa32 != nullptr;
+  if (f32s ? !a.sw32 : (!a.sa8 || !a.sw8)) throw std::runtime_error("fp8 gemm: scales");
+  a.rows_cap = std::min(a.M, DN_MAXROWS);
+  const size_t lds = size_t(a.rows_cap) * (a.K + DN_PAD) + size_t(a.rows_cap) * (a.K / 128) * (f32s ? 4 : 1);
+  const dim3 grid(cdiv(cdiv(size_t(a.N), 16), DN_WAVES * DN_TN), cdiv(size_t(a.M), size_t(a.rows_cap)));
+  if (f32s) {
+    if (lds > 65536)
+      UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&fp8_skinny_kernel<true>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+    fp8_skinny_kernel<true><<<grid, DN_NT, lds, st>>>(a);
+  } else {
+    if (lds > 65536)
+      UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&fp8_skinny_kernel<false>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+    fp8_skinny_kernel<false><<<grid, DN_NT, lds, st>>>(a);
+  }
+  UH_CHECK_LAUNCH();
+}
+
+// ---- entry points ---------------------------------------------------------------------------------------------------
+void act_quant_fp8(const bf16* x, int ldx, uint8_t* q, uint8_t* s, int rows, int cols, int block, hipStream_t st) {
+  launch_act_quant<0>(x, ldx, q, s, rows, cols, block, st);
+}
+void fake_quant_fp8(bf16* x, int ldx, int rows, int cols, int block, hipStream_t st) {
+  launch_act_quant<1>(x, ldx, nullptr, nullptr, rows, cols, block, st);
+}
+void act_quant_fp8_f32s(const bf16* x, int ldx, uint8_t* q, float* s, int rows, int cols, int block, hipStream_t st) {
+  launch_act_quant<2>(x, ldx, q, s, rows, cols, block, st);
+}
+
+void gemm_a8w4(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, bf16* c, int ldc, int M,
+               int N, int K, hipStream_t st) {
+  if (M <= 0) return;
+  if (K % 128) throw std::runtime_error("gemm_a8w4: K % 128");
+  gemm_a8w4_ref_kernel<false><<<dim3(cdiv(size_t(N), 256), unsigned(M)), 256, 0, st>>>(a, sa, w, sw, c, ldc, M, N, K);
+  UH_CHECK_LAUNCH();
+}
+void gemm_a8w4_tiled(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, bf16* c, int ldc,
+                     int M, int N, int K, hipStream_t st) {
+  if (M <= 0) return;
+  if (K % 128 || N % 16) throw std::runtime_error("gemm_a8w4_tiled: K % 128, N % 16");
+  gemm_a8w4_ref_kernel<true><<<dim3(cdiv(size_t(N), 256), unsigned(M)), 256, 0, st>>>(a, sa, w, sw, c, ldc, M, N, K);
+  UH_CHECK_LAUNCH();
+}
+
+void gemm_w8a8(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, bf16* c, int ldc, int M,
+               int N, int K, hipStream_t st) {
+  Fp8GemmArgs g{};
+  g.a = a;
+  g.sa8 = sa;
+  g.w = w;
+  g.sw8 = sw;
+  g.c = c;
+  g.ldc = ldc;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  launch_fp8_gemm(g, st);
+}
+void gemm_w8a8_wmma(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, bf16* c, int ldc,
+                    int M, int N, int K, hipStream_t st) {
+  gemm_w8a8(a, sa, w, sw, c, ldc, M, N, K, st);
+}
+void gemv_w8a8(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, bf16* c, int ldc, int M,
+               int N, int K, hipStream_t st) {
+  if (M > kGemvRowsCap) throw std::runtime_error("gemv_w8a8: M > 32");
+  Fp8GemmArgs g{};
+  g.a = a;
+  g.sa8 = sa;
+  g.w = w;
+  g.sw8 = sw;
+  g.c = c;
+  g.ldc = ldc;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  launch_fp8_skinny(g, st);
+}
+void gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw, bf16* c, int ldc, int M,
+                   int N, int K, hipStream_t st) {
+  Fp8GemmArgs g{};
+  g.a = a;
+  g.sa32 = sa;
+  g.w = w;
+  g.sw32 = sw;
+  g.c = c;
+  g.ldc = ldc;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  launch_fp8_gemm(g, st);
+}
+
+int gemv_max_rows() { return 8; }
+void gemm_force_skinny(int) {}
+
+}  // namespace unholy::kernels

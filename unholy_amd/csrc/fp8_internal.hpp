@@ -1,0 +1,28 @@
+// Launch descriptor of the dense fp8 GEMM kernels (not part of the public interface).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace unholy::kernels {
+
+// C[M, N] (bf16, ldc) = A[M, K] (e4m3) x W[N, K]^T (e4m3), per-128 scales: e8m0 (sa8 [M, K/128], sw8
+// [ceil(N/128), K/128]) or fp32 (sa32, sw32, same shapes).
+struct Fp8GemmArgs {
+  const uint8_t* a;
+  const uint8_t* sa8;
+  const float* sa32;
+  const uint8_t* w;
+  const uint8_t* sw8;
+  const float* sw32;
+  uint16_t* c;
+  int ldc, M, N, K;
+  int rows_cap;
+};
+
+void launch_fp8_skinny(const Fp8GemmArgs& a, hipStream_t st);
+// Picks the skinny kernel (M <= 64) or the LDS-tiled MFMA GEMM.
+void launch_fp8_gemm(const Fp8GemmArgs& a, hipStream_t st);
+
+}  // namespace unholy::kernels

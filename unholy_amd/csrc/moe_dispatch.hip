@@ -1,0 +1,509 @@
+// Routing, dispatch bookkeeping, SwiGLU, gather/scatter and combine for the routed-expert path on gfx950.
+// Interfaces: include/unholy/kernels/moe_dispatch.hpp and ref.hpp.
+//
+// The dispatch permutation is deterministic (rows of an expert = its tokens in ascending order, each token's
+// picks sorted by expert id: src/model/forward_ref.hip:1302-1328): a block per expert walks the tokens in order
+// and ranks its own picks with a block scan, instead of the reference device path's atomic fill counters
+// (src/kernels/moe_dispatch.hip:82-109).
+#include <algorithm>
+#include <cmath>
+
+#include "common.hpp"
+#include "numerics.hpp"
+#include "unholy/kernels/moe_dispatch.hpp"
+#include "unholy/kernels/ref.hpp"
+
+namespace unholy::kernels {
+
+using namespace uh;
+
+namespace {
+
+constexpr int kMaxK = 8;
+
+// Exclusive scan of v over a block of NT threads (NT / 64 waves); returns the prefix, total in *tot.
+template <int NT>
+__device__ __forceinline__ int block_exclusive_scan(int v, int* tot, int* lds /* >= NT/64 + 1 ints */) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int inc = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += y;
+  }
+  if (lane == 63) lds[wave] = inc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int w = 0; w < NT / 64; ++w) {
+      const int c = lds[w];
+      lds[w] = run;
+      run += c;
+    }
+    lds[NT / 64] = run;
+  }
+  __syncthreads();
+  const int res = lds[wave] + inc - v;
+  *tot = lds[NT / 64];
+  __syncthreads();
+  return res;
+}
+
+__global__ void moe_count_kernel(const int32_t* __restrict__ sel, int n, int32_t* count, uint32_t* hist) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  atomicAdd(&count[sel[i]], 1);
+  if (hist) atomicAdd(&hist[sel[i]], 1u);
+}
+
+// Offsets and tiles for E <= 1024 experts: resident experts first, then the others, each in ascending id
+// (ref moe_dispatch.hip:39-79 semantics; scans here are wave shuffles plus one LDS pass).
+constexpr int PLAN_NT = 1024;
+__global__ __launch_bounds__(PLAN_NT) void moe_plan_kernel(int32_t* count, const uint8_t* resident, int E, int P,
+                                                           MoePlan* plan, Exl3Tile* local_tiles,
+                                                           Exl3Tile* remote_tiles, int32_t* off, int32_t* fill,
+                                                           int max_tiles, int tile_rows) {
+  __shared__ int lds[4][PLAN_NT / 64 + 1];
+  const int e = threadIdx.x;
+  const bool in = e < E, loc = in && (!resident || resident[e] != 0);
+  const int c = in ? count[e] : 0, nt = (c + tile_rows - 1) / tile_rows;
+  int tot[4];
+  const int lrow = block_exclusive_scan<PLAN_NT>(loc ? c : 0, &tot[0], lds[0]);
+  const int rrow = block_exclusive_scan<PLAN_NT>(in && !loc ? c : 0, &tot[1], lds[1]);
+  const int ltile = block_exclusive_scan<PLAN_NT>(loc ? nt : 0, &tot[2], lds[2]);
+  const int rtile = block_exclusive_scan<PLAN_NT>(in && !loc ? nt : 0, &tot[3], lds[3]);
+  const int remote0 = tot[0];
+  if (in) {
+    const int row = loc ? lrow : remote0 + rrow, tile = loc ? ltile : rtile;
+    Exl3Tile* dst = loc ? local_tiles : remote_tiles;
+    off[e] = row;
+    if (dst)
+      for (int i = 0; i < nt && tile + i < max_tiles; ++i)
+        dst[tile + i] = Exl3Tile{e, row + i * tile_rows, min(tile_rows, c - i * tile_rows)};
+    if (fill) fill[e] = 0;
+    count[e] = 0;
+  }
+  if (e == 0) {
+    plan->P = P;
+    plan->remote0 = remote0;
+    plan->n_local_tiles = min(tot[2], max_tiles);
+    plan->n_remote_tiles = min(tot[3], max_tiles);
+    plan->n_remote_tokens = 0;
+  }
+}
+
+// Block e: the tokens that picked e, in token order, get rows off[e], off[e] + 1, ...; each gets pidx at its
+// position among its own picks sorted by expert id (the number of its picks below e; equal picks stay in
+// selection order).
+constexpr int SC_NT = 256;
+__global__ __launch_bounds__(SC_NT) void moe_scatter_kernel(const int32_t* __restrict__ sel, const float* __restrict__ wt,
+                                                            int T, int K, const int32_t* __restrict__ off,
+                                                            int32_t* eidx, float* ewt, int32_t* row_expert,
+                                                            int32_t* pidx) {
+  __shared__ int lds[SC_NT / 64 + 1];
+  const int e = blockIdx.x;
+  int run = 0, base_row = -1;
+  for (int t0 = 0; t0 < T; t0 += SC_NT) {
+    const int t = t0 + threadIdx.x;
+    int c = 0, below = 0;
+    if (t < T)
+      for (int j = 0; j < K; ++j) {
+        const int v = sel[size_t(t) * K + j];
+        c += v == e;
+        below += v < e;
+      }
+    int tot;
+    const int pre = block_exclusive_scan<SC_NT>(c, &tot, lds);
+    if (c) {
+      if (base_row < 0) base_row = off[e];
+      int d = 0;
+      for (int j = 0; j < K; ++j)
+        if (sel[size_t(t) * K + j] == e) {
+          const int p = base_row + run + pre + d;
+          eidx[p] = t;
+          ewt[p] = wt ? wt[size_t(t) * K + j] : 1.0f;
+          row_expert[p] = e;
+          pidx[size_t(t) * K + below + d] = p;
+          ++d;
+        }
+    }
+    run += tot;
+  }
+}
+
+// ---- routers: a wave per token ---------------------------------------------------------------------------------------
+// Top-K of key[] (E <= 64 * NV) with ties to the lower index, in selection order, into chosen[] (every lane).
+template <int NV>
+__device__ __forceinline__ void wave_topk(float key[NV], int E, int K, int* chosen) {
+  const int lane = threadIdx.x & 63;
+  for (int k = 0; k < K; ++k) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E && (key[i] > bv || bi == 0x7fffffff)) bv = key[i], bi = e;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (ov > bv || (ov == bv && oi < bi)) bv = ov, bi = oi;
+    }
+    chosen[k] = bi;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (lane + 64 * i == bi) key[i] = -INFINITY;
+  }
+}
+
+__device__ __forceinline__ float ds_score(float x) { return sqrtf(x > 20.0f ? x : log1pf(expf(x))); }
+__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// mode 0: DSV4 (sqrt-softplus + bias, hash tid2eid, bias_vl for image ids), 1: GLM sigmoid, 2: softmax top-K.
+template <int MODE>
+__global__ __launch_bounds__(256) void route_wave_kernel(const float* __restrict__ logits, const float* bias0,
+                                                         const int32_t* tid2eid0, const int32_t* ids, int32_t* sel,
+                                                         float* weights, int T, int E, int K, float route_scale,
+                                                         const float* bias_vl, int vocab) {
+  constexpr int NV = 16;  // E <= 1024
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (t >= T) return;
+  const float* lr = logits + size_t(t) * E;
+  const bool image = MODE == 0 && bias_vl && ids[t] >= vocab;
+  const float* bias = image ? bias_vl : bias0;
+  const int32_t* tid2eid = MODE == 0 && !image ? tid2eid0 : nullptr;
+  int chosen[kMaxK];
+  if (tid2eid) {
+    for (int k = 0; k < K; ++k) chosen[k] = tid2eid[size_t(ids[t]) * K + k];
+  } else {
+    float key[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = lane + 64 * i;
+      float v = -INFINITY;
+      if (e < E) {
+        if constexpr (MODE == 0) v = ds_score(lr[e]) + bias[e];
+        else if constexpr (MODE == 1) v = sigmoid(lr[e]) + bias[e];
+        else v = lr[e];
+      }
+      key[i] = v;
+    }
+    wave_topk<NV>(key, E, K, chosen);
+  }
+  if (lane != 0) return;
+  if (MODE == 1)
+    for (int x = 1; x < K; ++x)
+      for (int y = x; y > 0 && chosen[y - 1] > chosen[y]; --y) {
+        const int c = chosen[y];
+        chosen[y] = chosen[y - 1];
+        chosen[y - 1] = c;
+      }
+  float w[kMaxK], sum = 0.0f;
+  for (int k = 0; k < K; ++k) {
+    const float l = lr[chosen[k]];
+    w[k] = MODE == 0 ? ds_score(l) : MODE == 1 ? sigmoid(l) : expf(l - lr[chosen[0]]);
+    sum += w[k];
+  }
+  for (int k = 0; k < K; ++k) {
+    sel[size_t(t) * K + k] = chosen[k];
+    weights[size_t(t) * K + k] = MODE == 0 ? (w[k] / sum) * route_scale
+                                 : MODE == 1 ? w[k] / (sum + 1e-20f) * route_scale
+                                             : w[k] / sum;
+  }
+}
+
+// The reference's one-thread-per-token DSV4 router (ref_moe.hip:14-60): the same picks and weights as the wave
+// form; kept as the `route` entry point.
+__global__ void route_thread_kernel(const float* logits, const float* bias0, const int32_t* tid2eid0,
+                                    const int32_t* ids, int32_t* sel, float* weights, int T, int E, int K,
+                                    float route_scale, const float* bias_vl, int vocab) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= T) return;
+  const bool image = bias_vl && ids[t] >= vocab;
+  const float* bias = image ? bias_vl : bias0;
+  const int32_t* tid2eid = image ? nullptr : tid2eid0;
+  const float* lg = logits + size_t(t) * E;
+  int chosen[kMaxK];
+  if (tid2eid) {
+    for (int k = 0; k < K; ++k) chosen[k] = tid2eid[size_t(ids[t]) * K + k];
+  } else {
+    for (int k = 0; k < K; ++k) {
+      int best = -1;
+      float bv = -INFINITY;
+      for (int e = 0; e < E; ++e) {
+        bool used = false;
+        for (int j = 0; j < k; ++j) used |= chosen[j] == e;
+        if (used) continue;
+        const float v = ds_score(lg[e]) + bias[e];
+        if (best < 0 || v > bv) best = e, bv = v;
+      }
+      chosen[k] = best;
+    }
+  }
+  float w[kMaxK], sum = 0.0f;
+  for (int k = 0; k < K; ++k) {
+    w[k] = ds_score(lg[chosen[k]]);
+    sum += w[k];
+  }
+  for (int k = 0; k < K; ++k) {
+    sel[size_t(t) * K + k] = chosen[k];
+    weights[size_t(t) * K + k] = (w[k] / sum) * route_scale;
+  }
+}
+
+// ---- single-block dispatch for small steps -------------------------------------------------------------------------
+constexpr int SMALL_NT = 1024;
+__global__ __launch_bounds__(SMALL_NT) void moe_dispatch_small_kernel(MoeSmallArgs a) {
+  __shared__ int ssel[kMoeSmallMaxTokens * kMaxK];
+  __shared__ float swt[kMoeSmallMaxTokens * kMaxK];
+  __shared__ int lds[2][SMALL_NT / 64 + 1];
+  const int T = a.T, K = a.K, E = a.E, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // Routing in the launch: a wave per token.
+  if (a.route_logits || a.ds_logits) {
+    for (int t = wave; t < T; t += SMALL_NT / 64) {
+      constexpr int NV = 16;
+      const bool glm = a.route_logits != nullptr;
+      const float* lr = (glm ? a.route_logits : a.ds_logits) + size_t(t) * E;
+      const bool image = !glm && a.ds_bias_vl && a.ids[t] >= a.vocab;
+      const float* bias = glm ? a.route_bias : image ? a.ds_bias_vl : a.ds_bias;
+      const int32_t* tid2eid = !glm && !image ? a.ds_tid2eid : nullptr;
+      int chosen[kMaxK];
+      if (tid2eid) {
+        for (int k = 0; k < K; ++k) chosen[k] = tid2eid[size_t(a.ids[t]) * K + k];
+      } else {
+        float key[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          const int e = lane + 64 * i;
+          key[i] = e < E ? (glm ? sigmoid(lr[e]) : ds_score(lr[e])) + bias[e] : -INFINITY;
+        }
+        wave_topk<NV>(key, E, K, chosen);
+      }
+      if (lane == 0) {
+        if (glm)
+          for (int x = 1; x < K; ++x)
+            for (int y = x; y > 0 && chosen[y - 1] > chosen[y]; --y) {
+              const int c = chosen[y];
+              chosen[y] = chosen[y - 1];
+              chosen[y - 1] = c;
+            }
+        float w[kMaxK], sum = 0.0f;
+        for (int k = 0; k < K; ++k) {
+          w[k] = glm ? sigmoid(lr[chosen[k]]) : ds_score(lr[chosen[k]]);
+          sum += w[k];
+        }
+        for (int k = 0; k < K; ++k) {
+          const_cast<int32_t*>(a.sel)[size_t(t) * K + k] = chosen[k];
+          const_cast<float*>(a.wt)[size_t(t) * K + k] =
+              glm ? w[k] / (sum + 1e-20f) * a.route_scale : (w[k] / sum) * a.route_scale;
+        }
+      }
+    }
+    __threadfence_block();
+    __syncthreads();
+  }
+  for (int i = tid; i < T * K; i += SMALL_NT) {
+    ssel[i] = a.sel[i];
+    swt[i] = a.wt[i];
+    if (a.hist) atomicAdd(&a.hist[a.sel[i]], 1u);
+  }
+  __syncthreads();
+  // Thread e: its count and, in token order, its rows.
+  const int e = tid;
+  int c = 0;
+  if (e < E)
+    for (int i = 0; i < T * K; ++i) c += ssel[i] == e;
+  const int nt = (c + a.tile_rows - 1) / a.tile_rows;
+  int tot_rows, tot_tiles;
+  const int row = block_exclusive_scan<SMALL_NT>(c, &tot_rows, lds[0]);
+  const int tile = block_exclusive_scan<SMALL_NT>(nt, &tot_tiles, lds[1]);
+  if (e < E && c > 0) {
+    int p = row;
+    for (int t = 0; t < T; ++t) {
+      int below = 0;
+      for (int j = 0; j < K; ++j) below += ssel[t * K + j] < e;
+      for (int j = 0; j < K; ++j)
+        if (ssel[t * K + j] == e) {
+          a.eidx[p] = t;
+          a.ewt[p] = swt[t * K + j];
+          a.row_expert[p] = e;
+          a.pidx[size_t(t) * K + below++] = p;
+          ++p;
+        }
+    }
+    for (int i = 0; i < nt && tile + i < a.max_tiles; ++i)
+      a.lt[tile + i] = Exl3Tile{e, row + i * a.tile_rows, min(a.tile_rows, c - i * a.tile_rows)};
+  }
+  if (tid == 0) {
+    a.plan->P = a.P;
+    a.plan->remote0 = tot_rows;
+    a.plan->n_local_tiles = min(tot_tiles, a.max_tiles);
+    a.plan->n_remote_tiles = 0;
+    a.plan->n_remote_tokens = 0;
+  }
+}
+
+// ---- elementwise -----------------------------------------------------------------------------------------------------
+__global__ void swiglu_kernel(const bf16* gate, const bf16* up, const float* w, bf16* h, int rows, int dim,
+                              float limit) {
+  const size_t gid = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (gid >= size_t(rows) * dim) return;
+  h[gid] = f32_to_bf16(swiglu_value(bf16_to_f32(gate[gid]), bf16_to_f32(up[gid]), w ? w[gid / dim] : 0.0f,
+                                    w != nullptr, limit));
+}
+
+__global__ void gather_rows_kernel(const bf16* src, const int32_t* rows_idx, bf16* dst, int n, int dim) {
+  const size_t gid = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (gid >= size_t(n) * dim) return;
+  dst[gid] = src[size_t(rows_idx[gid / dim]) * dim + gid % dim];
+}
+
+// One thread per column, rows in order (the same fp32 sums as the reference's row-ordered scatter).
+__global__ void scatter_add_kernel(const bf16* src, const int32_t* rows_idx, float* y, int n, int dim) {
+  const int d = blockIdx.x * blockDim.x + threadIdx.x;
+  if (d >= dim) return;
+  for (int r = 0; r < n; ++r) y[size_t(rows_idx[r]) * dim + d] += bf16_to_f32(src[size_t(r) * dim + d]);
+}
+
+// out[t][d] = bf16(sum_j pair_out[pidx[t][j]][d] (j ascending) + shared[t][d]): a thread per 8 columns.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const bf16* __restrict__ pair_out,
+                                                          const int32_t* __restrict__ pidx,
+                                                          const bf16* __restrict__ shared, bf16* __restrict__ out,
+                                                          int K, int dim) {
+  const int t = blockIdx.y, d = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (d >= dim) return;
+  float acc[8] = {};
+  for (int j = 0; j < K; ++j) {
+    const uint4 v = *reinterpret_cast<const uint4*>(pair_out + size_t(pidx[size_t(t) * K + j]) * dim + d);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      acc[2 * q] += __uint_as_float(w[q] << 16);
+      acc[2 * q + 1] += __uint_as_float(w[q] & 0xffff0000u);
+    }
+  }
+  if (shared) {
+    const uint4 v = *reinterpret_cast<const uint4*>(shared + size_t(t) * dim + d);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      acc[2 * q] += __uint_as_float(w[q] << 16);
+      acc[2 * q + 1] += __uint_as_float(w[q] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc[q] += 0.0f;
+  }
+  uint32_t o[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) o[q] = uint32_t(f32_to_bf16(acc[2 * q])) | uint32_t(f32_to_bf16(acc[2 * q + 1])) << 16;
+  *reinterpret_cast<uint4*>(out + size_t(t) * dim + d) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+}  // namespace
+
+// ---- entry points ---------------------------------------------------------------------------------------------------
+void moe_count(const int32_t* sel, int T, int K, int32_t* count, int, hipStream_t st, uint32_t* hist) {
+  const int n = T * K;
+  if (n <= 0) return;
+  moe_count_kernel<<<cdiv(size_t(n), 256), 256, 0, st>>>(sel, n, count, hist);
+  UH_CHECK_LAUNCH();
+}
+
+void moe_plan(int32_t* count, const uint8_t* resident, int E, int P, MoePlan* plan, Exl3Tile* local_tiles,
+              Exl3Tile* remote_tiles, int32_t* off, int32_t* fill, int max_tiles, hipStream_t st, int tile_rows) {
+  if (E <= 0 || E > PLAN_NT) throw std::runtime_error("moe_plan: E must be in [1, 1024]");
+  if (tile_rows <= 0 || tile_rows > kExl3TileRows) throw std::runtime_error("moe_plan: tile_rows in [1, 128]");
+  moe_plan_kernel<<<1, PLAN_NT, 0, st>>>(count, resident, E, P, plan, local_tiles, remote_tiles, off, fill, max_tiles,
+                                         tile_rows);
+  UH_CHECK_LAUNCH();
+}
+
+void moe_scatter_e(const int32_t* sel, const float* wt, int T, int K, int E, const int32_t* off, int32_t* eidx,
+                   float* ewt, int32_t* row_expert, int32_t* pidx, hipStream_t st) {
+  if (T <= 0) return;
+  if (K <= 0 || K > kMaxK || E <= 0) throw std::runtime_error("moe_scatter: K in [1, 8], E > 0");
+  moe_scatter_kernel<<<unsigned(E), SC_NT, 0, st>>>(sel, wt, T, K, off, eidx, ewt, row_expert, pidx);
+  UH_CHECK_LAUNCH();
+}
+
+// Without E: one block per possible expert id (< 1024, moe_plan's limit); a block whose id no token picked never
+// reads off[] and writes nothing.
+void moe_scatter(const int32_t* sel, const float* wt, int T, int K, const int32_t* off, int32_t*, int32_t* eidx,
+                 float* ewt, int32_t* row_expert, int32_t* pidx, hipStream_t st) {
+  moe_scatter_e(sel, wt, T, K, PLAN_NT, off, eidx, ewt, row_expert, pidx, st);
+}
+
+void moe_dispatch_small(const MoeSmallArgs& a, hipStream_t st) {
+  if (a.T <= 0) return;
+  if (a.T > kMoeSmallMaxTokens || a.K <= 0 || a.K > kMaxK) throw std::runtime_error("moe_dispatch_small: T <= 32, K <= 8");
+  if (a.E <= 0 || a.E > SMALL_NT) throw std::runtime_error("moe_dispatch_small: E in [1, 1024]");
+  if (a.tile_rows <= 0) throw std::runtime_error("moe_dispatch_small: tile_rows");
+  if (a.remote || a.qin || a.x_dst || a.q_dst || a.req_flag || a.plan_dst)
+    throw std::runtime_error("moe_dispatch_small: remote experts are not supported on one GPU");
+  if (a.resident) throw std::runtime_error("moe_dispatch_small: resident mask not supported (all experts local)");
+  if (!a.sel || !a.wt || !a.plan || !a.lt || !a.eidx || !a.ewt || !a.row_expert || !a.pidx)
+    throw std::runtime_error("moe_dispatch_small: null output");
+  moe_dispatch_small_kernel<<<1, SMALL_NT, 0, st>>>(a);
+  UH_CHECK_LAUNCH();
+}
+
+void route(const float* logits, const float* bias, const int32_t* tid2eid, const int32_t* ids, int32_t* sel,
+           float* weights, int T, int E, int K, float route_scale, hipStream_t st, const float* bias_vl, int vocab) {
+  if (T <= 0) return;
+  if (K <= 0 || K > kMaxK || K > E) throw std::runtime_error("route: K in [1, 8], K <= E");
+  route_thread_kernel<<<cdiv(size_t(T), 64), 64, 0, st>>>(logits, bias, tid2eid, ids, sel, weights, T, E, K,
+                                                           route_scale, bias_vl, vocab);
+  UH_CHECK_LAUNCH();
+}
+void route_fast(const float* logits, const float* bias, const int32_t* tid2eid, const int32_t* ids, int32_t* sel,
+                float* weights, int T, int E, int K, float route_scale, hipStream_t st, const float* bias_vl,
+                int vocab) {
+  if (T <= 0) return;
+  if (E > 1024 || K <= 0 || K > kMaxK || K > E) throw std::runtime_error("route_fast: E <= 1024, K in [1, 8]");
+  route_wave_kernel<0><<<cdiv(size_t(T), 4), 256, 0, st>>>(logits, bias, tid2eid, ids, sel, weights, T, E, K,
+                                                            route_scale, bias_vl, vocab);
+  UH_CHECK_LAUNCH();
+}
+void route_glm(const float* logits, const float* bias, int32_t* sel, float* weights, int T, int E, int K,
+               float route_scale, hipStream_t st) {
+  if (T <= 0) return;
+  if (E > 1024 || K <= 0 || K > kMaxK || K > E) throw std::runtime_error("route_glm: E <= 1024, K in [1, 8]");
+  route_wave_kernel<1><<<cdiv(size_t(T), 4), 256, 0, st>>>(logits, bias, nullptr, nullptr, sel, weights, T, E, K,
+                                                            route_scale, nullptr, 0);
+  UH_CHECK_LAUNCH();
+}
+void route_softmax(const float* logits, int32_t* sel, float* weights, int T, int E, int K, hipStream_t st) {
+  if (T <= 0) return;
+  if (E > 1024 || K <= 0 || K > kMaxK || K > E) throw std::runtime_error("route_softmax: E <= 1024, K in [1, 8]");
+  route_wave_kernel<2><<<cdiv(size_t(T), 4), 256, 0, st>>>(logits, nullptr, nullptr, nullptr, sel, weights, T, E, K,
+                                                            1.0f, nullptr, 0);
+  UH_CHECK_LAUNCH();
+}
+
+void swiglu(const bf16* gate, const bf16* up, const float* w, bf16* h, int rows, int dim, float limit,
+            hipStream_t st) {
+  if (rows <= 0) return;
+  swiglu_kernel<<<cdiv(size_t(rows) * dim, 256), 256, 0, st>>>(gate, up, w, h, rows, dim, limit);
+  UH_CHECK_LAUNCH();
+}
+void gather_rows(const bf16* src, const int32_t* rows_idx, bf16* dst, int n, int dim, hipStream_t st) {
+  if (n <= 0) return;
+  gather_rows_kernel<<<cdiv(size_t(n) * dim, 256), 256, 0, st>>>(src, rows_idx, dst, n, dim);
+  UH_CHECK_LAUNCH();
+}
+void scatter_add(const bf16* src, const int32_t* rows_idx, float* y, int n, int dim, hipStream_t st) {
+  if (n <= 0) return;
+  scatter_add_kernel<<<cdiv(size_t(dim), 256), 256, 0, st>>>(src, rows_idx, y, n, dim);
+  UH_CHECK_LAUNCH();
+}
+void moe_combine(const bf16* pair_out, const int32_t* pidx, const bf16* shared, bf16* out, int T, int K, int dim,
+                 hipStream_t st) {
+  if (T <= 0) return;
+  if (dim % 8) throw std::runtime_error("moe_combine: dim % 8");
+  moe_combine_kernel<<<dim3(cdiv(size_t(dim), 2048), unsigned(T)), 256, 0, st>>>(pair_out, pidx, shared, out, K, dim);
+  UH_CHECK_LAUNCH();
+}
+
+}  // namespace unholy::kernels

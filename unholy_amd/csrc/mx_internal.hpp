@@ -1,0 +1,41 @@
+// Launch descriptors shared between the MXFP4 kernel files (not part of the public interface).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "unholy/kernels/exl3_moe.hpp"
+
+namespace unholy::kernels {
+
+// One grouped GEMV / GEMM launch: activations as e4m3 codes + e8m0 scales per 128 (aq, as) or fake-quantized
+// bf16 (xa); one or two projections (index 1 null: one); optional SwiGLU epilogue (hh and/or hq + hs).
+struct MxGemvArgs {
+  const uint8_t* aq;
+  const uint8_t* as;
+  const uint16_t* xa;
+  int K, N, ldo;
+  const Exl3Tile* tiles;
+  const int* ntiles_dev;
+  const uint8_t* const* w_tab[2];
+  const uint8_t* const* s_tab[2];
+  uint16_t* out[2];
+  float* out32;  // non-null: projection 0 written as fp32 (before bf16 rounding) instead
+  int rows_cap;
+  const float* gw;
+  const int32_t* grow_expert;
+  const uint8_t* const* gs_tab;
+  uint16_t* hh;
+  uint8_t* hq;
+  uint8_t* hs;
+  float limit;
+};
+
+void launch_mx_gemv(const MxGemvArgs& a, int ntiles, bool abf16, hipStream_t st);
+void launch_mx_gemm(const MxGemvArgs& a, int ntiles, bool abf16, hipStream_t st);
+void launch_mx_transform(int mode, const uint16_t* x, int ldx, const int32_t* x_rows, const uint16_t* u,
+                         const float* w, float limit, const int32_t* row_expert, const uint8_t* const* s_tab,
+                         uint16_t* out, uint8_t* q, uint8_t* qs, int K, int P, hipStream_t st);
+
+}  // namespace unholy::kernels

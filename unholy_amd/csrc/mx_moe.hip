@@ -1,0 +1,530 @@
+// MXFP4 routed-expert kernels for gfx950: layout repack, activation transforms, the grouped GEMV for decode /
+// verify tiles and its SwiGLU epilogue, and the MFMA decode self-check. The prefill grouped GEMM is in
+// mx_gemm.hip. Entry points and layouts: include/unholy/kernels/mx_moe.hpp.
+#include <algorithm>
+#include <cstdlib>
+#include <string>
+
+#include "common.hpp"
+#include "numerics.hpp"
+#include "unholy/kernels/mx_moe.hpp"
+#include "mx_internal.hpp"
+
+namespace unholy::kernels {
+
+using namespace uh;
+
+namespace {
+
+// One thread per (row n, 16-byte piece p of the row's K/2 code bytes), which is also one scale byte (K/32 of
+// each per row): the piece goes to chunk (p/2) * (N/16) + n/16 at (n % 16) * 32 + (p % 2) * 16, the scale
+// byte b = p to chunk (b/2) * (N/16) + n/16 at (n % 16) * 2 + b % 2 (ref mx_moe.hip:82-96, expert_pack.cpp:146-166).
+__global__ __launch_bounds__(256) void mx_repack_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ s,
+                                                        uint8_t* __restrict__ tw, uint8_t* __restrict__ ts, int N,
+                                                        int K) {
+  const size_t gid = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  const int per_row = K / 32;
+  if (gid >= size_t(N) * per_row) return;
+  const int n = int(gid / per_row), p = int(gid % per_row);
+  const size_t chunk = size_t(p / 2) * (N / 16) + n / 16;
+  *reinterpret_cast<uint4*>(tw + chunk * 512 + (n % 16) * 32 + (p % 2) * 16) =
+      *reinterpret_cast<const uint4*>(w + gid * 16);
+  ts[chunk * 32 + (n % 16) * 2 + p % 2] = s[gid];
+}
+
+// Activation transforms on a wave per (row, 128-value segment), two values per lane, items striding over the
+// grid. kMode 0: x rows -> fake-quantized bf16 (mx_xform_in); 1: x rows -> e4m3 codes + e8m0 scale
+// (mx_xform_in_fp8); 2: g/u rows -> bf16 SwiGLU -> fake-quantized bf16 and/or codes (mx_swiglu). Rows whose
+// expert's scale-table entry is null are skipped (ref mx_moe.hip:132-179).
+template <int kMode>
+__global__ __launch_bounds__(256) void mx_transform_kernel(const bf16* __restrict__ x, int ldx,
+                                                           const int32_t* __restrict__ x_rows,
+                                                           const bf16* __restrict__ u, const float* __restrict__ w,
+                                                           float limit, const int32_t* __restrict__ row_expert,
+                                                           const uint8_t* const* __restrict__ s_tab,
+                                                           bf16* __restrict__ out, uint8_t* __restrict__ q,
+                                                           uint8_t* __restrict__ qs, int K, int P) {
+  const int lane = threadIdx.x & 63, segs = K / 128;
+  const size_t n = size_t(P) * segs;
+  for (size_t it = size_t(blockIdx.x) * 4 + (threadIdx.x >> 6); it < n; it += size_t(gridDim.x) * 4) {
+    const int r = int(it / segs), seg = int(it % segs), k0 = seg * 128 + 2 * lane;
+    if (s_tab && !s_tab[row_expert[r]]) continue;  // uniform per wave
+    float v[2];
+    if constexpr (kMode == 2) {
+      const uint32_t graw = *reinterpret_cast<const uint32_t*>(x + size_t(r) * ldx + k0);
+      const uint32_t uraw = *reinterpret_cast<const uint32_t*>(u + size_t(r) * ldx + k0);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        v[i] = round_bf16(swiglu_value(bf16_to_f32(uint16_t(graw >> (16 * i))), bf16_to_f32(uint16_t(uraw >> (16 * i))),
+                                       w ? w[r] : 0.0f, w != nullptr, limit));
+    } else {
+      const size_t src = x_rows ? size_t(x_rows[r]) : size_t(r);
+      const uint32_t raw = *reinterpret_cast<const uint32_t*>(x + src * ldx + k0);
+      v[0] = bf16_to_f32(uint16_t(raw));
+      v[1] = bf16_to_f32(uint16_t(raw >> 16));
+    }
+    const Fp8Block b = fp8_block_scale(wave_max(fmaxf(fabsf(v[0]), fabsf(v[1]))));
+    const uint8_t c0 = fp8_code(v[0], b.sc), c1 = fp8_code(v[1], b.sc);
+    if (out)
+      *reinterpret_cast<uint32_t*>(out + size_t(r) * K + k0) =
+          uint32_t(f32_to_bf16(e4m3_to_f32(c0) * b.sc)) | uint32_t(f32_to_bf16(e4m3_to_f32(c1) * b.sc)) << 16;
+    if (q) {
+      *reinterpret_cast<uint16_t*>(q + size_t(r) * K + k0) = uint16_t(c0 | uint32_t(c1) << 8);
+      if (lane == 0) qs[size_t(r) * segs + seg] = b.se;
+    }
+  }
+}
+
+unsigned transform_blocks(int P, int K) { return unsigned(std::min<size_t>((size_t(P) * (K / 128) + 3) / 4, 16384)); }
+
+// ---- grouped GEMV ----------------------------------------------------------------------------------------------------
+// A workgroup = 4 waves x GV_TN 16-output tiles = 128 outputs of one tile (one expert's run of <= 16 pair rows), for
+// one or two projections (w1 and w3 of the same rows). The tile's rows are staged once into LDS as e4m3 codes + e8m0
+// scales (copied from the fp8 form, or recovered exactly from fake-quantized bf16 rows); then every wave streams its
+// weight columns straight from HBM into registers: per 128-input step, lane l takes the 16 code bytes of column
+// l % 16, inputs 32 (l / 16) .. + 31 (chunk 2s + (l/16)/2 at (l % 16) * 32 + ((l/16) % 2) * 16: each half-wave
+// reads one contiguous 512-byte chunk of the tile-major layout) and that 32-block's scale byte, dequantizes them
+// exactly to bf16 with the scaled conversion instructions and issues four bf16 MFMAs against the matching
+// activation inputs. The MFMA accumulates in fp32 with exact products; no cross-lane reductions are needed.
+constexpr int GV_NT = 256, GV_WAVES = 4, GV_TN = 2, GV_PAD = 16, GV_MAXROWS = 16;
+
+template <int NP, bool GLU, bool ABF16>
+__global__ __launch_bounds__(GV_NT) void mx_gemv_kernel(MxGemvArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  if (a.ntiles_dev && int(blockIdx.y) >= *a.ntiles_dev) return;
+  const Exl3Tile tile = a.tiles[blockIdx.y];
+  if (tile.rows <= 0) return;
+  const uint8_t* wp[NP];
+  const uint8_t* sp[NP];
+  wp[0] = a.w_tab[0][tile.expert];
+  sp[0] = a.s_tab[0][tile.expert];
+  if constexpr (NP == 2) {
+    wp[1] = a.w_tab[1][tile.expert];
+    sp[1] = a.s_tab[1][tile.expert];
+  }
+#pragma unroll
+  for (int p = 0; p < NP; ++p)
+    if (!wp[p] || !sp[p]) return;
+  const int K = a.K, N = a.N, KS = K / 128, ldA = K + GV_PAD, ntn = N / 16;
+  uint8_t* sA = smem;
+  uint8_t* sS = smem + size_t(a.rows_cap) * ldA;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nl = lane & 15, g = lane >> 4;
+  int nt[GV_TN];
+#pragma unroll
+  for (int j = 0; j < GV_TN; ++j) nt[j] = blockIdx.x * (GV_WAVES * GV_TN) + wave * GV_TN + j;
+  const int boff = nl * 32 + (g & 1) * 16, soff = nl * 2 + (g & 1);
+  for (int rg = 0; rg < tile.rows; rg += a.rows_cap) {
+    const int M = min(a.rows_cap, tile.rows - rg);
+    const size_t row0 = size_t(tile.row0) + rg;
+    __syncthreads();
+    if constexpr (ABF16) {
+      // 8 values per thread; 16 consecutive threads hold one 128-block (K / 8 is a multiple of 16).
+      const int total = M * (K / 8);
+      for (int base = 0; base < total; base += GV_NT) {
+        const int i = base + tid, m = i / (K / 8), c = (i % (K / 8)) * 8;
+        const bool valid = i < total;
+        float v[8];
+        float am = 0.0f;
+        if (valid) {
+          const uint4 raw = *reinterpret_cast<const uint4*>(a.xa + (row0 + m) * size_t(K) + c);
+          const uint32_t r4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            v[2 * t] = __uint_as_float(r4[t] << 16);
+            v[2 * t + 1] = __uint_as_float(r4[t] & 0xffff0000u);
+          }
+#pragma unroll
+          for (int t = 0; t < 8; ++t) am = fmaxf(am, fabsf(v[t]));
+        }
+        am = group_max<16>(am);
+        if (valid) {
+          const uint8_t se = uint8_t(min(max(int(exact_fp8_scale(am)), 1), 254));
+          const float inv = e8m0_to_f32(uint8_t(254 - se));  // 2^(127 - se), exact
+          uint32_t lo = 0, hi = 0;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            lo |= uint32_t(f32_to_e4m3(v[t] * inv)) << (8 * t);
+            hi |= uint32_t(f32_to_e4m3(v[t + 4] * inv)) << (8 * t);
+          }
+          *reinterpret_cast<uint2*>(sA + m * ldA + c) = make_uint2(lo, hi);
+          if ((c & 127) == 0) sS[m * KS + c / 128] = se;
+        }
+      }
+    } else {
+      const int total = M * (K / 16);
+      for (int i = tid; i < total; i += GV_NT) {
+        const int m = i / (K / 16), c = (i % (K / 16)) * 16;
+        *reinterpret_cast<uint4*>(sA + m * ldA + c) = *reinterpret_cast<const uint4*>(a.aq + (row0 + m) * K + c);
+      }
+      for (int i = tid; i < M * KS; i += GV_NT) sS[i] = a.as[row0 * KS + i];
+    }
+    __syncthreads();
+
+    v4f acc[NP][GV_TN];
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int j = 0; j < GV_TN; ++j) acc[p][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    const bool arow = nl < M;
+    const uint8_t* ap = sA + nl * ldA + g * 32;
+    const uint8_t* asp = sS + nl * KS;
+#pragma unroll 2
+    for (int s = 0; s < KS; ++s) {
+      v4i b[NP][GV_TN];
+      uint32_t sb[NP][GV_TN];
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int j = 0; j < GV_TN; ++j)
+          if (nt[j] < ntn) {
+            const size_t chunk = size_t(2 * s + (g >> 1)) * ntn + nt[j];
+            b[p][j] = *reinterpret_cast<gptr<v4i>>(as_global(wp[p] + chunk * 512 + boff));
+            sb[p][j] = *as_global(sp[p] + chunk * 32 + soff);
+          }
+      // The lane's activation inputs 32g .. 32g + 31 of the step (row nl), dequantized to bf16 once and used
+      // for every column tile; MFMA sub-step t takes inputs 32g + 8t .. + 7 on both operands.
+      bf16x8 af[4];
+      if (arow) {
+        const v4i lo = *reinterpret_cast<const v4i*>(ap + s * 128), hi = *reinterpret_cast<const v4i*>(ap + s * 128 + 16);
+        const float sc = e8m0_to_f32(asp[s]);
+        af[0] = fp8x8_to_bf16(lo[0], lo[1], sc);
+        af[1] = fp8x8_to_bf16(lo[2], lo[3], sc);
+        af[2] = fp8x8_to_bf16(hi[0], hi[1], sc);
+        af[3] = fp8x8_to_bf16(hi[2], hi[3], sc);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) af[t] = bf16x8{};
+      }
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int j = 0; j < GV_TN; ++j)
+          if (nt[j] < ntn) {
+            const float sc = __uint_as_float(sb[p][j] << 23);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[p][j] = mfma_bf16(af[t], fp4x8_to_bf16(uint32_t(b[p][j][t]), sc), acc[p][j]);
+          }
+    }
+
+    if constexpr (!GLU) {
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        bf16* o = a.out[p];
+#pragma unroll
+        for (int j = 0; j < GV_TN; ++j)
+          if (nt[j] < ntn)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int r = 4 * g + i;
+              if (r >= M) continue;
+              if (p == 0 && a.out32) a.out32[(row0 + r) * a.ldo + nt[j] * 16 + nl] = acc[p][j][i];
+              else o[(row0 + r) * a.ldo + nt[j] * 16 + nl] = f32_to_bf16(acc[p][j][i]);
+            }
+      }
+    } else {
+      // SwiGLU of the bf16-rounded projections, then the fake quantization of each row's 128 outputs (the whole
+      // workgroup: N % 128 == 0 is checked on the host) with the row's amax gathered over the 4 waves.
+      __shared__ float red[GV_WAVES][16];
+      float h[GV_TN][4], am[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < GV_TN; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 4 * g + i;
+          const float gv = round_bf16(acc[0][j][i]), uv = round_bf16(acc[NP - 1][j][i]);
+          h[j][i] = 0.0f;
+          if (r < M) {
+            const size_t row = row0 + r, col = size_t(nt[j]) * 16 + nl;
+            if (a.out[0]) a.out[0][row * a.ldo + col] = f32_to_bf16(gv);
+            if (a.out[1]) a.out[1][row * a.ldo + col] = f32_to_bf16(uv);
+            h[j][i] = round_bf16(swiglu_value(gv, uv, a.gw ? a.gw[row] : 0.0f, a.gw != nullptr, a.limit));
+          }
+          am[i] = fmaxf(am[i], fabsf(h[j][i]));
+        }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        am[i] = group_max<16>(am[i]);
+        if (nl == 0) red[wave][4 * g + i] = am[i];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * g + i;
+        if (r >= M) continue;
+        const size_t row = row0 + r;
+        if (a.gs_tab && !a.gs_tab[a.grow_expert[row]]) continue;
+        const Fp8Block blk =
+            fp8_block_scale(fmaxf(fmaxf(red[0][r], red[1][r]), fmaxf(red[2][r], red[3][r])));
+#pragma unroll
+        for (int j = 0; j < GV_TN; ++j) {
+          const size_t col = size_t(nt[j]) * 16 + nl;
+          const uint8_t c = fp8_code(h[j][i], blk.sc);
+          if (a.hh) a.hh[row * N + col] = f32_to_bf16(e4m3_to_f32(c) * blk.sc);
+          if (a.hq) a.hq[row * N + col] = c;
+        }
+        if (a.hs && wave == 0 && nl == 0) a.hs[row * (N / 128) + blockIdx.x] = blk.se;
+      }
+    }
+  }
+}
+
+// Exhaustive decode check, one wave per e8m0 scale value sv (0..254): the scaled bf16 conversions of every e2m1 and
+// e4m3 code (the bf16-MFMA kernels' dequantization), then the block-scaled MFMA's own decode. Weight operand: B[k][n] = e2m1 code
+// (k/8 + n) % 16 with scale sv, activations one-hot 1.0 at k = 8m, so C[m][n] = e2m1((m+n) % 16) * 2^(sv-127).
+// Activation operand: A[m][8m] = e4m3 code 16q + m (q = 0..15, 16 MFMAs) with scale sv, B all 1.0 (scale 127),
+// so C[m][n] = e4m3(16q + m) * 2^(sv-127). Results are compared with the closed forms in fp32; cnt[0]
+// counts mismatches where the expected value is a normal number, cnt[1] the compared normal values, cnt[2]
+// mismatches at zero / subnormal / overflowing values (the hardware may flush those; no checkpoint scale
+// produces them).
+__device__ __forceinline__ void check_count(float got, float want, unsigned long long* c) {
+  const float aw = fabsf(want);
+  const bool normal = aw >= 1.17549435e-38f && aw <= 3.40282347e38f;
+  const bool same = got == want;
+  if (normal) {
+    if (!same) atomicAdd(&c[0], 1ull);
+    atomicAdd(&c[1], 1ull);
+  } else if (aw != 0.0f && !same) {
+    atomicAdd(&c[2], 1ull);
+  }
+}
+// Sets the 8-bit operand byte of input k (0..127) to `code` in the lane of group (k % 64) / 16.
+__device__ __forceinline__ void put_a8(v8i& a, int g, int k, int code) {
+  if ((k % 64) / 16 != g) return;
+  const int byte = (k / 64) * 16 + k % 16;
+  a[byte / 4] |= code << (8 * (byte % 4));
+}
+__global__ __launch_bounds__(64) void mx_check_dequant_kernel(unsigned long long* cnt) {
+  const int sv = blockIdx.x, lane = threadIdx.x, nl = lane & 15, g = lane >> 4;
+  {  // weight side
+    v8i a = {0, 0, 0, 0, 0, 0, 0, 0};
+    put_a8(a, g, 8 * nl, 0x38);  // A[m][8m] = 1.0
+    v4i b;
+    for (int d = 0; d < 4; ++d) {
+      uint32_t word = 0;
+      for (int t = 0; t < 8; ++t) {
+        const int k = 32 * g + 8 * d + t;
+        word |= uint32_t((k / 8 + nl) % 16) << (4 * t);
+      }
+      b[d] = int(word);
+    }
+    const v4f c = mfma_fp8_fp4(a, b, 127, sv, v4f{0.0f, 0.0f, 0.0f, 0.0f});
+    for (int i = 0; i < 4; ++i) {
+      const int m = 4 * g + i;
+      check_count(c[i], e2m1_to_f32(uint32_t((m + nl) % 16)) * e8m0_to_f32(uint8_t(sv)), cnt);
+    }
+  }
+  {  // the scaled conversions used by the bf16 kernels: lane = byte value (x4), every code of the dword
+    const float sc = e8m0_to_f32(uint8_t(sv));
+    for (int rep = 0; rep < 4; ++rep) {
+      const uint32_t byte = uint32_t(lane + 64 * rep);
+      const uint32_t w = byte | (byte << 8) | (byte << 16) | (byte << 24);
+      const bf16x8 d4 = fp4x8_to_bf16(w, sc);
+      const bf16x8 d8 = fp8x8_to_bf16(w, w, sc);
+      for (int i = 0; i < 8; ++i) {
+        check_count(float(d4[i]), round_bf16(e2m1_to_f32((i & 1) ? (byte >> 4) : (byte & 15)) * sc), cnt);
+        if ((byte & 0x7f) != 0x7f) check_count(float(d8[i]), round_bf16(e4m3_to_f32(uint8_t(byte)) * sc), cnt);
+      }
+    }
+  }
+  v4i ones;
+  for (int d = 0; d < 4; ++d) ones[d] = 0x22222222;  // e2m1 code 2 = 1.0
+  for (int q = 0; q < 16; ++q) {  // activation side
+    const int code = 16 * q + nl;
+    v8i a = {0, 0, 0, 0, 0, 0, 0, 0};
+    put_a8(a, g, 8 * nl, code);
+    const v4f c = mfma_fp8_fp4(a, ones, sv, 127, v4f{0.0f, 0.0f, 0.0f, 0.0f});
+    for (int i = 0; i < 4; ++i) {
+      const int cm = 16 * q + 4 * g + i;
+      if ((cm & 0x7f) == 0x7f) continue;  // e4m3fn NaN codes
+      check_count(c[i], e4m3_to_f32(uint8_t(cm)) * e8m0_to_f32(uint8_t(sv)), cnt);
+    }
+  }
+}
+
+template <class K>
+void set_lds_limit(K kernel, size_t bytes) {
+  if (bytes > 65536) UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes)));
+}
+
+template <int NP, bool GLU, bool ABF16>
+void launch_gemv_t(const MxGemvArgs& a, int ntiles, hipStream_t st) {
+  const size_t lds = size_t(a.rows_cap) * (a.K + GV_PAD) + size_t(a.rows_cap) * (a.K / 128);
+  auto* kern = &mx_gemv_kernel<NP, GLU, ABF16>;
+  set_lds_limit(kern, lds);
+  const dim3 grid(cdiv(size_t(a.N) / 16, GV_WAVES * GV_TN), unsigned(ntiles), 1);
+  kern<<<grid, GV_NT, lds, st>>>(a);
+  UH_CHECK_LAUNCH();
+}
+
+}  // namespace
+
+// ---- internal launchers (mx_internal.hpp) -----------------------------------------------------------------------------
+void launch_mx_gemv(const MxGemvArgs& a, int ntiles, bool abf16, hipStream_t st) {
+  if (ntiles <= 0) return;
+  if (a.K % 128 || a.N % 16 || a.K <= 0 || a.N <= 0) throw std::runtime_error("mx_grouped_gemv: K % 128 or N % 16");
+  if (a.rows_cap < 1 || a.rows_cap > GV_MAXROWS) throw std::runtime_error("mx_grouped_gemv: rows_cap");
+  const bool np2 = a.w_tab[1] != nullptr, glu = a.hh || a.hq;
+  if (glu && (!np2 || a.N % 128)) throw std::runtime_error("mx_grouped_gemv: glu needs two projections, N % 128");
+  if (glu && a.hq && !a.hs) throw std::runtime_error("mx_grouped_gemv: glu hq without hs");
+  if (abf16 ? !a.xa : (!a.aq || !a.as)) throw std::runtime_error("mx_grouped_gemv: null activations");
+  if (!glu && ((!a.out[0] && !a.out32) || (np2 && !a.out[1]))) throw std::runtime_error("mx_grouped_gemv: null output");
+  if (!a.tiles) throw std::runtime_error("mx_grouped_gemv: null tiles");
+#define UH_GV(NP, GLU)                                             \
+  (abf16 ? launch_gemv_t<NP, GLU, true>(a, ntiles, st) : launch_gemv_t<NP, GLU, false>(a, ntiles, st))
+  if (glu) UH_GV(2, true);
+  else if (np2) UH_GV(2, false);
+  else UH_GV(1, false);
+#undef UH_GV
+}
+
+void launch_mx_transform(int mode, const bf16* x, int ldx, const int32_t* x_rows, const bf16* u, const float* w,
+                         float limit, const int32_t* row_expert, const uint8_t* const* s_tab, bf16* out, uint8_t* q,
+                         uint8_t* qs, int K, int P, hipStream_t st) {
+  if (P <= 0) return;
+  if (K % 128) throw std::runtime_error("mx transform: K % 128");
+  if (ldx % 2) throw std::runtime_error("mx transform: ldx must be even (4-byte row pairs)");
+  if (s_tab && !row_expert) throw std::runtime_error("mx transform: s_tab without row_expert");
+  const unsigned blocks = transform_blocks(P, K);
+  if (mode == 2)
+    mx_transform_kernel<2><<<blocks, 256, 0, st>>>(x, ldx, nullptr, u, w, limit, row_expert, s_tab, out, q, qs, K, P);
+  else if (out)
+    mx_transform_kernel<0><<<blocks, 256, 0, st>>>(x, ldx, x_rows, nullptr, nullptr, 0.0f, row_expert, s_tab, out, q, qs, K, P);
+  else
+    mx_transform_kernel<1><<<blocks, 256, 0, st>>>(x, ldx, x_rows, nullptr, nullptr, 0.0f, row_expert, s_tab, nullptr, q, qs,
+                                                   K, P);
+  UH_CHECK_LAUNCH();
+}
+
+// ---- public entry points ----------------------------------------------------------------------------------------------
+void mx_repack_to(const uint8_t* w, const uint8_t* s, uint8_t* tw, uint8_t* ts, int N, int K, hipStream_t st) {
+  if (N <= 0 || K <= 0 || N % 16 || K % 64) throw std::runtime_error("mx_repack_to: N % 16 or K % 64");
+  mx_repack_kernel<<<cdiv(size_t(N) * (K / 32), 256), 256, 0, st>>>(w, s, tw, ts, N, K);
+  UH_CHECK_LAUNCH();
+}
+
+void mx_repack(uint8_t* w, uint8_t* s, int N, int K, uint8_t* tmp, hipStream_t st) {
+  const size_t wb = size_t(N) * K / 2, sb = size_t(N) * (K / 32);
+  mx_repack_to(w, s, tmp, tmp + wb, N, K, st);
+  UH_CHECK(hipMemcpyAsync(w, tmp, wb, hipMemcpyDeviceToDevice, st));
+  UH_CHECK(hipMemcpyAsync(s, tmp + wb, sb, hipMemcpyDeviceToDevice, st));
+}
+
+void mx_xform_in(const bf16* x, int ldx, const int32_t* row_expert, const uint8_t* const* s_tab, bf16* xa, int P,
+                 int K, hipStream_t st, const int32_t* x_rows) {
+  launch_mx_transform(0, x, ldx, x_rows, nullptr, nullptr, 0.0f, row_expert, s_tab, xa, nullptr, nullptr, K, P, st);
+}
+
+void mx_xform_in_fp8(const bf16* x, int ldx, const int32_t* row_expert, const uint8_t* const* s_tab, uint8_t* q,
+                     uint8_t* qs, int P, int K, hipStream_t st, const int32_t* x_rows) {
+  if (!q || !qs) throw std::runtime_error("mx_xform_in_fp8: null q / qs");
+  launch_mx_transform(1, x, ldx, x_rows, nullptr, nullptr, 0.0f, row_expert, s_tab, nullptr, q, qs, K, P, st);
+}
+
+void mx_swiglu(const bf16* g, const bf16* u, const float* w, const int32_t* row_expert, const uint8_t* const* s_tab,
+               bf16* hh, int P, int I, float limit, hipStream_t st) {
+  launch_mx_transform(2, g, I, nullptr, u, w, limit, row_expert, s_tab, hh, nullptr, nullptr, I, P, st);
+}
+
+int mx_gemv_max_tokens() {
+  static const int v = [] {
+    const char* e = std::getenv("UNHOLY_MX_GEMV_TOKENS");
+    return e ? std::max(kMxGemvTileRows, std::atoi(e)) : kMxGemvTileRows;
+  }();
+  return v;
+}
+bool mx_skinny_enabled() { return true; }
+bool mx_gemm_rb() { return false; }
+void mx_gemm_force_rb(int) {}
+void mx_gemm_rb_double_buffer(int) {}
+namespace {
+int g_glu = -1;
+}
+bool mx_gemm_glu() {
+  static const bool env = [] {
+    const char* v = std::getenv("UNHOLY_MX_GLU");
+    return !v || std::string(v) != "0";
+  }();
+  return g_glu < 0 ? env : g_glu > 0;
+}
+void mx_gemm_force_glu(int on) { g_glu = on; }
+
+unsigned long long mx_check_dequant(unsigned long long* total) {
+  unsigned long long* cnt = nullptr;
+  UH_CHECK(hipMalloc(&cnt, 3 * sizeof(unsigned long long)));
+  UH_CHECK(hipMemset(cnt, 0, 3 * sizeof(unsigned long long)));
+  mx_check_dequant_kernel<<<255, 64>>>(cnt);
+  UH_CHECK_LAUNCH();
+  unsigned long long h[3] = {};
+  UH_CHECK(hipMemcpy(h, cnt, sizeof(h), hipMemcpyDeviceToHost));
+  UH_CHECK(hipFree(cnt));
+  if (total) *total = h[1];
+  return h[0];
+}
+
+namespace {
+MxGemvArgs gemv_args(const bf16* xa, const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles,
+                     const uint8_t* const* w_tab, const uint8_t* const* s_tab, bf16* out, int ldo, int N,
+                     const int* ntiles_dev, const uint8_t* const* w_tab2, const uint8_t* const* s_tab2, bf16* out2,
+                     int rows_cap, const MxGlu& glu) {
+  MxGemvArgs a{};
+  a.xa = xa;
+  a.aq = q;
+  a.as = qs;
+  a.K = K;
+  a.N = N;
+  a.ldo = ldo;
+  a.tiles = tiles;
+  a.ntiles_dev = ntiles_dev;
+  a.w_tab[0] = w_tab;
+  a.s_tab[0] = s_tab;
+  a.out[0] = out;
+  a.w_tab[1] = w_tab2;
+  a.s_tab[1] = s_tab2;
+  a.out[1] = out2;
+  a.rows_cap = std::max(1, std::min(rows_cap, GV_MAXROWS));
+  a.gw = glu.w;
+  a.grow_expert = glu.row_expert;
+  a.gs_tab = glu.s_tab;
+  a.hh = glu.hh;
+  a.hq = glu.hq;
+  a.hs = glu.hs;
+  a.limit = glu.limit;
+  if ((a.hh || a.hq) && a.gs_tab && !a.grow_expert) throw std::runtime_error("MxGlu: s_tab without row_expert");
+  if (!w_tab || !s_tab) throw std::runtime_error("mx grouped: null tables");
+  if (!w_tab2 != !s_tab2) throw std::runtime_error("mx grouped: second projection tables");
+  return a;
+}
+}  // namespace
+
+void mx_grouped_gemv(const bf16* xa, int K, const Exl3Tile* tiles, int ntiles, const uint8_t* const* w_tab,
+                     const uint8_t* const* s_tab, bf16* out, int ldo, int N, hipStream_t st, const int* ntiles_dev,
+                     const uint8_t* const* w_tab2, const uint8_t* const* s_tab2, bf16* out2, int max_rows,
+                     const MxGlu& glu, const MxSums& sums) {
+  if (sums.dst) throw std::runtime_error("mx_grouped_gemv: MxSums (remote token sums) is not supported");
+  if ((glu.hh || glu.hq) && ldo != N) throw std::runtime_error("mx_grouped_gemv: glu shape (ldo != N)");
+  launch_mx_gemv(gemv_args(xa, nullptr, nullptr, K, tiles, w_tab, s_tab, out, ldo, N, ntiles_dev, w_tab2, s_tab2,
+                           out2, max_rows, glu),
+                 ntiles, true, st);
+}
+
+void mx_grouped_gemv_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles, int ntiles,
+                              const uint8_t* const* w_tab, const uint8_t* const* s_tab, float* out, int ldo, int N,
+                              hipStream_t st, const int* ntiles_dev, int max_rows) {
+  MxGemvArgs a = gemv_args(nullptr, q, qs, K, tiles, w_tab, s_tab, nullptr, ldo, N, ntiles_dev, nullptr, nullptr,
+                           nullptr, max_rows, MxGlu{});
+  a.out32 = out;
+  launch_mx_gemv(a, ntiles, false, st);
+}
+
+void mx_grouped_gemv_q(const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles, int ntiles,
+                       const uint8_t* const* w_tab, const uint8_t* const* s_tab, bf16* out, int ldo, int N,
+                       hipStream_t st, const int* ntiles_dev, const uint8_t* const* w_tab2,
+                       const uint8_t* const* s_tab2, bf16* out2, int max_rows, const MxGlu& glu) {
+  if ((glu.hh || glu.hq) && ldo != N && (out || out2)) throw std::runtime_error("mx_grouped_gemv_q: glu shape");
+  launch_mx_gemv(gemv_args(nullptr, q, qs, K, tiles, w_tab, s_tab, out, ldo, N, ntiles_dev, w_tab2, s_tab2, out2,
+                           max_rows, glu),
+                 ntiles, false, st);
+}
+
+}  // namespace unholy::kernels

@@ -1,0 +1,116 @@
+// Device numerics for gfx950 (wave64). Storage types are raw integers: bf16 = uint16_t, fp8 e4m3fn and
+// e2m1 codes and e8m0 scale exponents = uint8_t. Every conversion that decides a stored bit is written out
+// here so that it rounds exactly as the reference's device helpers (src/kernels/dev.hip.hpp:40-127):
+// bf16 RNE with NaN kept quiet, e4m3fn RNE with the subnormal range scaled by 2^9, power-of-two ceil
+// scales as e8m0 bytes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace uh {
+
+using bf16 = uint16_t;
+
+__device__ __forceinline__ float bf16_to_f32(bf16 v) { return __uint_as_float(uint32_t(v) << 16); }
+
+// Round to nearest even; NaN stays a quiet NaN (dev.hip.hpp:43-48).
+__device__ __forceinline__ bf16 f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return bf16((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return bf16(u >> 16);
+}
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// OCP e4m3fn decode (dev.hip.hpp:59-63).
+__device__ __forceinline__ float e4m3_to_f32(uint8_t v) {
+  const uint32_t e = (v >> 3) & 0xf, m = v & 7;
+  const float a = e == 0 ? float(m) * (1.0f / 512.0f) : __uint_as_float((e + 120u) << 23 | m << 20);
+  return (v & 0x80) ? -a : a;
+}
+
+// RNE into e4m3fn for |x| <= 448 (dev.hip.hpp:82-94): below 2^-6 the value is scaled by 2^9 (exact) and
+// rounded to an integer mantissa; above, the fp32 mantissa is rounded at 3 bits.
+__device__ __forceinline__ uint8_t f32_to_e4m3(float x) {
+  uint32_t u = __float_as_uint(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  u &= 0x7fffffffu;
+  const int e = int(u >> 23) - 127;
+  if (e < -6) return uint8_t(sign | uint32_t(rintf(__uint_as_float(u) * 512.0f)));
+  u += 0x7ffffu + ((u >> 20) & 1u);
+  return uint8_t(sign | ((u >> 23) - 120u) << 3 | ((u >> 20) & 7u));
+}
+
+__device__ __forceinline__ float e8m0_to_f32(uint8_t v) { return __uint_as_float(uint32_t(v) << 23); }
+
+__device__ __forceinline__ float e2m1_to_f32(uint32_t nib) {
+  const uint32_t m = nib & 7;
+  const float mag = m < 4 ? 0.5f * float(m) : (m == 7 ? 6.0f : float(m - 2));
+  return (nib & 8) ? -mag : mag;
+}
+
+// 2^ceil(log2(v)) of a positive normal v, as an e8m0 byte (dev.hip.hpp:123-127).
+__device__ __forceinline__ uint8_t pow2_ceil_e8m0(float v) {
+  const uint32_t b = __float_as_uint(v);
+  return uint8_t(int((b >> 23) & 0xff) + ((b & 0x7fffff) != 0 ? 1 : 0));
+}
+
+// The e8m0 byte of the smallest power-of-two scale sc with amax / sc <= 448, exactly (integer logic, no
+// rounding of amax / 448): amax = f * 2^E, f in [1, 2): E - 8 when f <= 1.75 (448 = 1.75 * 2^8), else E - 7.
+// Used to recover the fp8 codes of values that are already e4m3 * 2^k (fake-quantized rows): any such scale
+// leaves every code exact. amax == 0 gives 127 (codes all zero).
+__device__ __forceinline__ uint8_t exact_fp8_scale(float amax) {
+  const uint32_t b = __float_as_uint(amax);
+  if (b == 0) return 127;
+  const int E = int(b >> 23);  // biased
+  return uint8_t(E - 8 + ((b & 0x7fffff) > 0x600000u ? 1 : 0));
+}
+
+// Wave64 reductions over all 64 lanes (every lane active).
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+// Max over groups of G consecutive lanes (G a power of two <= 64).
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = G / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// The reference's activation fake quantization of one value given its block's amax (ref_elem.hip:32-37):
+// amax floored at 1e-4, e8m0 scale 2^ceil(log2(amax / 448)), e4m3 RNE of the clamped quotient.
+struct Fp8Block {
+  uint8_t se;
+  float sc;
+};
+__device__ __forceinline__ Fp8Block fp8_block_scale(float amax) {
+  const uint8_t se = pow2_ceil_e8m0(fmaxf(amax, 1e-4f) * (1.0f / 448.0f));
+  return {se, e8m0_to_f32(se)};
+}
+__device__ __forceinline__ uint8_t fp8_code(float v, float sc) {
+  return f32_to_e4m3(fminf(fmaxf(v / sc, -448.0f), 448.0f));
+}
+
+// SwiGLU with the clamp and optional routing weight (ref_moe.hip:66-72): x = silu(min(g, l)) * clamp(u, +-l),
+// then w * x; limit <= 0 turns the clamp off.
+__device__ __forceinline__ float swiglu_value(float g, float u, float w, bool has_w, float limit) {
+  if (limit > 0.0f) {
+    u = fminf(fmaxf(u, -limit), limit);
+    g = fminf(g, limit);
+  }
+  float x = (g / (1.0f + expf(-g))) * u;
+  if (has_w) x = w * x;
+  return x;
+}
+
+}  // namespace uh
