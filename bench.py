@@ -1,0 +1,284 @@
+#!/usr/bin/env python3
+"""Benchmark of the MXFP4 routed-expert FFN on one MI355X (gfx950).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
+
+A step is one routed-expert FFN over one batch of synthetic tokens: softmax top-6 routing of [T, 256] logits,
+dispatch, fp8 input transform, w1/w3 grouped GEMV with the SwiGLU epilogue, w2 grouped GEMV, combine to bf16
+[T, 4096] -- everything uh_mx_moe_forward enqueues. The headline workload is BASELINE configs[1] (decode, T = 8
+tokens, 256 experts of MXFP4 w1/w3 [2048, 4096] + w2 [4096, 2048]); inputs and weights are resident in HBM before
+the timed region. Each step takes the next of R rotating (x, logits) sets, so consecutive steps route to different
+experts and the touched weights (~590 MB per step) do not stay in the 256 MB Infinity Cache.
+
+Prints ONE JSON line (rank 0, N = 1). `roofline` is for the dominant kernel (the w1/w3 + SwiGLU grouped GEMV),
+timed with HIP events on the launch stream inside the timed region; `cpu_baseline` is the repository's CPU oracle
+(oracle/, the reference arithmetic) on a bounded sample of the same workload. `workloads` adds the other BASELINE
+configurations (single GEMV, verify M = 64, prefill M = 4096, fp8 dense M = 1 / 64 / 4096), each timed the same way.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+D, I, E, TOPK = 4096, 2048, 256, 6
+MAT_BYTES = I * D // 2 + I * D // 32  # 4,456,448: codes + e8m0 scales of one MXFP4 [2048, 4096] matrix
+EXPERT_BYTES = 3 * MAT_BYTES
+LIMIT = 10.0
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def to_bf16(x):
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+class Weights:
+    """256 experts of synthetic MXFP4 weights in the tile-major layout: code bytes uniform over 0..255 (every
+    nibble uniform over the 16 e2m1 codes), e8m0 scales uniform in [119, 125] (2^-8 .. 2^-2), written on the device."""
+
+    def __init__(self, seed=0):
+        from unholy_amd.device import DeviceBuffer, fill_random_bytes, pointer_table
+        self.buf = DeviceBuffer(E * EXPERT_BYTES)
+        base = self.buf.ptr
+        shapes = [(I, D), (I, D), (D, I)]
+        tab = [[None] * E for _ in range(6)]
+        off = 0
+        for e in range(E):
+            for m, (n, k) in enumerate(shapes):
+                cb, sb = n * k // 2, n * k // 32
+                tab[2 * m][e] = base + off
+                tab[2 * m + 1][e] = base + off + cb
+                off += cb + sb
+        fill_random_bytes(self.buf, E * EXPERT_BYTES, seed, 0, 255)
+        for e in range(E):  # scales
+            for m in range(3):
+                fill_random_bytes(tab[2 * m + 1][e], shapes[m][0] * shapes[m][1] // 32, seed + 1 + 3 * e + m, 119, 125)
+        self.ptrs = tab
+        self.table = pointer_table([p for row in tab for p in row])
+
+
+def routing_sets(rng, T, R, bias_scale=0.0):
+    sets = []
+    bias = rng.standard_normal(E).astype(np.float32) * np.float32(bias_scale) if bias_scale else None
+    for _ in range(R):
+        x = to_bf16(rng.standard_normal((T, D), dtype=np.float32))
+        logits = rng.standard_normal((T, E), dtype=np.float32)
+        if bias is not None:
+            logits = logits + bias
+        sets.append((x, logits))
+    return sets
+
+
+def distinct_experts(logits):
+    """Experts a softmax top-6 step touches (selection by logit, as the router)."""
+    sel = np.argsort(-logits, axis=1, kind="stable")[:, :TOPK]
+    return len(np.unique(sel)), sel
+
+
+class MoeRunner:
+    def __init__(self, w, sets):
+        from unholy_amd import call
+        from unholy_amd.device import DeviceBuffer, Event
+        self.call, self.w = call, w
+        self.T = sets[0][0].shape[0]
+        self.dev = [(DeviceBuffer.from_array(x), DeviceBuffer.from_array(l)) for x, l in sets]
+        self.U = [distinct_experts(l)[0] for _, l in sets]
+        self.ws_bytes = call("uh_mx_moe_workspace_size", self.T, TOPK, E, D, I)
+        self.ws = DeviceBuffer(self.ws_bytes)
+        self.out = DeviceBuffer(self.T * D * 2)
+        self.ev = []  # per timed step: events around the w1/w3 + SwiGLU GEMV
+        self.evarr = (ctypes.c_void_p * 6)()
+        self.Event = Event
+
+    def step(self, i, stage_events=False):
+        x, l = self.dev[i % len(self.dev)]
+        if stage_events:
+            while len(self.ev) <= i:
+                self.ev.append((self.Event(), self.Event()))
+            self.evarr[2], self.evarr[3] = self.ev[i][0].handle, self.ev[i][1].handle
+        self.call("uh_mx_moe_forward_ev", x, l, self.T, TOPK, E, D, I, self.w.table, LIMIT, self.ws, self.ws_bytes,
+                  self.out, None, None, None, self.evarr if stage_events else None)
+
+
+def time_steps(fn, steps, warmup, timed_fn=None):
+    """Total ms of `steps` calls after `warmup` (timed_fn, if given, is the form used inside the timed region)."""
+    from unholy_amd.device import Event, synchronize
+    for i in range(warmup):
+        fn(i)
+    synchronize()
+    a, b = Event(), Event()
+    a.record()
+    for i in range(steps):
+        (timed_fn or fn)(i)
+    b.record()
+    b.synchronize()
+    return a.elapsed_ms(b)
+
+
+def bench_moe(w, T, steps, warmup, rng, R=8, bias=0.0, stage=False):
+    from unholy_amd.device import synchronize
+    sets = routing_sets(rng, T, R, bias)
+    r = MoeRunner(w, sets)
+    ms = time_steps(lambda i: r.step(i), steps, warmup, (lambda i: r.step(i, True)) if stage else None)
+    synchronize()
+    stage_ms = [(r.ev[i][0].elapsed_ms(r.ev[i][1]), r.U[i % R]) for i in range(steps)] if stage else []
+    u_mean = float(np.mean([r.U[i % R] for i in range(steps)]))
+    return dict(ms=ms / steps, U=u_mean, stage=stage_ms, runner=r)
+
+
+def bench_single_gemv(w, steps, warmup, rng):
+    """x [1, 4096] through act_quant, one MXFP4 [2048, 4096] matrix (a 1-row tile), rotating
+    over the 256 experts' w1 matrices (1.1 GB) so the weights come from HBM."""
+    from unholy_amd import call
+    from unholy_amd.device import DeviceBuffer
+    x = to_bf16(rng.standard_normal((1, D), dtype=np.float32))
+    dx = DeviceBuffer.from_array(x)
+    q, qs = DeviceBuffer(D), DeviceBuffer(D // 128)
+    call("uh_act_quant_fp8", dx, D, q, qs, 1, D, 128, None)
+    tiles = [DeviceBuffer.from_array(np.array([[e, 0, 1]], np.int32)) for e in range(E)]
+    out = DeviceBuffer(I * 2)
+    wt, st = w.table.ptr, w.table.ptr + 8 * E
+
+    def fn(i):
+        call("uh_mx_grouped_gemv_q", q, qs, D, tiles[i % E], 1, wt, st, out, I, I, None, None, None, None, None, 1,
+             None, None, None, None, None, None, 0.0)
+
+    ms = time_steps(fn, steps, warmup) / steps
+    return ms
+
+
+def bench_fp8_dense(M, steps, warmup, rng, copies):
+    """A bf16 [M, 4096] -> e4m3 per 1x128 with fp32 scales (in the step); W e4m3 [4096, 4096]
+    with fp32 128x128 scales (quantized once from N(0, 0.02)); rotating over `copies` weight copies."""
+    from unholy_amd import call
+    from unholy_amd.device import DeviceBuffer
+    N = K = 4096
+    wf = DeviceBuffer.from_array(rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+    wq = [DeviceBuffer(N * K) for _ in range(copies)]
+    ws = DeviceBuffer((N // 128) * (K // 128) * 4)
+    for c in wq:
+        call("uh_quant_weight_fp8_f32s", wf, c, ws, N, K, None)
+    del wf
+    x = DeviceBuffer.from_array(to_bf16(rng.standard_normal((M, K), dtype=np.float32)))
+    q, sa = DeviceBuffer(M * K), DeviceBuffer(M * (K // 128) * 4)
+    c = DeviceBuffer(M * N * 2)
+
+    def fn(i):
+        call("uh_act_quant_fp8_f32s", x, K, q, sa, M, K, 128, None)
+        call("uh_gemm_fp8_f32s", q, sa, wq[i % copies], ws, c, N, M, N, K, None)
+
+    return time_steps(fn, steps, warmup) / steps
+
+
+def cpu_baseline(seconds=10.0, max_reps=5):
+    """The CPU oracle (reference arithmetic, oracle/uh_oracle.cpp) on one decode step of the headline workload:
+    T = 8 tokens, softmax top-6 over 256 experts; host weights are generated for the experts the step touches only
+    (the others are never read). Threads: one per host core up to 16 (the box's CPU share)."""
+    import oracle
+    rng = np.random.default_rng(1234)
+    T = 8
+    x = to_bf16(rng.standard_normal((T, D), dtype=np.float32))
+    logits = rng.standard_normal((T, E), dtype=np.float32)
+    sel, wt = oracle.route_softmax(logits, TOPK)
+    touched = sorted(set(sel.ravel().tolist()))
+    experts = [None] * E
+    for e in touched:
+        ex = {}
+        for (wn, sn), (n, k) in ((("w1", "s1"), (I, D)), (("w3", "s3"), (I, D)), (("w2", "s2"), (D, I))):
+            ex[wn] = rng.integers(0, 256, n * k // 2, dtype=np.uint8)
+            ex[sn] = rng.integers(119, 126, n * k // 32, dtype=np.uint8)
+        experts[e] = ex
+    threads = max(1, min(16, os.cpu_count() or 1))
+    reps, t0 = 0, time.perf_counter()
+    while reps < max_reps and (time.perf_counter() - t0) < seconds:
+        oracle.moe_forward(x, sel, wt, experts, D, I, LIMIT, tiled=True, threads=threads)
+        reps += 1
+    dt = time.perf_counter() - t0
+    return dict(value=T * reps / dt, unit="tokens/s", cores=threads, kind="port",
+                sample=f"{reps} decode step(s) of T=8 tokens, 256 experts, top-6 ({len(touched)} experts touched, "
+                       f"{dt:.1f} s on {threads} threads)")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the MoE expert path runs on a single MI355X in this build "
+              "(expert-parallel sharding is a design note, not implemented); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    from unholy_amd.device import device_name
+
+    rng = np.random.default_rng(0)
+    w = Weights(seed=0)
+    dec = bench_moe(w, 8, args.steps, args.warmup, rng, stage=True)
+    ms = dec["ms"]
+    U = dec["U"]
+    # dominant kernel: the w1/w3 + SwiGLU grouped GEMV; algorithmic bytes = touched experts' w1 + w3 (codes +
+    # scales) + the pair rows' fp8 inputs (P x 4096 + scales) + hh out (P x 2048 codes + scales)
+    P = 8 * TOPK
+    gemv_ms = [m for m, _ in dec["stage"]]
+    gemv_bytes = [u * 2 * MAT_BYTES + P * (D + D // 128) + P * (I + I // 128) for _, u in dec["stage"]]
+    g_ms = float(np.mean(gemv_ms))
+    achieved = float(np.mean(gemv_bytes)) / (g_ms * 1e-3) / 1e9
+    step_bytes = U * EXPERT_BYTES + 8 * D * 2 * 2
+    result = {
+        "metric": "MoE expert-FFN tokens/s (decode, BASELINE configs[1])",
+        "value": 8 / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp4 weights x e4m3 activations, exact bf16 dequant, bf16 MFMA, fp32 accumulate",
+        "data": "synthetic (device splitmix64 weights, numpy PCG64 activations/logits)",
+        "config": {"workload": "moe_decode_T8 (BASELINE configs[1])", "tokens": 8, "experts": E, "top_k": TOPK,
+                   "dim": D, "moe_inter": I, "swiglu_limit": LIMIT, "rotating_sets": 8,
+                   "distinct_experts_per_step": U, "step_algorithmic_bytes": step_bytes,
+                   "step_GBps": step_bytes / (ms * 1e-3) / 1e9, "device": device_name()},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "mx_gemv_kernel<2,true,false> (w1/w3 + SwiGLU)", "avg_launch_ms": g_ms,
+                     "algorithmic_bytes_per_launch": float(np.mean(gemv_bytes))},
+    }
+    if not args.no_sweep:
+        wl = {}
+        s0 = bench_single_gemv(w, 500, 50, rng)
+        wl["single_gemv_M1 (configs[0])"] = {"ms": s0, "GBps": (MAT_BYTES + D + D // 128 + I * 2) / (s0 * 1e-3) / 1e9}
+        v = bench_moe(w, 64, 50, 5, rng, bias=0.5)
+        wl["moe_verify_T64 (configs[2])"] = {"ms": v["ms"], "tokens_per_s": 64 / (v["ms"] * 1e-3),
+                                              "distinct_experts": v["U"],
+                                              "GBps_weights": v["U"] * EXPERT_BYTES / (v["ms"] * 1e-3) / 1e9}
+        p = bench_moe(w, 4096, 5, 1, rng, R=2)
+        flops = 4096 * TOPK * 3 * 2 * D * I
+        wl["moe_prefill_T4096 (configs[3])"] = {"ms": p["ms"], "tokens_per_s": 4096 / (p["ms"] * 1e-3),
+                                                 "TFLOPs": flops / (p["ms"] * 1e-3) / 1e12,
+                                                 "frac_bf16_mfma_peak": flops / (p["ms"] * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+                                                 "GBps_weights": E * EXPERT_BYTES / (p["ms"] * 1e-3) / 1e9}
+        for M, copies in ((1, 64), (64, 64), (4096, 4)):
+            t = bench_fp8_dense(M, 100 if M < 4096 else 10, 10 if M < 4096 else 2, rng, copies)
+            wl[f"fp8_dense_M{M} (configs[4])"] = {"ms": t, "tokens_per_s": M / (t * 1e-3),
+                                                  "TFLOPs": 2 * M * D * D / (t * 1e-3) / 1e12,
+                                                  "GBps_weights": D * D / (t * 1e-3) / 1e9}
+        result["workloads"] = wl
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

@@ -174,6 +174,11 @@ size_t uh_mx_moe_workspace_size(int T, int K, int E, int D, int I);
 int uh_mx_moe_forward(const uint16_t* x, const float* logits, int T, int K, int E, int D, int I,
                       const uint8_t* const* tab, float limit, void* ws, size_t ws_bytes, uint16_t* out, int32_t* sel,
                       float* wt, void* stream);
+/* The same with stage events (6 hipEvent_t, recorded on `stream` before routing, after routing + dispatch, after
+ * the input transform, after w1/w3 + SwiGLU, after w2, after the combine; NULL entries are skipped). */
+int uh_mx_moe_forward_ev(const uint16_t* x, const float* logits, int T, int K, int E, int D, int I,
+                         const uint8_t* const* tab, float limit, void* ws, size_t ws_bytes, uint16_t* out, int32_t* sel,
+                         float* wt, void* stream, void* const* events);
 
 #ifdef __cplusplus
 }

@@ -399,7 +399,16 @@ size_t uh_mx_moe_workspace_size(int T, int K, int E, int D, int I) { return carv
 int uh_mx_moe_forward(const uint16_t* x, const float* logits, int T, int K, int E, int D, int I,
                       const uint8_t* const* tab, float limit, void* ws, size_t ws_bytes, uint16_t* out, int32_t* sel,
                       float* wt, void* stream) {
+  return uh_mx_moe_forward_ev(x, logits, T, K, E, D, I, tab, limit, ws, ws_bytes, out, sel, wt, stream, nullptr);
+}
+
+int uh_mx_moe_forward_ev(const uint16_t* x, const float* logits, int T, int K, int E, int D, int I,
+                         const uint8_t* const* tab, float limit, void* ws, size_t ws_bytes, uint16_t* out, int32_t* sel,
+                         float* wt, void* stream, void* const* events) {
   return guard([&] {
+    const auto mark = [&](int i) {
+      if (events && events[i]) UH_CHECK(hipEventRecord(static_cast<hipEvent_t>(events[i]), static_cast<hipStream_t>(stream)));
+    };
     if (T <= 0) return;
     const MoeWs w = carve(static_cast<char*>(ws), T, K, E, D, I);
     if (ws_bytes < w.bytes) throw std::runtime_error("uh_mx_moe_forward: workspace too small");
@@ -409,6 +418,7 @@ int uh_mx_moe_forward(const uint16_t* x, const float* logits, int T, int K, int 
     int32_t* s_sel = sel ? sel : w.sel;
     float* s_wt = wt ? wt : w.wt;
     const auto t = [&](int m, int f) { return tab + size_t(2 * m + f) * E; };
+    mark(0);
     k::route_softmax(logits, s_sel, s_wt, T, E, K, st);
     const int* ntd = &reinterpret_cast<const k::MoePlan*>(w.plan)->n_local_tiles;
     k::Exl3Tile* tiles = reinterpret_cast<k::Exl3Tile*>(w.tiles);
@@ -436,20 +446,26 @@ int uh_mx_moe_forward(const uint16_t* x, const float* logits, int T, int K, int 
                   w.max_tiles, st, w.tile_rows);
       k::moe_scatter_e(s_sel, s_wt, T, K, E, w.off, w.eidx, w.ewt, w.row_expert, w.pidx, st);
     }
+    mark(1);
     k::mx_xform_in_fp8(x, D, w.row_expert, t(0, 1), w.xq, w.xs, P, D, st, w.eidx);
+    mark(2);
     const k::MxGlu glu{w.ewt, w.row_expert, t(2, 1), nullptr, limit, nullptr, w.hq, w.hs};
     if (T <= 64) {
       k::mx_grouped_gemv_q(w.xq, w.xs, D, tiles, w.max_tiles, t(0, 0), t(0, 1), nullptr, I, I, st, ntd, t(1, 0), t(1, 1),
                            nullptr, w.tile_rows, glu);
+      mark(3);
       k::mx_grouped_gemv_q(w.hq, w.hs, I, tiles, w.max_tiles, t(2, 0), t(2, 1), w.pair_out, D, D, st, ntd, nullptr,
                            nullptr, nullptr, w.tile_rows);
     } else {
       k::mx_grouped_gemm_q(w.xq, w.xs, D, tiles, w.max_tiles, t(0, 0), t(0, 1), nullptr, I, I, st, ntd, t(1, 0), t(1, 1),
                            nullptr, w.tile_rows, glu);
+      mark(3);
       k::mx_grouped_gemm_q(w.hq, w.hs, I, tiles, w.max_tiles, t(2, 0), t(2, 1), w.pair_out, D, D, st, ntd, nullptr,
                            nullptr, nullptr, w.tile_rows);
     }
+    mark(4);
     k::moe_combine(w.pair_out, w.pidx, nullptr, out, T, K, D, st);
+    mark(5);
   });
 }
 

@@ -78,18 +78,19 @@ __global__ __launch_bounds__(256) void mx_transform_kernel(const bf16* __restric
 unsigned transform_blocks(int P, int K) { return unsigned(std::min<size_t>((size_t(P) * (K / 128) + 3) / 4, 16384)); }
 
 // ---- grouped GEMV ----------------------------------------------------------------------------------------------------
-// A workgroup = 4 waves x GV_TN 16-output tiles = 128 outputs of one tile (one expert's run of <= 16 pair rows), for
+// A workgroup = 8 waves x one 16-output tile each = 128 outputs of one tile (one expert's run of <= 16 pair rows), for
 // one or two projections (w1 and w3 of the same rows). The tile's rows are staged once into LDS as e4m3 codes + e8m0
 // scales (copied from the fp8 form, or recovered exactly from fake-quantized bf16 rows); then every wave streams its
-// weight columns straight from HBM into registers: per 128-input step, lane l takes the 16 code bytes of column
-// l % 16, inputs 32 (l / 16) .. + 31 (chunk 2s + (l/16)/2 at (l % 16) * 32 + ((l/16) % 2) * 16: each half-wave
-// reads one contiguous 512-byte chunk of the tile-major layout) and that 32-block's scale byte, dequantizes them
-// exactly to bf16 with the scaled conversion instructions and issues four bf16 MFMAs against the matching
-// activation inputs. The MFMA accumulates in fp32 with exact products; no cross-lane reductions are needed.
-constexpr int GV_NT = 256, GV_WAVES = 4, GV_TN = 2, GV_PAD = 16, GV_MAXROWS = 16;
+// weight columns straight from HBM into registers, GV_PF 128-input steps ahead of use: per step, lane l takes the
+// 16 code bytes of column l % 16, inputs 32 (l / 16) .. + 31 (chunk 2s + (l/16)/2 at (l % 16) * 32 + ((l/16) % 2)
+// * 16: each half-wave reads one contiguous 512-byte chunk of the tile-major layout) and that 32-block's scale
+// byte, dequantizes them exactly to bf16 with the scaled conversion instructions and issues four bf16 MFMAs against
+// the matching activation inputs. The MFMA accumulates in fp32 with exact products; no cross-lane reductions.
+constexpr int GV_WAVES = 8, GV_NT = 64 * GV_WAVES, GV_PAD = 16, GV_MAXROWS = 16, GV_PF = 4;
 
-template <int NP, bool GLU, bool ABF16>
-__global__ __launch_bounds__(GV_NT) void mx_gemv_kernel(MxGemvArgs a) {
+// OCC: waves per SIMD the register budget is sized for (4: two workgroups per CU).
+template <int NP, bool GLU, bool ABF16, int OCC>
+__global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(OCC))) void mx_gemv_kernel(MxGemvArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   if (a.ntiles_dev && int(blockIdx.y) >= *a.ntiles_dev) return;
   const Exl3Tile tile = a.tiles[blockIdx.y];
@@ -109,13 +110,28 @@ __global__ __launch_bounds__(GV_NT) void mx_gemv_kernel(MxGemvArgs a) {
   uint8_t* sA = smem;
   uint8_t* sS = smem + size_t(a.rows_cap) * ldA;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nl = lane & 15, g = lane >> 4;
-  int nt[GV_TN];
-#pragma unroll
-  for (int j = 0; j < GV_TN; ++j) nt[j] = blockIdx.x * (GV_WAVES * GV_TN) + wave * GV_TN + j;
+  const int nt = blockIdx.x * GV_WAVES + wave;
+  const bool active = nt < ntn;  // uniform per wave
   const int boff = nl * 32 + (g & 1) * 16, soff = nl * 2 + (g & 1);
   for (int rg = 0; rg < tile.rows; rg += a.rows_cap) {
     const int M = min(a.rows_cap, tile.rows - rg);
     const size_t row0 = size_t(tile.row0) + rg;
+    // Prefetch the first GV_PF steps of weights before staging the activations (independent of them).
+    v4i bq[GV_PF][NP];
+    uint32_t sq[GV_PF][NP];
+    // 32-bit offsets from the (uniform) matrix base: loads take the scalar-base + vector-offset form.
+    const uint32_t cofs = uint32_t(((g >> 1) * ntn + nt) * 512 + boff), sofs = uint32_t(((g >> 1) * ntn + nt) * 32 + soff);
+    const uint32_t cstep = uint32_t(2 * ntn * 512), sstep = uint32_t(2 * ntn * 32);
+    const auto load_step = [&](int s, int slot) {
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        bq[slot][p] = *reinterpret_cast<gptr<v4i>>(as_global(wp[p]) + (cofs + uint32_t(s) * cstep));
+        sq[slot][p] = *(as_global(sp[p]) + (sofs + uint32_t(s) * sstep));
+      }
+    };
+    if (active)
+#pragma unroll
+      for (int i = 0; i < GV_PF; ++i) load_step(min(i, KS - 1), i);  // K < 128 * GV_PF: re-read the last step
     __syncthreads();
     if constexpr (ABF16) {
       // 8 values per thread; 16 consecutive threads hold one 128-block (K / 8 is a multiple of 16).
@@ -160,90 +176,76 @@ __global__ __launch_bounds__(GV_NT) void mx_gemv_kernel(MxGemvArgs a) {
     }
     __syncthreads();
 
-    v4f acc[NP][GV_TN];
+    v4f acc[NP];
 #pragma unroll
-    for (int p = 0; p < NP; ++p)
-#pragma unroll
-      for (int j = 0; j < GV_TN; ++j) acc[p][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int p = 0; p < NP; ++p) acc[p] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     const bool arow = nl < M;
     const uint8_t* ap = sA + nl * ldA + g * 32;
     const uint8_t* asp = sS + nl * KS;
-#pragma unroll 2
-    for (int s = 0; s < KS; ++s) {
-      v4i b[NP][GV_TN];
-      uint32_t sb[NP][GV_TN];
+    if (active)
+      for (int s0 = 0; s0 < KS; s0 += GV_PF) {
 #pragma unroll
-      for (int p = 0; p < NP; ++p)
+        for (int i = 0; i < GV_PF; ++i) {
+          const int s = s0 + i;
+          if (s < KS) {
+          // The lane's activation inputs 32g .. 32g + 31 of the step (row nl), dequantized to bf16 once for both
+          // projections; MFMA sub-step t takes inputs 32g + 8t .. + 7 on both operands.
+          bf16x8 af[4];
+          if (arow) {
+            const v4i lo = *reinterpret_cast<const v4i*>(ap + s * 128);
+            const v4i hi = *reinterpret_cast<const v4i*>(ap + s * 128 + 16);
+            const float sc = e8m0_to_f32(asp[s]);
+            af[0] = fp8x8_to_bf16(lo[0], lo[1], sc);
+            af[1] = fp8x8_to_bf16(lo[2], lo[3], sc);
+            af[2] = fp8x8_to_bf16(hi[0], hi[1], sc);
+            af[3] = fp8x8_to_bf16(hi[2], hi[3], sc);
+          } else {
 #pragma unroll
-        for (int j = 0; j < GV_TN; ++j)
-          if (nt[j] < ntn) {
-            const size_t chunk = size_t(2 * s + (g >> 1)) * ntn + nt[j];
-            b[p][j] = *reinterpret_cast<gptr<v4i>>(as_global(wp[p] + chunk * 512 + boff));
-            sb[p][j] = *as_global(sp[p] + chunk * 32 + soff);
+            for (int t = 0; t < 4; ++t) af[t] = bf16x8{};
           }
-      // The lane's activation inputs 32g .. 32g + 31 of the step (row nl), dequantized to bf16 once and used
-      // for every column tile; MFMA sub-step t takes inputs 32g + 8t .. + 7 on both operands.
-      bf16x8 af[4];
-      if (arow) {
-        const v4i lo = *reinterpret_cast<const v4i*>(ap + s * 128), hi = *reinterpret_cast<const v4i*>(ap + s * 128 + 16);
-        const float sc = e8m0_to_f32(asp[s]);
-        af[0] = fp8x8_to_bf16(lo[0], lo[1], sc);
-        af[1] = fp8x8_to_bf16(lo[2], lo[3], sc);
-        af[2] = fp8x8_to_bf16(hi[0], hi[1], sc);
-        af[3] = fp8x8_to_bf16(hi[2], hi[3], sc);
-      } else {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) af[t] = bf16x8{};
+          for (int p = 0; p < NP; ++p) {
+            const float sc = __uint_as_float(sq[i][p] << 23);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[p] = mfma_bf16(af[t], fp4x8_to_bf16(uint32_t(bq[i][p][t]), sc), acc[p]);
+          }
+          }
+          load_step(min(s + GV_PF, KS - 1), i);  // unconditional: past the end it re-reads the last step (cached)
+          // Keep each step's conversions and MFMAs together: interleaving the unrolled steps would only
+          // raise register pressure (the loads of later steps are already in flight).
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
-#pragma unroll
-      for (int p = 0; p < NP; ++p)
-#pragma unroll
-        for (int j = 0; j < GV_TN; ++j)
-          if (nt[j] < ntn) {
-            const float sc = __uint_as_float(sb[p][j] << 23);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) acc[p][j] = mfma_bf16(af[t], fp4x8_to_bf16(uint32_t(b[p][j][t]), sc), acc[p][j]);
-          }
-    }
 
     if constexpr (!GLU) {
+      if (active)
 #pragma unroll
-      for (int p = 0; p < NP; ++p) {
-        bf16* o = a.out[p];
+        for (int p = 0; p < NP; ++p)
 #pragma unroll
-        for (int j = 0; j < GV_TN; ++j)
-          if (nt[j] < ntn)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int r = 4 * g + i;
-              if (r >= M) continue;
-              if (p == 0 && a.out32) a.out32[(row0 + r) * a.ldo + nt[j] * 16 + nl] = acc[p][j][i];
-              else o[(row0 + r) * a.ldo + nt[j] * 16 + nl] = f32_to_bf16(acc[p][j][i]);
-            }
-      }
+          for (int i = 0; i < 4; ++i) {
+            const int r = 4 * g + i;
+            if (r >= M) continue;
+            const size_t o = (row0 + r) * a.ldo + nt * 16 + nl;
+            if (p == 0 && a.out32) a.out32[o] = acc[p][i];
+            else a.out[p][o] = f32_to_bf16(acc[p][i]);
+          }
     } else {
       // SwiGLU of the bf16-rounded projections, then the fake quantization of each row's 128 outputs (the whole
-      // workgroup: N % 128 == 0 is checked on the host) with the row's amax gathered over the 4 waves.
+      // workgroup: N % 128 == 0 is checked on the host) with the row's amax gathered over the 8 waves.
       __shared__ float red[GV_WAVES][16];
-      float h[GV_TN][4], am[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int j = 0; j < GV_TN; ++j)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = 4 * g + i;
-          const float gv = round_bf16(acc[0][j][i]), uv = round_bf16(acc[NP - 1][j][i]);
-          h[j][i] = 0.0f;
-          if (r < M) {
-            const size_t row = row0 + r, col = size_t(nt[j]) * 16 + nl;
-            if (a.out[0]) a.out[0][row * a.ldo + col] = f32_to_bf16(gv);
-            if (a.out[1]) a.out[1][row * a.ldo + col] = f32_to_bf16(uv);
-            h[j][i] = round_bf16(swiglu_value(gv, uv, a.gw ? a.gw[row] : 0.0f, a.gw != nullptr, a.limit));
-          }
-          am[i] = fmaxf(am[i], fabsf(h[j][i]));
-        }
+      float h[4], am[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        am[i] = group_max<16>(am[i]);
+        const int r = 4 * g + i;
+        const float gv = round_bf16(acc[0][i]), uv = round_bf16(acc[NP - 1][i]);
+        h[i] = 0.0f;
+        if (r < M) {
+          const size_t row = row0 + r, col = size_t(nt) * 16 + nl;
+          if (a.out[0]) a.out[0][row * a.ldo + col] = f32_to_bf16(gv);
+          if (a.out[1]) a.out[1][row * a.ldo + col] = f32_to_bf16(uv);
+          h[i] = round_bf16(swiglu_value(gv, uv, a.gw ? a.gw[row] : 0.0f, a.gw != nullptr, a.limit));
+        }
+        am[i] = group_max<16>(fabsf(h[i]));
         if (nl == 0) red[wave][4 * g + i] = am[i];
       }
       __syncthreads();
@@ -253,15 +255,14 @@ __global__ __launch_bounds__(GV_NT) void mx_gemv_kernel(MxGemvArgs a) {
         if (r >= M) continue;
         const size_t row = row0 + r;
         if (a.gs_tab && !a.gs_tab[a.grow_expert[row]]) continue;
-        const Fp8Block blk =
-            fp8_block_scale(fmaxf(fmaxf(red[0][r], red[1][r]), fmaxf(red[2][r], red[3][r])));
+        float rm = red[0][r];
 #pragma unroll
-        for (int j = 0; j < GV_TN; ++j) {
-          const size_t col = size_t(nt[j]) * 16 + nl;
-          const uint8_t c = fp8_code(h[j][i], blk.sc);
-          if (a.hh) a.hh[row * N + col] = f32_to_bf16(e4m3_to_f32(c) * blk.sc);
-          if (a.hq) a.hq[row * N + col] = c;
-        }
+        for (int w = 1; w < GV_WAVES; ++w) rm = fmaxf(rm, red[w][r]);
+        const Fp8Block blk = fp8_block_scale(rm);
+        const size_t col = size_t(nt) * 16 + nl;
+        const uint8_t c = fp8_code(h[i], blk.sc);
+        if (a.hh) a.hh[row * N + col] = f32_to_bf16(e4m3_to_f32(c) * blk.sc);
+        if (a.hq) a.hq[row * N + col] = c;
         if (a.hs && wave == 0 && nl == 0) a.hs[row * (N / 128) + blockIdx.x] = blk.se;
       }
     }
@@ -347,12 +348,20 @@ void set_lds_limit(K kernel, size_t bytes) {
                                                   hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes)));
 }
 
+int gemv_occ() {
+  static const int v = [] {
+    const char* e = std::getenv("UH_GEMV_OCC");
+    return e ? std::atoi(e) : 2;
+  }();
+  return v;
+}
+
 template <int NP, bool GLU, bool ABF16>
 void launch_gemv_t(const MxGemvArgs& a, int ntiles, hipStream_t st) {
   const size_t lds = size_t(a.rows_cap) * (a.K + GV_PAD) + size_t(a.rows_cap) * (a.K / 128);
-  auto* kern = &mx_gemv_kernel<NP, GLU, ABF16>;
+  auto* kern = gemv_occ() >= 4 ? &mx_gemv_kernel<NP, GLU, ABF16, 4> : &mx_gemv_kernel<NP, GLU, ABF16, 2>;
   set_lds_limit(kern, lds);
-  const dim3 grid(cdiv(size_t(a.N) / 16, GV_WAVES * GV_TN), unsigned(ntiles), 1);
+  const dim3 grid(cdiv(size_t(a.N) / 16, GV_WAVES), unsigned(ntiles), 1);
   kern<<<grid, GV_NT, lds, st>>>(a);
   UH_CHECK_LAUNCH();
 }
