@@ -78,6 +78,9 @@ struct MoeSmallArgs {
   uint8_t* qs_dst = nullptr;
   uint32_t* req_flag = nullptr;
   uint32_t req_value = 0;
+  // Extension (no counterpart in the reference): softmax top-K routing in the launch (route_softmax's picks and
+  // weights written to sel / wt).
+  const float* softmax_logits = nullptr;
 };
 void moe_dispatch_small(const MoeSmallArgs& a, hipStream_t st);
 

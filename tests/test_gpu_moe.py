@@ -156,3 +156,35 @@ def test_moe_forward_vs_oracle(T, E, K, D, I, bias):
     mr = max_rel(got, ref)
     print(f"moe T={T} E={E}: max_rel {mr:.3e}, rel_l2 {rel_l2(got, ref):.3e}")
     assert mr <= 1e-2
+
+
+@pytest.mark.parametrize("mode", ["glm", "ds"])
+def test_dispatch_small_with_routing(mode):
+    """moe_dispatch_small routing in the launch (the reference's MoeSmallArgs route_logits / ds_logits)."""
+    rng = np.random.default_rng(17)
+    T, E, K, tile_rows = 12, 256, 6, 8
+    logits = rng.standard_normal((T, E), dtype=np.float32) * 2
+    bias = rng.standard_normal(E, dtype=np.float32) * 0.2
+    if mode == "glm":
+        sel_ref, wt_ref = oracle.route_glm(logits, bias, K, 2.0)
+    else:
+        sel_ref, wt_ref = oracle.route_ds(logits, bias, K, 2.0)
+    P = T * K
+    ref = oracle.dispatch(sel_ref, wt_ref, E, tile_rows)
+    max_tiles = P + E
+    sel, wt = DeviceBuffer(P * 4), DeviceBuffer(P * 4)
+    bufs = dict(plan=DeviceBuffer(20), tiles=DeviceBuffer(max_tiles * 12), eidx=DeviceBuffer(P * 4),
+                ewt=DeviceBuffer(P * 4), row_expert=DeviceBuffer(P * 4), pidx=DeviceBuffer(P * 4))
+    dl, db = dev(logits), dev(bias)
+    glm = mode == "glm"
+    call("uh_moe_dispatch_small", sel, wt, T, K, E, P, max_tiles, tile_rows, bufs["plan"], bufs["tiles"],
+         bufs["eidx"], bufs["ewt"], bufs["row_expert"], bufs["pidx"], None, dl if glm else None, db if glm else None,
+         2.0, None if glm else dl, None if glm else db, None, None, None, 0, None)
+    assert np.array_equal(sel.download((T, K), np.int32), sel_ref)
+    np.testing.assert_allclose(wt.download((T, K), np.float32), wt_ref, rtol=1e-5)
+    plan = bufs["plan"].download(5, np.int32)
+    assert np.array_equal(bufs["eidx"].download(P, np.int32), ref["eidx"])
+    assert np.array_equal(bufs["row_expert"].download(P, np.int32), ref["row_expert"])
+    assert np.array_equal(bufs["pidx"].download((T, K), np.int32), ref["pidx"])
+    assert plan[2] == ref["plan"][2]
+    assert np.array_equal(bufs["tiles"].download((max_tiles, 3), np.int32)[: plan[2]], ref["tiles"])

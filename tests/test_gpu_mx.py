@@ -208,3 +208,37 @@ def test_grouped_gemv_glu(abf16):
         q2, s2 = oracle.act_quant_fp8(oracle.swiglu(gg, uu, rw, limit))
         same = (hgot == h_ref).all(axis=1)
         assert np.array_equal(codes[same], q2[same]) and np.array_equal(scales[same], s2[same])
+
+
+def test_gemv_x_fused_quant_is_bit_identical():
+    """uh_mx_grouped_gemv_x (act_quant of gathered token rows in the GEMV's staging) == xform_in_fp8 + gemv_q."""
+    rng = np.random.default_rng(21)
+    E, K, N, T, limit = 3, 2048, 256, 9, 10.0
+    rows = [4, 7, 2]
+    P = sum(rows)
+    tiles, row_expert, r0 = [], [], 0
+    for e, c in enumerate(rows):
+        tiles.append([e, r0, c])
+        row_expert += [e] * c
+        r0 += c
+    x = randn_bf16(rng, (T, K), 2.0)
+    x_rows = rng.integers(0, T, P).astype(np.int32)
+    w1, w3 = _make_experts(rng, E, N, K), _make_experts(rng, E, N, K)
+    b1, t1 = _expert_tables(w1, ("w", "s"))
+    b3, t3 = _expert_tables(w3, ("w", "s"))
+    rw = rng.random(P).astype(np.float32)
+    dx, dr, de, drw, dt = dev(x), dev(x_rows), dev(np.array(row_expert, np.int32)), dev(rw), dev(np.array(tiles, np.int32))
+    q, qs = DeviceBuffer(P * K), DeviceBuffer(P * K // 128)
+    call("uh_mx_xform_in_fp8", dx, K, de, t1["s"], q, qs, P, K, None, dr)
+    outs = []
+    for fused in (False, True):
+        hq, hs, g = DeviceBuffer(P * N), DeviceBuffer(P * N // 128), DeviceBuffer(P * N * 2)
+        if fused:
+            call("uh_mx_grouped_gemv_x", dx, K, dr, K, dt, 3, t1["w"], t1["s"], g, N, N, None, None, t3["w"], t3["s"],
+                 None, 16, drw, de, t1["s"], None, hq, hs, limit)
+        else:
+            call("uh_mx_grouped_gemv_q", q, qs, K, dt, 3, t1["w"], t1["s"], g, N, N, None, None, t3["w"], t3["s"],
+                 None, 16, drw, de, t1["s"], None, hq, hs, limit)
+        outs.append((g.download((P, N), np.uint16), hq.download((P, N), np.uint8), hs.download((P, N // 128), np.uint8)))
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)

@@ -253,6 +253,18 @@ int uh_mx_grouped_gemv_q(const uint8_t* q, const uint8_t* qs, int K, const int32
                          out2, max_rows, glu);
   });
 }
+int uh_mx_grouped_gemv_x(const uint16_t* x, int ldx, const int32_t* x_rows, int K, const int32_t* tiles, int ntiles,
+                         const uint8_t* const* w_tab, const uint8_t* const* s_tab, uint16_t* out, int ldo, int N,
+                         void* st, const int* ntiles_dev, const uint8_t* const* w_tab2, const uint8_t* const* s_tab2,
+                         uint16_t* out2, int max_rows, const float* glu_w, const int32_t* glu_row_expert,
+                         const uint8_t* const* glu_s_tab, uint16_t* glu_hh, uint8_t* glu_hq, uint8_t* glu_hs,
+                         float glu_limit) {
+  return guard([&] {
+    k::MxGlu glu{glu_w, glu_row_expert, glu_s_tab, glu_hh, glu_limit, nullptr, glu_hq, glu_hs};
+    k::mx_grouped_gemv_x(x, ldx, x_rows, K, T3(tiles), ntiles, w_tab, s_tab, out, ldo, N, S(st), ntiles_dev, w_tab2,
+                         s_tab2, out2, max_rows, glu);
+  });
+}
 int uh_mx_grouped_gemv_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const int32_t* tiles, int ntiles,
                                 const uint8_t* const* w_tab, const uint8_t* const* s_tab, float* out, int ldo, int N,
                                 void* st, const int* ntiles_dev, int max_rows) {
@@ -419,7 +431,7 @@ int uh_mx_moe_forward_ev(const uint16_t* x, const float* logits, int T, int K, i
     float* s_wt = wt ? wt : w.wt;
     const auto t = [&](int m, int f) { return tab + size_t(2 * m + f) * E; };
     mark(0);
-    k::route_softmax(logits, s_sel, s_wt, T, E, K, st);
+    if (T > k::kMoeSmallMaxTokens) k::route_softmax(logits, s_sel, s_wt, T, E, K, st);
     const int* ntd = &reinterpret_cast<const k::MoePlan*>(w.plan)->n_local_tiles;
     k::Exl3Tile* tiles = reinterpret_cast<k::Exl3Tile*>(w.tiles);
     if (T <= k::kMoeSmallMaxTokens) {
@@ -438,6 +450,7 @@ int uh_mx_moe_forward_ev(const uint16_t* x, const float* logits, int T, int K, i
       a.ewt = w.ewt;
       a.row_expert = w.row_expert;
       a.pidx = w.pidx;
+      a.softmax_logits = logits;  // routing in the same launch
       k::moe_dispatch_small(a, st);
     } else {
       UH_CHECK(hipMemsetAsync(w.count, 0, size_t(E) * 4, st));
@@ -447,16 +460,17 @@ int uh_mx_moe_forward_ev(const uint16_t* x, const float* logits, int T, int K, i
       k::moe_scatter_e(s_sel, s_wt, T, K, E, w.off, w.eidx, w.ewt, w.row_expert, w.pidx, st);
     }
     mark(1);
-    k::mx_xform_in_fp8(x, D, w.row_expert, t(0, 1), w.xq, w.xs, P, D, st, w.eidx);
-    mark(2);
     const k::MxGlu glu{w.ewt, w.row_expert, t(2, 1), nullptr, limit, nullptr, w.hq, w.hs};
-    if (T <= 64) {
-      k::mx_grouped_gemv_q(w.xq, w.xs, D, tiles, w.max_tiles, t(0, 0), t(0, 1), nullptr, I, I, st, ntd, t(1, 0), t(1, 1),
-                           nullptr, w.tile_rows, glu);
+    if (T <= 64) {  // the input quantization happens in the GEMV's staging
+      mark(2);
+      k::mx_grouped_gemv_x(x, D, w.eidx, D, tiles, w.max_tiles, t(0, 0), t(0, 1), nullptr, I, I, st, ntd, t(1, 0),
+                           t(1, 1), nullptr, w.tile_rows, glu);
       mark(3);
       k::mx_grouped_gemv_q(w.hq, w.hs, I, tiles, w.max_tiles, t(2, 0), t(2, 1), w.pair_out, D, D, st, ntd, nullptr,
                            nullptr, nullptr, w.tile_rows);
     } else {
+      k::mx_xform_in_fp8(x, D, w.row_expert, t(0, 1), w.xq, w.xs, P, D, st, w.eidx);
+      mark(2);
       k::mx_grouped_gemm_q(w.xq, w.xs, D, tiles, w.max_tiles, t(0, 0), t(0, 1), nullptr, I, I, st, ntd, t(1, 0), t(1, 1),
                            nullptr, w.tile_rows, glu);
       mark(3);

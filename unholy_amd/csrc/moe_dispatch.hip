@@ -132,33 +132,71 @@ __global__ __launch_bounds__(SC_NT) void moe_scatter_kernel(const int32_t* __res
 }
 
 // ---- routers: a wave per token ---------------------------------------------------------------------------------------
-// Top-K of key[] (E <= 64 * NV) with ties to the lower index, in selection order, into chosen[] (every lane).
+// Top-K of key[] (E <= 64 * NV) with ties to the lower index, in selection order, into chosen[] (every lane): per
+// round the largest key (a DPP max of the order-preserving bits), then the lowest expert holding it (a DPP min).
 template <int NV>
 __device__ __forceinline__ void wave_topk(float key[NV], int E, int K, int* chosen) {
   const int lane = threadIdx.x & 63;
-  for (int k = 0; k < K; ++k) {
+#pragma unroll
+  for (int k = 0; k < kMaxK; ++k) {  // unrolled: chosen[] stays in registers (a runtime index would put it in scratch)
+    if (k >= K) break;
     float bv = -INFINITY;
-    int bi = 0x7fffffff;
+    uint32_t bi = 0xffffffffu;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int e = lane + 64 * i;
-      if (e < E && (key[i] > bv || bi == 0x7fffffff)) bv = key[i], bi = e;
+      if (e < E && (key[i] > bv || bi == 0xffffffffu)) bv = key[i], bi = uint32_t(e);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (ov > bv || (ov == bv && oi < bi)) bv = ov, bi = oi;
-    }
-    chosen[k] = bi;
+    const uint32_t ob = bi == 0xffffffffu ? 0u : orderable(bv);
+    const uint32_t m = wave_reduce_u32<true>(ob);
+    const uint32_t idx = wave_reduce_u32<false>(ob == m ? bi : 0xffffffffu);
+    chosen[k] = int(idx);
 #pragma unroll
     for (int i = 0; i < NV; ++i)
-      if (lane + 64 * i == bi) key[i] = -INFINITY;
+      if (uint32_t(lane + 64 * i) == idx) key[i] = -INFINITY;
   }
 }
 
 __device__ __forceinline__ float ds_score(float x) { return sqrtf(x > 20.0f ? x : log1pf(expf(x))); }
 __device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// Lane 0's part of a router: GLM reports its picks in ascending id; weights in selection (or id) order:
+// mode 0 score / sum * scale, 1 sigmoid / (sum + 1e-20) * scale, 2 exp(l - l_first) / sum. Loops are unrolled
+// over kMaxK so that the picks stay in registers.
+__device__ __forceinline__ void route_weights(int mode, const float* lr, int* chosen, int K, float route_scale,
+                                              int32_t* sel_t, float* wt_t, int* ssel, float* swt) {
+  if (mode == 1) {
+#pragma unroll
+    for (int x = 1; x < kMaxK; ++x)
+#pragma unroll
+      for (int y = x; y > 0; --y)
+        if (x < K && chosen[y - 1] > chosen[y]) {
+          const int c = chosen[y];
+          chosen[y] = chosen[y - 1];
+          chosen[y - 1] = c;
+        }
+  }
+  float w[kMaxK], sum = 0.0f;
+  const float l0 = lr[chosen[0]];
+#pragma unroll
+  for (int k = 0; k < kMaxK; ++k)
+    if (k < K) {
+      const float l = lr[chosen[k]];
+      w[k] = mode == 2 ? expf(l - l0) : mode == 1 ? sigmoid(l) : ds_score(l);
+      sum += w[k];
+    }
+#pragma unroll
+  for (int k = 0; k < kMaxK; ++k)
+    if (k < K) {
+      const float wk = mode == 2 ? w[k] / sum : mode == 1 ? w[k] / (sum + 1e-20f) * route_scale : (w[k] / sum) * route_scale;
+      sel_t[k] = chosen[k];
+      wt_t[k] = wk;
+      if (ssel) {
+        ssel[k] = chosen[k];
+        swt[k] = wk;
+      }
+    }
+}
 
 // mode 0: DSV4 (sqrt-softplus + bias, hash tid2eid, bias_vl for image ids), 1: GLM sigmoid, 2: softmax top-K.
 template <int MODE>
@@ -175,7 +213,9 @@ __global__ __launch_bounds__(256) void route_wave_kernel(const float* __restrict
   const int32_t* tid2eid = MODE == 0 && !image ? tid2eid0 : nullptr;
   int chosen[kMaxK];
   if (tid2eid) {
-    for (int k = 0; k < K; ++k) chosen[k] = tid2eid[size_t(ids[t]) * K + k];
+#pragma unroll
+    for (int k = 0; k < kMaxK; ++k)
+      if (k < K) chosen[k] = tid2eid[size_t(ids[t]) * K + k];
   } else {
     float key[NV];
 #pragma unroll
@@ -192,25 +232,7 @@ __global__ __launch_bounds__(256) void route_wave_kernel(const float* __restrict
     wave_topk<NV>(key, E, K, chosen);
   }
   if (lane != 0) return;
-  if (MODE == 1)
-    for (int x = 1; x < K; ++x)
-      for (int y = x; y > 0 && chosen[y - 1] > chosen[y]; --y) {
-        const int c = chosen[y];
-        chosen[y] = chosen[y - 1];
-        chosen[y - 1] = c;
-      }
-  float w[kMaxK], sum = 0.0f;
-  for (int k = 0; k < K; ++k) {
-    const float l = lr[chosen[k]];
-    w[k] = MODE == 0 ? ds_score(l) : MODE == 1 ? sigmoid(l) : expf(l - lr[chosen[0]]);
-    sum += w[k];
-  }
-  for (int k = 0; k < K; ++k) {
-    sel[size_t(t) * K + k] = chosen[k];
-    weights[size_t(t) * K + k] = MODE == 0 ? (w[k] / sum) * route_scale
-                                 : MODE == 1 ? w[k] / (sum + 1e-20f) * route_scale
-                                             : w[k] / sum;
-  }
+  route_weights(MODE, lr, chosen, K, route_scale, sel + size_t(t) * K, weights + size_t(t) * K, nullptr, nullptr);
 }
 
 // The reference's one-thread-per-token DSV4 router (ref_moe.hip:14-60): the same picks and weights as the wave
@@ -252,93 +274,134 @@ __global__ void route_thread_kernel(const float* logits, const float* bias0, con
   }
 }
 
-// ---- single-block dispatch for small steps -------------------------------------------------------------------------
-constexpr int SMALL_NT = 1024;
-__global__ __launch_bounds__(SMALL_NT) void moe_dispatch_small_kernel(MoeSmallArgs a) {
-  __shared__ int ssel[kMoeSmallMaxTokens * kMaxK];
-  __shared__ float swt[kMoeSmallMaxTokens * kMaxK];
-  __shared__ int lds[2][SMALL_NT / 64 + 1];
-  const int T = a.T, K = a.K, E = a.E, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // Routing in the launch: a wave per token.
-  if (a.route_logits || a.ds_logits) {
-    for (int t = wave; t < T; t += SMALL_NT / 64) {
-      constexpr int NV = 16;
-      const bool glm = a.route_logits != nullptr;
-      const float* lr = (glm ? a.route_logits : a.ds_logits) + size_t(t) * E;
-      const bool image = !glm && a.ds_bias_vl && a.ids[t] >= a.vocab;
-      const float* bias = glm ? a.route_bias : image ? a.ds_bias_vl : a.ds_bias;
-      const int32_t* tid2eid = !glm && !image ? a.ds_tid2eid : nullptr;
-      int chosen[kMaxK];
-      if (tid2eid) {
-        for (int k = 0; k < K; ++k) chosen[k] = tid2eid[size_t(a.ids[t]) * K + k];
-      } else {
-        float key[NV];
+// One token's routing by one wave inside moe_dispatch_small (MODE 0 DSV4, 1 GLM, 2 softmax; E <= 64 * NV).
+template <int MODE, int NV>
+__device__ __forceinline__ void route_token(const MoeSmallArgs& a, int t, int* skey, float* swt) {
+  const int lane = threadIdx.x & 63, E = a.E, K = a.K;
+  const float* lr = (MODE == 2 ? a.softmax_logits : MODE == 1 ? a.route_logits : a.ds_logits) + size_t(t) * E;
+  const bool image = MODE == 0 && a.ds_bias_vl && a.ids[t] >= a.vocab;
+  const float* bias = MODE == 1 ? a.route_bias : image ? a.ds_bias_vl : a.ds_bias;
+  const int32_t* tid2eid = MODE == 0 && !image ? a.ds_tid2eid : nullptr;
+  int chosen[kMaxK];
+  if (tid2eid) {
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-          const int e = lane + 64 * i;
-          key[i] = e < E ? (glm ? sigmoid(lr[e]) : ds_score(lr[e])) + bias[e] : -INFINITY;
-        }
-        wave_topk<NV>(key, E, K, chosen);
+    for (int k = 0; k < kMaxK; ++k)
+      if (k < K) chosen[k] = tid2eid[size_t(a.ids[t]) * K + k];
+  } else {
+    float key[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = lane + 64 * i;
+      float v = -INFINITY;
+      if (e < E) {
+        if constexpr (MODE == 2) v = lr[e];
+        else if constexpr (MODE == 1) v = sigmoid(lr[e]) + bias[e];
+        else v = ds_score(lr[e]) + bias[e];
       }
-      if (lane == 0) {
-        if (glm)
-          for (int x = 1; x < K; ++x)
-            for (int y = x; y > 0 && chosen[y - 1] > chosen[y]; --y) {
-              const int c = chosen[y];
-              chosen[y] = chosen[y - 1];
-              chosen[y - 1] = c;
-            }
-        float w[kMaxK], sum = 0.0f;
-        for (int k = 0; k < K; ++k) {
-          w[k] = glm ? sigmoid(lr[chosen[k]]) : ds_score(lr[chosen[k]]);
-          sum += w[k];
-        }
-        for (int k = 0; k < K; ++k) {
-          const_cast<int32_t*>(a.sel)[size_t(t) * K + k] = chosen[k];
-          const_cast<float*>(a.wt)[size_t(t) * K + k] =
-              glm ? w[k] / (sum + 1e-20f) * a.route_scale : (w[k] / sum) * a.route_scale;
-        }
+      key[i] = v;
+    }
+    wave_topk<NV>(key, E, K, chosen);
+  }
+  if (lane == 0)
+    route_weights(MODE, lr, chosen, K, a.route_scale, const_cast<int32_t*>(a.sel) + size_t(t) * K,
+                  const_cast<float*>(a.wt) + size_t(t) * K, skey + t * K, swt + t * K);
+}
+
+// ---- single-block dispatch for small steps -------------------------------------------------------------------------
+// T <= 32 tokens, K <= 8 picks: n = T * K <= 256 pair rows, one thread per pick. Optional routing first (a wave per
+// token). Pick i = t * K + j gets the key (e * T + t) * K + j; its pair row is the number of smaller keys, which is
+// exactly the host order (experts ascending, tokens ascending within an expert, equal picks of one token in
+// selection order); the same counting pass gives the expert's first row (keys of smaller experts) and its row
+// count. Tiles start where a row is a multiple of tile_rows into its expert's run; their index is a block scan.
+constexpr int SMALL_NT = 512;
+__global__ __launch_bounds__(SMALL_NT) void moe_dispatch_small_kernel(MoeSmallArgs a) {
+  __shared__ __align__(16) int skey[SMALL_NT];
+  __shared__ float swt[SMALL_NT];
+  __shared__ int lds[SMALL_NT / 64 + 1];
+  const int T = a.T, K = a.K, E = a.E, n = T * K, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool route = a.route_logits || a.ds_logits || a.softmax_logits;
+  if (route) {
+    const int mode = a.softmax_logits ? 2 : a.route_logits ? 1 : 0;
+    for (int t = wave; t < T; t += SMALL_NT / 64) {
+      if (E <= 256) {
+        if (mode == 2) route_token<2, 4>(a, t, skey, swt);
+        else if (mode == 1) route_token<1, 4>(a, t, skey, swt);
+        else route_token<0, 4>(a, t, skey, swt);
+      } else {
+        if (mode == 2) route_token<2, 16>(a, t, skey, swt);
+        else if (mode == 1) route_token<1, 16>(a, t, skey, swt);
+        else route_token<0, 16>(a, t, skey, swt);
       }
     }
-    __threadfence_block();
-    __syncthreads();
-  }
-  for (int i = tid; i < T * K; i += SMALL_NT) {
-    ssel[i] = a.sel[i];
-    swt[i] = a.wt[i];
-    if (a.hist) atomicAdd(&a.hist[a.sel[i]], 1u);
+  } else {
+    for (int i = tid; i < n; i += SMALL_NT) {
+      skey[i] = a.sel[i];
+      swt[i] = a.wt[i];
+    }
   }
   __syncthreads();
-  // Thread e: its count and, in token order, its rows.
-  const int e = tid;
-  int c = 0;
-  if (e < E)
-    for (int i = 0; i < T * K; ++i) c += ssel[i] == e;
-  const int nt = (c + a.tile_rows - 1) / a.tile_rows;
-  int tot_rows, tot_tiles;
-  const int row = block_exclusive_scan<SMALL_NT>(c, &tot_rows, lds[0]);
-  const int tile = block_exclusive_scan<SMALL_NT>(nt, &tot_tiles, lds[1]);
-  if (e < E && c > 0) {
-    int p = row;
-    for (int t = 0; t < T; ++t) {
-      int below = 0;
-      for (int j = 0; j < K; ++j) below += ssel[t * K + j] < e;
-      for (int j = 0; j < K; ++j)
-        if (ssel[t * K + j] == e) {
-          a.eidx[p] = t;
-          a.ewt[p] = swt[t * K + j];
-          a.row_expert[p] = e;
-          a.pidx[size_t(t) * K + below++] = p;
-          ++p;
-        }
-    }
-    for (int i = 0; i < nt && tile + i < a.max_tiles; ++i)
-      a.lt[tile + i] = Exl3Tile{e, row + i * a.tile_rows, min(a.tile_rows, c - i * a.tile_rows)};
+  const int i = tid;
+  const bool live = i < n;
+  int e = 0, t = 0, j = 0;
+  float w = 0.0f;
+  if (live) {
+    e = skey[i];
+    w = swt[i];
+    t = i / K;
+    j = i % K;
+    if (a.hist) atomicAdd(&a.hist[e], 1u);
   }
+  __syncthreads();
+  if (live) skey[i] = (e * T + t) * K + j;
+  __syncthreads();
+  const int mykey = (e * T + t) * K + j, lo = e * T * K, hi = (e + 1) * T * K;
+  int rank = 0, off = 0, cnt = 0;
+  if (live) {
+    int q = 0;
+    for (; q + 4 <= n; q += 4) {  // the same address in every lane: broadcast reads, four keys at a time
+      const int4 k4 = *reinterpret_cast<const int4*>(&skey[q]);
+      const int kk[4] = {k4.x, k4.y, k4.z, k4.w};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        rank += kk[u] < mykey;
+        off += kk[u] < lo;
+        cnt += kk[u] >= lo && kk[u] < hi;
+      }
+    }
+    for (; q < n; ++q) {
+      const int kq = skey[q];
+      rank += kq < mykey;
+      off += kq < lo;
+      cnt += kq >= lo && kq < hi;
+    }
+  }
+  int below = 0;  // token t's picks ordered before this one (expert, then selection order)
+  if (live)
+    for (int q = 0; q < K; ++q) {
+      const int kq = skey[t * K + q];
+      below += kq < mykey;
+    }
+  const int p = rank;
+  __shared__ int srow_e[SMALL_NT], srow_left[SMALL_NT];
+  if (live) {
+    a.eidx[p] = t;
+    a.ewt[p] = w;
+    a.row_expert[p] = e;
+    a.pidx[size_t(t) * K + below] = p;
+    srow_e[p] = e;
+    // rows of the expert's run from here, or 0 when this row does not start a tile
+    srow_left[p] = (p - off) % a.tile_rows == 0 ? cnt - (p - off) : 0;
+  }
+  __syncthreads();
+  // Now thread r stands for pair row r: tiles are numbered in row order.
+  const int r = tid, left = r < n ? srow_left[r] : 0;
+  int ntiles;
+  const int tile = block_exclusive_scan<SMALL_NT>(left > 0 ? 1 : 0, &ntiles, lds);
+  if (left > 0 && tile < a.max_tiles) a.lt[tile] = Exl3Tile{srow_e[r], r, min(a.tile_rows, left)};
   if (tid == 0) {
     a.plan->P = a.P;
-    a.plan->remote0 = tot_rows;
-    a.plan->n_local_tiles = min(tot_tiles, a.max_tiles);
+    a.plan->remote0 = n;
+    a.plan->n_local_tiles = min(ntiles, a.max_tiles);
     a.plan->n_remote_tiles = 0;
     a.plan->n_remote_tokens = 0;
   }
@@ -438,7 +501,8 @@ void moe_scatter(const int32_t* sel, const float* wt, int T, int K, const int32_
 void moe_dispatch_small(const MoeSmallArgs& a, hipStream_t st) {
   if (a.T <= 0) return;
   if (a.T > kMoeSmallMaxTokens || a.K <= 0 || a.K > kMaxK) throw std::runtime_error("moe_dispatch_small: T <= 32, K <= 8");
-  if (a.E <= 0 || a.E > SMALL_NT) throw std::runtime_error("moe_dispatch_small: E in [1, 1024]");
+  if (a.E <= 0 || a.E > 1024) throw std::runtime_error("moe_dispatch_small: E in [1, 1024]");
+  if (a.P != a.T * a.K) throw std::runtime_error("moe_dispatch_small: P != T * K");
   if (a.tile_rows <= 0) throw std::runtime_error("moe_dispatch_small: tile_rows");
   if (a.remote || a.qin || a.x_dst || a.q_dst || a.req_flag || a.plan_dst)
     throw std::runtime_error("moe_dispatch_small: remote experts are not supported on one GPU");

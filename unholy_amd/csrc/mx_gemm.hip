@@ -11,10 +11,10 @@ namespace unholy::kernels {
 
 using namespace uh;
 
-void launch_mx_gemm(const MxGemvArgs& a0, int ntiles, bool abf16, hipStream_t st) {
+void launch_mx_gemm(const MxGemvArgs& a0, int ntiles, int amode, hipStream_t st) {
   MxGemvArgs a = a0;
   a.rows_cap = 16;
-  launch_mx_gemv(a, ntiles, abf16, st);
+  launch_mx_gemv(a, ntiles, amode, st);
 }
 
 void launch_fp8_gemm(const Fp8GemmArgs& a, hipStream_t st) { launch_fp8_skinny(a, st); }
@@ -58,7 +58,7 @@ void mx_grouped_gemm(const bf16* xa, int K, const Exl3Tile* tiles, int ntiles, c
                      const uint8_t* const* w_tab2, const uint8_t* const* s_tab2, bf16* out2, int) {
   launch_mx_gemm(gemm_args(xa, nullptr, nullptr, K, tiles, w_tab, s_tab, out, ldo, N, ntiles_dev, w_tab2, s_tab2, out2,
                            MxGlu{}),
-                 ntiles, true, st);
+                 ntiles, 1, st);
 }
 
 void mx_grouped_gemm_q(const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles, int ntiles,
@@ -66,7 +66,7 @@ void mx_grouped_gemm_q(const uint8_t* q, const uint8_t* qs, int K, const Exl3Til
                        hipStream_t st, const int* ntiles_dev, const uint8_t* const* w_tab2,
                        const uint8_t* const* s_tab2, bf16* out2, int, const MxGlu& glu) {
   launch_mx_gemm(gemm_args(nullptr, q, qs, K, tiles, w_tab, s_tab, out, ldo, N, ntiles_dev, w_tab2, s_tab2, out2, glu),
-                 ntiles, false, st);
+                 ntiles, 0, st);
 }
 
 void mx_grouped_gemm_glu(const bf16* xa, int K, const Exl3Tile* tiles, int ntiles, const uint8_t* const* w1_tab,
@@ -76,7 +76,7 @@ void mx_grouped_gemm_glu(const bf16* xa, int K, const Exl3Tile* tiles, int ntile
   if (!glu.s_tab || !glu.row_expert) throw std::runtime_error("mx_grouped_gemm_glu: glu");
   launch_mx_gemm(gemm_args(xa, nullptr, nullptr, K, tiles, w1_tab, s1_tab, nullptr, N, N, ntiles_dev, w3_tab, s3_tab,
                            nullptr, glu),
-                 ntiles, true, st);
+                 ntiles, 1, st);
 }
 
 }  // namespace unholy::kernels

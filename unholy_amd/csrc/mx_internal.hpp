@@ -15,6 +15,8 @@ struct MxGemvArgs {
   const uint8_t* aq;
   const uint8_t* as;
   const uint16_t* xa;
+  const int32_t* x_rows;  // activation mode 2: pair row r reads token row x_rows[r] of x (xa, row stride ldx)
+  int ldx;
   int K, N, ldo;
   const Exl3Tile* tiles;
   const int* ntiles_dev;
@@ -32,8 +34,9 @@ struct MxGemvArgs {
   float limit;
 };
 
-void launch_mx_gemv(const MxGemvArgs& a, int ntiles, bool abf16, hipStream_t st);
-void launch_mx_gemm(const MxGemvArgs& a, int ntiles, bool abf16, hipStream_t st);
+// amode: 0 e4m3 codes + scales, 1 fake-quantized bf16 rows, 2 raw bf16 token rows (act_quant in the kernel).
+void launch_mx_gemv(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st);
+void launch_mx_gemm(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st);
 void launch_mx_transform(int mode, const uint16_t* x, int ldx, const int32_t* x_rows, const uint16_t* u,
                          const float* w, float limit, const int32_t* row_expert, const uint8_t* const* s_tab,
                          uint16_t* out, uint8_t* q, uint8_t* qs, int K, int P, hipStream_t st);

@@ -88,8 +88,10 @@ unsigned transform_blocks(int P, int K) { return unsigned(std::min<size_t>((size
 // the matching activation inputs. The MFMA accumulates in fp32 with exact products; no cross-lane reductions.
 constexpr int GV_WAVES = 8, GV_NT = 64 * GV_WAVES, GV_PAD = 16, GV_MAXROWS = 16, GV_PF = 4;
 
+// AM: activation source -- 0: e4m3 codes + e8m0 scales (aq, as); 1: fake-quantized bf16 rows (xa), codes recovered
+// exactly; 2: raw bf16 token rows x[x_rows[r]] quantized here with the reference's act_quant (mx_xform_in_fp8 fused).
 // OCC: waves per SIMD the register budget is sized for (4: two workgroups per CU).
-template <int NP, bool GLU, bool ABF16, int OCC>
+template <int NP, bool GLU, int AM, int OCC>
 __global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(OCC))) void mx_gemv_kernel(MxGemvArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   if (a.ntiles_dev && int(blockIdx.y) >= *a.ntiles_dev) return;
@@ -133,7 +135,7 @@ __global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(OCC))) vo
 #pragma unroll
       for (int i = 0; i < GV_PF; ++i) load_step(min(i, KS - 1), i);  // K < 128 * GV_PF: re-read the last step
     __syncthreads();
-    if constexpr (ABF16) {
+    if constexpr (AM != 0) {
       // 8 values per thread; 16 consecutive threads hold one 128-block (K / 8 is a multiple of 16).
       const int total = M * (K / 8);
       for (int base = 0; base < total; base += GV_NT) {
@@ -142,7 +144,9 @@ __global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(OCC))) vo
         float v[8];
         float am = 0.0f;
         if (valid) {
-          const uint4 raw = *reinterpret_cast<const uint4*>(a.xa + (row0 + m) * size_t(K) + c);
+          const uint16_t* src = AM == 1 ? a.xa + (row0 + m) * size_t(K)
+                                        : a.xa + size_t(a.x_rows ? a.x_rows[row0 + m] : int(row0 + m)) * a.ldx;
+          const uint4 raw = *reinterpret_cast<const uint4*>(src + c);
           const uint32_t r4[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
@@ -154,13 +158,24 @@ __global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(OCC))) vo
         }
         am = group_max<16>(am);
         if (valid) {
-          const uint8_t se = uint8_t(min(max(int(exact_fp8_scale(am)), 1), 254));
-          const float inv = e8m0_to_f32(uint8_t(254 - se));  // 2^(127 - se), exact
+          uint8_t se;
           uint32_t lo = 0, hi = 0;
+          if constexpr (AM == 1) {
+            se = uint8_t(min(max(int(exact_fp8_scale(am)), 1), 254));
+            const float inv = e8m0_to_f32(uint8_t(254 - se));  // 2^(127 - se), exact
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            lo |= uint32_t(f32_to_e4m3(v[t] * inv)) << (8 * t);
-            hi |= uint32_t(f32_to_e4m3(v[t + 4] * inv)) << (8 * t);
+            for (int t = 0; t < 4; ++t) {
+              lo |= uint32_t(f32_to_e4m3(v[t] * inv)) << (8 * t);
+              hi |= uint32_t(f32_to_e4m3(v[t + 4] * inv)) << (8 * t);
+            }
+          } else {
+            const Fp8Block blk = fp8_block_scale(am);
+            se = blk.se;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              lo |= uint32_t(fp8_code(v[t], blk.sc)) << (8 * t);
+              hi |= uint32_t(fp8_code(v[t + 4], blk.sc)) << (8 * t);
+            }
           }
           *reinterpret_cast<uint2*>(sA + m * ldA + c) = make_uint2(lo, hi);
           if ((c & 127) == 0) sS[m * KS + c / 128] = se;
@@ -356,10 +371,10 @@ int gemv_occ() {
   return v;
 }
 
-template <int NP, bool GLU, bool ABF16>
+template <int NP, bool GLU, int AM>
 void launch_gemv_t(const MxGemvArgs& a, int ntiles, hipStream_t st) {
   const size_t lds = size_t(a.rows_cap) * (a.K + GV_PAD) + size_t(a.rows_cap) * (a.K / 128);
-  auto* kern = gemv_occ() >= 4 ? &mx_gemv_kernel<NP, GLU, ABF16, 4> : &mx_gemv_kernel<NP, GLU, ABF16, 2>;
+  auto* kern = gemv_occ() >= 4 ? &mx_gemv_kernel<NP, GLU, AM, 4> : &mx_gemv_kernel<NP, GLU, AM, 2>;
   set_lds_limit(kern, lds);
   const dim3 grid(cdiv(size_t(a.N) / 16, GV_WAVES), unsigned(ntiles), 1);
   kern<<<grid, GV_NT, lds, st>>>(a);
@@ -369,18 +384,21 @@ void launch_gemv_t(const MxGemvArgs& a, int ntiles, hipStream_t st) {
 }  // namespace
 
 // ---- internal launchers (mx_internal.hpp) -----------------------------------------------------------------------------
-void launch_mx_gemv(const MxGemvArgs& a, int ntiles, bool abf16, hipStream_t st) {
+void launch_mx_gemv(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st) {
   if (ntiles <= 0) return;
   if (a.K % 128 || a.N % 16 || a.K <= 0 || a.N <= 0) throw std::runtime_error("mx_grouped_gemv: K % 128 or N % 16");
   if (a.rows_cap < 1 || a.rows_cap > GV_MAXROWS) throw std::runtime_error("mx_grouped_gemv: rows_cap");
   const bool np2 = a.w_tab[1] != nullptr, glu = a.hh || a.hq;
   if (glu && (!np2 || a.N % 128)) throw std::runtime_error("mx_grouped_gemv: glu needs two projections, N % 128");
   if (glu && a.hq && !a.hs) throw std::runtime_error("mx_grouped_gemv: glu hq without hs");
-  if (abf16 ? !a.xa : (!a.aq || !a.as)) throw std::runtime_error("mx_grouped_gemv: null activations");
+  if (amode ? !a.xa : (!a.aq || !a.as)) throw std::runtime_error("mx_grouped_gemv: null activations");
+  if (amode == 2 && a.ldx % 8) throw std::runtime_error("mx_grouped_gemv: ldx % 8 (16-byte row loads)");
   if (!glu && ((!a.out[0] && !a.out32) || (np2 && !a.out[1]))) throw std::runtime_error("mx_grouped_gemv: null output");
   if (!a.tiles) throw std::runtime_error("mx_grouped_gemv: null tiles");
-#define UH_GV(NP, GLU)                                             \
-  (abf16 ? launch_gemv_t<NP, GLU, true>(a, ntiles, st) : launch_gemv_t<NP, GLU, false>(a, ntiles, st))
+#define UH_GV(NP, GLU)                                                       \
+  (amode == 2   ? launch_gemv_t<NP, GLU, 2>(a, ntiles, st)                     \
+   : amode == 1 ? launch_gemv_t<NP, GLU, 1>(a, ntiles, st)                     \
+                : launch_gemv_t<NP, GLU, 0>(a, ntiles, st))
   if (glu) UH_GV(2, true);
   else if (np2) UH_GV(2, false);
   else UH_GV(1, false);
@@ -514,7 +532,7 @@ void mx_grouped_gemv(const bf16* xa, int K, const Exl3Tile* tiles, int ntiles, c
   if ((glu.hh || glu.hq) && ldo != N) throw std::runtime_error("mx_grouped_gemv: glu shape (ldo != N)");
   launch_mx_gemv(gemv_args(xa, nullptr, nullptr, K, tiles, w_tab, s_tab, out, ldo, N, ntiles_dev, w_tab2, s_tab2,
                            out2, max_rows, glu),
-                 ntiles, true, st);
+                 ntiles, 1, st);
 }
 
 void mx_grouped_gemv_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles, int ntiles,
@@ -523,7 +541,7 @@ void mx_grouped_gemv_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const 
   MxGemvArgs a = gemv_args(nullptr, q, qs, K, tiles, w_tab, s_tab, nullptr, ldo, N, ntiles_dev, nullptr, nullptr,
                            nullptr, max_rows, MxGlu{});
   a.out32 = out;
-  launch_mx_gemv(a, ntiles, false, st);
+  launch_mx_gemv(a, ntiles, 0, st);
 }
 
 void mx_grouped_gemv_q(const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles, int ntiles,
@@ -533,7 +551,19 @@ void mx_grouped_gemv_q(const uint8_t* q, const uint8_t* qs, int K, const Exl3Til
   if ((glu.hh || glu.hq) && ldo != N && (out || out2)) throw std::runtime_error("mx_grouped_gemv_q: glu shape");
   launch_mx_gemv(gemv_args(nullptr, q, qs, K, tiles, w_tab, s_tab, out, ldo, N, ntiles_dev, w_tab2, s_tab2, out2,
                            max_rows, glu),
-                 ntiles, false, st);
+                 ntiles, 0, st);
+}
+
+void mx_grouped_gemv_x(const bf16* x, int ldx, const int32_t* x_rows, int K, const Exl3Tile* tiles, int ntiles,
+                       const uint8_t* const* w_tab, const uint8_t* const* s_tab, bf16* out, int ldo, int N,
+                       hipStream_t st, const int* ntiles_dev, const uint8_t* const* w_tab2,
+                       const uint8_t* const* s_tab2, bf16* out2, int max_rows, const MxGlu& glu) {
+  if ((glu.hh || glu.hq) && ldo != N && (out || out2)) throw std::runtime_error("mx_grouped_gemv_x: glu shape");
+  MxGemvArgs a = gemv_args(x, nullptr, nullptr, K, tiles, w_tab, s_tab, out, ldo, N, ntiles_dev, w_tab2, s_tab2, out2,
+                           max_rows, glu);
+  a.x_rows = x_rows;
+  a.ldx = ldx;
+  launch_mx_gemv(a, ntiles, 2, st);
 }
 
 }  // namespace unholy::kernels

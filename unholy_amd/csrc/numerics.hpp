@@ -87,6 +87,25 @@ __device__ __forceinline__ float group_max(float v) {
   return v;
 }
 
+// Uniform wave64 reductions of 32-bit unsigned values through DPP (pairs, quads, half-rows, rows) and four lane
+// reads, instead of a shuffle per level: a few cycles per level rather than an LDS round trip.
+template <bool MAX>
+__device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v) {
+  const auto op = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
+  v = op(v, uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), 0xB1, 0xf, 0xf, false)));   // quad_perm [1,0,3,2]
+  v = op(v, uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), 0x4E, 0xf, 0xf, false)));   // quad_perm [2,3,0,1]
+  v = op(v, uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), 0x141, 0xf, 0xf, false)));  // row_half_mirror
+  v = op(v, uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), 0x140, 0xf, 0xf, false)));  // row_mirror
+  const uint32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+  const uint32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+  return op(op(r0, r1), op(r2, r3));
+}
+// A float's bits mapped so that unsigned order is float order.
+__device__ __forceinline__ uint32_t orderable(float f) {
+  const uint32_t b = __float_as_uint(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
 // The reference's activation fake quantization of one value given its block's amax (ref_elem.hip:32-37):
 // amax floored at 1e-4, e8m0 scale 2^ceil(log2(amax / 448)), e4m3 RNE of the clamped quotient.
 struct Fp8Block {
