@@ -112,6 +112,11 @@ void mx_grouped_gemv_x(const bf16* x, int ldx, const int32_t* x_rows, int K, con
                        hipStream_t st, const int* ntiles_dev = nullptr, const uint8_t* const* w_tab2 = nullptr,
                        const uint8_t* const* s_tab2 = nullptr, bf16* out2 = nullptr, int max_rows = kMxGemvTileRows,
                        const MxGlu& glu = {});
+// mx_xform_in_fp8 + mx_grouped_gemm_q in one launch (the workgroup quantizes its tile's token rows while staging).
+void mx_grouped_gemm_x(const bf16* x, int ldx, const int32_t* x_rows, int K, const Exl3Tile* tiles, int ntiles,
+                       const uint8_t* const* w_tab, const uint8_t* const* s_tab, bf16* out, int ldo, int N,
+                       hipStream_t st, const int* ntiles_dev = nullptr, const uint8_t* const* w_tab2 = nullptr,
+                       const uint8_t* const* s_tab2 = nullptr, bf16* out2 = nullptr, const MxGlu& glu = {});
 // The GEMV with fp32 outputs (no bf16 rounding): for accuracy checks against an fp64 oracle.
 void mx_grouped_gemv_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles, int ntiles,
                               const uint8_t* const* w_tab, const uint8_t* const* s_tab, float* out, int ldo, int N,

@@ -242,3 +242,75 @@ def test_gemv_x_fused_quant_is_bit_identical():
         outs.append((g.download((P, N), np.uint16), hq.download((P, N), np.uint8), hs.download((P, N // 128), np.uint8)))
     for a, b in zip(*outs):
         assert np.array_equal(a, b)
+
+
+def _gemm_case(rng, rows, E, K, N):
+    tiles, row_expert, r0 = [], [], 0
+    for e, c in enumerate(rows):
+        for i in range(0, c, 128):
+            tiles.append([e, r0 + i, min(128, c - i)])
+        row_expert += [e] * c
+        r0 += c
+    return np.array(tiles, np.int32), np.array(row_expert, np.int32), sum(rows)
+
+
+@pytest.mark.parametrize("amode", ["q", "bf16", "x"])
+def test_grouped_gemm_prefill_tiles(amode):
+    """The 128-row MFMA GEMM: tiles of 1..128 rows (and one expert split over two tiles), w1 and w3 in two launches
+    (no epilogue) and in one launch with the SwiGLU epilogue, against the oracle; fp32 outputs against fp64."""
+    rng = np.random.default_rng(33)
+    E, K, N, T, limit = 4, 1024, 256, 300, 10.0
+    rows = [96, 1, 200, 37]
+    tiles, row_expert, P = _gemm_case(rng, rows, E, K, N)
+    x = randn_bf16(rng, (T, K), 2.0)
+    x_rows = rng.integers(0, T, P).astype(np.int32)
+    q, qs = oracle.act_quant_fp8(x[x_rows])
+    w1, w3 = _make_experts(rng, E, N, K), _make_experts(rng, E, N, K)
+    b1, t1 = _expert_tables(w1, ("w", "s"))
+    b3, t3 = _expert_tables(w3, ("w", "s"))
+    rw = rng.random(P).astype(np.float32)
+    g_ref = np.zeros((P, N), np.uint16)
+    g64 = np.zeros((P, N))
+    for e, a0, c in tiles:
+        w, s_ = oracle.unrepack(w1[e]["w"], w1[e]["s"], N, K)
+        g_ref[a0:a0 + c] = oracle.gemm_a8w4(q[a0:a0 + c], qs[a0:a0 + c], w, s_, N)[0]
+        g64[a0:a0 + c] = oracle.gemm_a8w4_f64(q[a0:a0 + c], qs[a0:a0 + c], w, s_, N)
+    dq, dqs, dt, de, drw = dev(q), dev(qs), dev(tiles), dev(row_expert), dev(rw)
+    dx, dr = dev(x), dev(x_rows)
+    g, u = DeviceBuffer(P * N * 2), DeviceBuffer(P * N * 2)
+    nt = len(tiles)
+    if amode == "q":
+        call("uh_mx_grouped_gemm_q", dq, dqs, K, dt, nt, t1["w"], t1["s"], g, N, N, None, None, t3["w"], t3["s"], u, 128,
+             None, None, None, None, None, None, 0.0)
+    elif amode == "bf16":
+        xa = dev(oracle.fake_quant_fp8(x[x_rows]))
+        call("uh_mx_grouped_gemm", xa, K, dt, nt, t1["w"], t1["s"], g, N, N, None, None, t3["w"], t3["s"], u, 128)
+    else:
+        call("uh_mx_grouped_gemm_x", dx, K, dr, K, dt, nt, t1["w"], t1["s"], g, N, N, None, None, t3["w"], t3["s"], u,
+             None, None, None, None, None, None, 0.0)
+    gg, uu = g.download((P, N), np.uint16), u.download((P, N), np.uint16)
+    mr = max_rel(from_bf16(gg), from_bf16(g_ref))
+    print(f"gemm {amode}: max_rel {mr:.3e} bit-identical {np.mean(gg == g_ref):.4f}")
+    assert mr <= 1e-2
+    # the SwiGLU epilogue in one launch: its g / u, and hh / hq / hs against the transform of those
+    hq, hs, hh, g2, u2 = DeviceBuffer(P * N), DeviceBuffer(P * N // 128), DeviceBuffer(P * N * 2), DeviceBuffer(P * N * 2), DeviceBuffer(P * N * 2)
+    if amode == "q":
+        call("uh_mx_grouped_gemm_q", dq, dqs, K, dt, nt, t1["w"], t1["s"], g2, N, N, None, None, t3["w"], t3["s"], u2,
+             128, drw, de, t1["s"], hh, hq, hs, limit)
+    elif amode == "bf16":
+        call("uh_mx_grouped_gemm_glu", xa, K, dt, nt, t1["w"], t1["s"], t3["w"], t3["s"], N, drw, de, t1["s"], hh,
+             limit, None, None)
+    else:
+        call("uh_mx_grouped_gemm_x", dx, K, dr, K, dt, nt, t1["w"], t1["s"], g2, N, N, None, None, t3["w"], t3["s"], u2,
+             drw, de, t1["s"], hh, hq, hs, limit)
+    synchronize()
+    if amode != "bf16":
+        assert np.array_equal(g2.download((P, N), np.uint16), gg) and np.array_equal(u2.download((P, N), np.uint16), uu)
+    h_ref = oracle.fake_quant_fp8(oracle.swiglu(gg, uu, rw, limit))
+    hgot = hh.download((P, N), np.uint16)
+    print(f"gemm glu {amode}: hh bit-identical {np.mean(hgot == h_ref):.6f}")
+    assert np.mean(hgot == h_ref) > 0.999 and max_rel(from_bf16(hgot), from_bf16(h_ref)) <= 1e-2
+    if amode != "bf16":
+        codes, scales = hq.download((P, N), np.uint8), hs.download((P, N // 128), np.uint8)
+        deq = oracle.e4m3_to_f32(codes) * np.ldexp(1.0, scales.astype(np.int32) - 127).repeat(128, axis=1)
+        assert np.array_equal(deq.astype(np.float32), from_bf16(hgot))

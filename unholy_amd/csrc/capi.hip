@@ -265,6 +265,18 @@ int uh_mx_grouped_gemv_x(const uint16_t* x, int ldx, const int32_t* x_rows, int 
                          s_tab2, out2, max_rows, glu);
   });
 }
+int uh_mx_grouped_gemm_x(const uint16_t* x, int ldx, const int32_t* x_rows, int K, const int32_t* tiles, int ntiles,
+                         const uint8_t* const* w_tab, const uint8_t* const* s_tab, uint16_t* out, int ldo, int N,
+                         void* st, const int* ntiles_dev, const uint8_t* const* w_tab2, const uint8_t* const* s_tab2,
+                         uint16_t* out2, const float* glu_w, const int32_t* glu_row_expert,
+                         const uint8_t* const* glu_s_tab, uint16_t* glu_hh, uint8_t* glu_hq, uint8_t* glu_hs,
+                         float glu_limit) {
+  return guard([&] {
+    k::MxGlu glu{glu_w, glu_row_expert, glu_s_tab, glu_hh, glu_limit, nullptr, glu_hq, glu_hs};
+    k::mx_grouped_gemm_x(x, ldx, x_rows, K, T3(tiles), ntiles, w_tab, s_tab, out, ldo, N, S(st), ntiles_dev, w_tab2,
+                         s_tab2, out2, glu);
+  });
+}
 int uh_mx_grouped_gemv_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const int32_t* tiles, int ntiles,
                                 const uint8_t* const* w_tab, const uint8_t* const* s_tab, float* out, int ldo, int N,
                                 void* st, const int* ntiles_dev, int max_rows) {
@@ -468,7 +480,7 @@ int uh_mx_moe_forward_ev(const uint16_t* x, const float* logits, int T, int K, i
       mark(3);
       k::mx_grouped_gemv_q(w.hq, w.hs, I, tiles, w.max_tiles, t(2, 0), t(2, 1), w.pair_out, D, D, st, ntd, nullptr,
                            nullptr, nullptr, w.tile_rows);
-    } else {
+    } else {  // quantized once (each tile's rows are read by all its column blocks), then the fp8 GEMM
       k::mx_xform_in_fp8(x, D, w.row_expert, t(0, 1), w.xq, w.xs, P, D, st, w.eidx);
       mark(2);
       k::mx_grouped_gemm_q(w.xq, w.xs, D, tiles, w.max_tiles, t(0, 0), t(0, 1), nullptr, I, I, st, ntd, t(1, 0), t(1, 1),

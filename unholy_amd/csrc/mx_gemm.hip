@@ -1,4 +1,11 @@
-// Grouped GEMM for prefill tiles (rows > 16 per tile) and the dense fp8 GEMM dispatcher.
+// Grouped MXFP4 GEMM for prefill tiles (up to 128 pair rows of one expert), and the dense fp8 GEMM dispatcher.
+//
+// Workgroup = one tile x 128 output columns (x 2 projections for w1 / w3 with the SwiGLU epilogue). Each wave owns a
+// 64-row x 64-column block. Per 128-input stage the tile's activation rows are staged into LDS as bf16 (double
+// buffered, the next stage's global loads in flight during the current stage's MFMAs), while every wave streams its
+// own weight columns from HBM straight into registers (one stage ahead), dequantizes them exactly to bf16 and issues
+// 32x32x16 bf16 MFMAs with fp32 accumulation. Weight columns are read from HBM once per tile; the activation tile is
+// shared by the tile's column blocks, which the block mapping keeps on one XCD (one L2).
 #include <algorithm>
 
 #include "common.hpp"
@@ -11,10 +18,368 @@ namespace unholy::kernels {
 
 using namespace uh;
 
-void launch_mx_gemm(const MxGemvArgs& a0, int ntiles, int amode, hipStream_t st) {
-  MxGemvArgs a = a0;
-  a.rows_cap = 16;
-  launch_mx_gemv(a, ntiles, amode, st);
+namespace {
+
+typedef float v16f_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ v16f_t mfma32_bf16(bf16x8 a, bf16x8 b, v16f_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+constexpr int GM_BM = 128, GM_KS = 128, GM_LDA = GM_KS + 8;  // LDS row: 128 bf16 + 16 bytes of padding
+constexpr size_t GM_ABUF = size_t(GM_BM) * GM_LDA * 2;       // one stage of A in LDS (bytes)
+
+// The LDS A stage: row r holds inputs s*128 .. +127 of pair row row0 + r as bf16 (zeros past the tile's rows).
+// Work item c of NT threads: row c / 8, inputs (c % 8) * 16 .. + 15 (16 values: 16 fp8 codes or 32 bytes of bf16).
+template <int AM, int NT>
+struct AStage {
+  static constexpr int CH = GM_BM * 8 / NT;  // items per thread
+  v4i raw[CH][AM == 0 ? 1 : 2];
+  uint32_t sc[CH];
+
+  // No branches around the loads (rows past the tile re-read its last row and are zeroed in store()): divergent
+  // control flow here would make the compiler drain every outstanding load, the weight prefetch included.
+  uint32_t rowoff[CH];  // element offset of each item's row (loop-invariant: no dependent loads in the stage loop)
+
+  __device__ __forceinline__ void rows(const MxGemvArgs& a, size_t row0, int M, int tid) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int r = min((tid + i * NT) / 8, M - 1);
+      rowoff[i] = AM == 2 ? uint32_t(a.x_rows ? a.x_rows[row0 + r] : int(row0 + r)) * uint32_t(a.ldx)
+                          : uint32_t(row0 + r) * uint32_t(a.K);
+    }
+  }
+
+  __device__ __forceinline__ void load(const MxGemvArgs& a, int s, int tid) {
+    const auto qbase = as_global(a.aq + size_t(s) * GM_KS);  // AM 0 (uniform per stage)
+    const auto xbase = as_global(a.xa + size_t(s) * GM_KS);  // AM 1, 2
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const uint32_t part = uint32_t((tid + i * NT) % 8);
+      if constexpr (AM == 0) {
+        raw[i][0] = *reinterpret_cast<gptr<v4i>>(qbase + (rowoff[i] + part * 16));
+        sc[i] = *(as_global(a.as) + (rowoff[i] / uint32_t(128) + uint32_t(s)));  // (row * K) / 128 = row * K/128
+      } else {
+        raw[i][0] = *reinterpret_cast<gptr<v4i>>(xbase + (rowoff[i] + part * 16));
+        raw[i][1] = *reinterpret_cast<gptr<v4i>>(xbase + (rowoff[i] + part * 16 + 8));
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(uint8_t* buf, int M, int tid) const {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int c = tid + i * NT, r = c / 8, part = c % 8;
+      uint4 o0 = make_uint4(0, 0, 0, 0), o1 = o0;
+      if constexpr (AM == 2) {  // act_quant of the raw row's 128-block: the 8 items of a row are 8 adjacent lanes
+        float v[16], am = 0.0f;
+        const uint32_t w[8] = {uint32_t(raw[i][0][0]), uint32_t(raw[i][0][1]), uint32_t(raw[i][0][2]),
+                               uint32_t(raw[i][0][3]), uint32_t(raw[i][1][0]), uint32_t(raw[i][1][1]),
+                               uint32_t(raw[i][1][2]), uint32_t(raw[i][1][3])};
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          v[2 * q] = __uint_as_float(w[q] << 16);
+          v[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+        }
+        if (r < M)
+#pragma unroll
+          for (int q = 0; q < 16; ++q) am = fmaxf(am, fabsf(v[q]));
+        am = group_max<8>(am);
+        if (r < M) {
+          const Fp8Block blk = fp8_block_scale(am);
+          uint32_t ow[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q)
+            ow[q] = uint32_t(f32_to_bf16(e4m3_to_f32(fp8_code(v[2 * q], blk.sc)) * blk.sc)) |
+                    uint32_t(f32_to_bf16(e4m3_to_f32(fp8_code(v[2 * q + 1], blk.sc)) * blk.sc)) << 16;
+          o0 = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+          o1 = make_uint4(ow[4], ow[5], ow[6], ow[7]);
+        }
+      } else if (r < M) {
+        if constexpr (AM == 0) {
+          const float s = e8m0_to_f32(uint8_t(sc[i]));
+          const bf16x8 lo = fp8x8_to_bf16(uint32_t(raw[i][0][0]), uint32_t(raw[i][0][1]), s);
+          const bf16x8 hi = fp8x8_to_bf16(uint32_t(raw[i][0][2]), uint32_t(raw[i][0][3]), s);
+          o0 = __builtin_bit_cast(uint4, lo);
+          o1 = __builtin_bit_cast(uint4, hi);
+        } else {
+          o0 = __builtin_bit_cast(uint4, raw[i][0]);
+          o1 = __builtin_bit_cast(uint4, raw[i][1]);
+        }
+      }
+      uint8_t* dst = buf + (size_t(r) * GM_LDA + part * 16) * 2;
+      *reinterpret_cast<uint4*>(dst) = o0;
+      *reinterpret_cast<uint4*>(dst + 16) = o1;
+    }
+  }
+};
+
+// A wave's weight columns for one stage: 2 column blocks x 2 slabs of 64 inputs, 16 code bytes + 1 scale byte each.
+struct BStage {
+  v4i q[2][2];
+  uint32_t s[2][2];
+};
+
+// LDS barrier that does not wait for outstanding global loads (the next stage's prefetch stays in flight).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+}
+
+// NP 1: 4 waves = 2 row halves x 2 column halves (128 x 128); NP 2: 8 waves, the same for w1 (waves 0-3) and
+// w3 (waves 4-7), with the SwiGLU + fake-quantization epilogue over the workgroup's 128 columns (one quant block).
+template <int NP, int AM>
+__global__ __launch_bounds__(256 * NP) void mx_gemm_kernel(MxGemvArgs a) {
+  constexpr int NT = 256 * NP;
+  extern __shared__ __align__(16) uint8_t smem[];
+  // XCD-aware mapping: linear block ids go round-robin over the 8 XCDs; consecutive logical ids (the column blocks
+  // of one tile, which read the same activation rows) are given to one XCD.
+  const int nbx = gridDim.x, total = gridDim.x * gridDim.y, lin = blockIdx.y * nbx + blockIdx.x;
+  const int logical = total % 8 == 0 ? (lin % 8) * (total / 8) + lin / 8 : lin;
+  const int bx = logical % nbx, by = logical / nbx;
+  if (a.ntiles_dev && by >= *a.ntiles_dev) return;
+  const Exl3Tile tile = a.tiles[by];
+  if (tile.rows <= 0) return;
+  const uint8_t* wps[NP];
+  const uint8_t* sps[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    wps[p] = a.w_tab[p][tile.expert];
+    sps[p] = a.s_tab[p][tile.expert];
+    if (!wps[p] || !sps[p]) return;
+  }
+  const int K = a.K, N = a.N, KS = K / GM_KS, ntn = N / 16;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+  const int rh = wave & 1, chh = (wave >> 1) & 1, p = NP == 2 ? (wave >> 2) : 0;
+  const uint8_t* wp = NP == 2 && p ? wps[NP - 1] : wps[0];
+  const uint8_t* sp = NP == 2 && p ? sps[NP - 1] : sps[0];
+  const int col0 = bx * 128 + chh * 64;  // the wave's first column
+  // Per-lane weight offsets (column col0 + cb * 32 + l32, input half h of each 64-input slab).
+  uint32_t cofs[2], sofs[2];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const int n = col0 + cb * 32 + l32;
+    cofs[cb] = uint32_t((n / 16) * 512 + (n % 16) * 32 + h * 16);
+    sofs[cb] = uint32_t((n / 16) * 32 + (n % 16) * 2 + h);
+  }
+  const size_t cslab = size_t(ntn) * 512, sslab = size_t(ntn) * 32;
+  // The slab's base is uniform (scalar registers); the per-lane offset is loop-invariant: scalar-base loads with
+  // no per-load address arithmetic and no 64-bit pointers kept live across the loop.
+  const auto load_b = [&](BStage& b, int s) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const size_t kt = size_t(2 * s + j);
+      const auto wbase = as_global(wp + kt * cslab);
+      const auto sbase = as_global(sp + kt * sslab);
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) {
+        b.q[j][cb] = *reinterpret_cast<gptr<v4i>>(wbase + cofs[cb]);
+        b.s[j][cb] = *(sbase + sofs[cb]);
+      }
+    }
+  };
+
+  for (int rg = 0; rg < tile.rows; rg += GM_BM) {
+    const int M = min(GM_BM, tile.rows - rg);
+    const size_t row0 = size_t(tile.row0) + rg;
+    // 32-row blocks of this wave with rows (wave-uniform: a scalar value, so the MFMA guards are scalar branches)
+    const int rb_live = __builtin_amdgcn_readfirstlane(min(2, max(0, (M - rh * 64 + 31) / 32)));
+    v16f_t acc[2][2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = v16f_t{};
+    AStage<AM, NT> ast;
+    BStage b2[2];
+    __syncthreads();  // the previous row group's LDS reads are done
+    ast.rows(a, row0, M, tid);
+    ast.load(a, 0, tid);
+    load_b(b2[0], 0);
+    ast.store(smem, M, tid);
+    lds_barrier();
+    // One stage: prefetch stage s + 1 (activations into registers, weights into the other B buffer), MFMAs on
+    // stage s, then the activations into the other LDS buffer. Unrolled by two so the B buffers do not move.
+    const auto stage = [&](int s, BStage& bc, BStage& bn) {
+      const uint8_t* abuf = smem + (s & 1) * GM_ABUF;
+      const int sn = min(s + 1, KS - 1);
+      if (s + 1 < KS) ast.load(a, sn, tid);
+      load_b(bn, sn);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          // MFMA sub-step (j, t): both operands take inputs 64j + 32h + 8t .. + 7 of the stage.
+          bf16x8 bf[2];
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb)
+            bf[cb] = fp4x8_to_bf16(uint32_t(bc.q[j][cb][t]), __uint_as_float(bc.s[j][cb] << 23));
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb) {
+            if (rb >= rb_live) break;
+            const int r = rh * 64 + rb * 32 + l32;
+            const bf16x8 af =
+                *reinterpret_cast<const bf16x8*>(abuf + (size_t(r) * GM_LDA + 64 * j + 32 * h + 8 * t) * 2);
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = mfma32_bf16(af, bf[cb], acc[rb][cb]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      if (s + 1 < KS) {
+        ast.store(smem + ((s + 1) & 1) * GM_ABUF, M, tid);
+        lds_barrier();
+      }
+    };
+    for (int s = 0; s < KS; s += 2) {
+      stage(s, b2[0], b2[1]);
+      if (s + 1 < KS) stage(s + 1, b2[1], b2[0]);
+    }
+
+    // ---- epilogue, through LDS (the A buffers are free after the last stage): each wave writes its 64 x 64 block,
+    // then the workgroup stores whole rows with 16-byte accesses. Value i of lane l of a 32 x 32 MFMA block sits at
+    // row 8 (i/4) + 4 h + i % 4, column l32.
+    __syncthreads();
+    constexpr int LDC = 128 + 8;  // LDS row of the 128-column tile (bf16), padded
+    uint16_t* sc = reinterpret_cast<uint16_t*>(smem);
+    const auto put = [&](uint16_t* t, int rb, int cb, int i, uint16_t v) {
+      t[(rh * 64 + rb * 32 + 8 * (i / 4) + 4 * h + (i % 4)) * LDC + chh * 64 + cb * 32 + l32] = v;
+    };
+    if constexpr (NP == 1) {
+      if (a.out32) {  // fp32 rows: 128 x 128 x 4 bytes, each wave's block written and stored in turn by its lanes
+        float* sf = reinterpret_cast<float*>(smem);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+              sf[(rh * 64 + rb * 32 + 8 * (i / 4) + 4 * h + (i % 4)) * 132 + chh * 64 + cb * 32 + l32] = acc[rb][cb][i];
+        __syncthreads();
+        for (int e = tid; e < M * 32; e += NT) {
+          const int r = e / 32, c4 = (e % 32) * 4;
+          *reinterpret_cast<float4*>(a.out32 + (row0 + r) * a.ldo + bx * 128 + c4) =
+              *reinterpret_cast<const float4*>(sf + r * 132 + c4);
+        }
+      } else {
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) put(sc, rb, cb, i, f32_to_bf16(acc[rb][cb][i]));
+        __syncthreads();
+        for (int e = tid; e < M * 16; e += NT) {
+          const int r = e / 16, c8 = (e % 16) * 8;
+          *reinterpret_cast<uint4*>(a.out[0] + (row0 + r) * a.ldo + bx * 128 + c8) =
+              *reinterpret_cast<const uint4*>(sc + r * LDC + c8);
+        }
+      }
+    } else {
+      // 1. w3 waves: bf16(u) into the tile. 2. w1 waves: h = bf16(SwiGLU(bf16(g), u)) over u in place, and each row's
+      // amax over their 64 columns. 3. the whole workgroup: fake quantization of each row's 128 outputs (one block).
+      float* red = reinterpret_cast<float*>(smem + size_t(GM_BM) * LDC * 2);  // [2 column halves][128 rows]
+      if (p == 1)
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) put(sc, rb, cb, i, f32_to_bf16(acc[rb][cb][i]));
+      __syncthreads();
+      if (p == 0) {
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int r = rh * 64 + rb * 32 + 8 * (i / 4) + 4 * h + (i % 4);
+            const float w = a.gw && r < M ? a.gw[row0 + r] : 0.0f;
+            float am = 0.0f;
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+              uint16_t* cell = sc + r * LDC + chh * 64 + cb * 32 + l32;
+              const float gv = round_bf16(acc[rb][cb][i]);
+              const uint16_t u = *cell;
+              const float hval = round_bf16(swiglu_value(gv, bf16_to_f32(u), w, a.gw != nullptr, a.limit));
+              if (r < M) {
+                if (a.out[0]) a.out[0][(row0 + r) * a.ldo + col0 + cb * 32 + l32] = f32_to_bf16(gv);
+                if (a.out[1]) a.out[1][(row0 + r) * a.ldo + col0 + cb * 32 + l32] = u;
+              }
+              *cell = f32_to_bf16(hval);
+              am = fmaxf(am, fabsf(hval));
+            }
+            am = group_max<32>(am);  // the 32 lanes of this half hold the row's other columns
+            if (l32 == 0) red[chh * 128 + r] = am;
+          }
+      }
+      __syncthreads();
+      for (int e = tid; e < M * 16; e += NT) {  // 8 outputs per item
+        const int r = e / 16, c8 = (e % 16) * 8;
+        const size_t row = row0 + r;
+        if (a.gs_tab && !a.gs_tab[a.grow_expert[row]]) continue;
+        const Fp8Block blk = fp8_block_scale(fmaxf(red[r], red[128 + r]));
+        const uint4 hv = *reinterpret_cast<const uint4*>(sc + r * LDC + c8);
+        const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+        uint32_t qb[2] = {0, 0}, fq[4];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const uint8_t c = fp8_code(bf16_to_f32(uint16_t(hw[q / 2] >> (16 * (q % 2)))), blk.sc);
+          qb[q / 4] |= uint32_t(c) << (8 * (q % 4));
+          const uint32_t f = f32_to_bf16(e4m3_to_f32(c) * blk.sc);
+          fq[q / 2] = (q % 2) ? (fq[q / 2] | f << 16) : f;
+        }
+        const size_t o = row * N + size_t(bx) * 128 + c8;
+        if (a.hq) *reinterpret_cast<uint2*>(a.hq + o) = make_uint2(qb[0], qb[1]);
+        if (a.hh) *reinterpret_cast<uint4*>(a.hh + o) = make_uint4(fq[0], fq[1], fq[2], fq[3]);
+        if (a.hs && c8 == 0) a.hs[row * (N / 128) + bx] = blk.se;
+      }
+    }
+  }
+}
+
+template <int NP, int AM>
+void launch_gemm_t(const MxGemvArgs& a, int ntiles, hipStream_t st) {
+  const size_t lds = 2 * GM_ABUF;
+  auto* kern = &mx_gemm_kernel<NP, AM>;
+  UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               int(lds)));
+  const dim3 grid(unsigned(a.N / 128), unsigned(ntiles));
+  kern<<<grid, 256 * NP, lds, st>>>(a);
+  UH_CHECK_LAUNCH();
+}
+
+}  // namespace
+
+void launch_mx_gemm(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st) {
+  if (ntiles <= 0) return;
+  if (a.K % GM_KS || a.N % 128 || a.K <= 0 || a.N <= 0) throw std::runtime_error("mx_grouped_gemm: K % 128 or N % 128");
+  const bool np2 = a.w_tab[1] != nullptr, glu = a.hh || a.hq;
+  if (np2 && !glu) {  // two projections without the epilogue: one launch each
+    MxGemvArgs b = a;
+    b.w_tab[1] = nullptr;
+    b.s_tab[1] = nullptr;
+    b.out[1] = nullptr;
+    launch_mx_gemm(b, ntiles, amode, st);
+    b.w_tab[0] = a.w_tab[1];
+    b.s_tab[0] = a.s_tab[1];
+    b.out[0] = a.out[1];
+    b.out32 = nullptr;
+    launch_mx_gemm(b, ntiles, amode, st);
+    return;
+  }
+  if (glu && !np2) throw std::runtime_error("mx_grouped_gemm: glu needs two projections");
+  if (glu && a.hq && !a.hs) throw std::runtime_error("mx_grouped_gemm: glu hq without hs");
+  if (!glu && !a.out[0] && !a.out32) throw std::runtime_error("mx_grouped_gemm: null output");
+  if (amode ? !a.xa : (!a.aq || !a.as)) throw std::runtime_error("mx_grouped_gemm: null activations");
+  if (amode == 2 && a.ldx % 8) throw std::runtime_error("mx_grouped_gemm: ldx % 8");
+  if (!a.tiles) throw std::runtime_error("mx_grouped_gemm: null tiles");
+  if ((a.out[0] || a.out[1]) && a.ldo % 8) throw std::runtime_error("mx_grouped_gemm: ldo % 8 (16-byte row stores)");
+#define UH_GM(NP)                                                      \
+  (amode == 2   ? launch_gemm_t<NP, 2>(a, ntiles, st)                   \
+   : amode == 1 ? launch_gemm_t<NP, 1>(a, ntiles, st)                   \
+                : launch_gemm_t<NP, 0>(a, ntiles, st))
+  if (glu) UH_GM(2);
+  else UH_GM(1);
+#undef UH_GM
 }
 
 void launch_fp8_gemm(const Fp8GemmArgs& a, hipStream_t st) { launch_fp8_skinny(a, st); }
@@ -67,6 +432,17 @@ void mx_grouped_gemm_q(const uint8_t* q, const uint8_t* qs, int K, const Exl3Til
                        const uint8_t* const* s_tab2, bf16* out2, int, const MxGlu& glu) {
   launch_mx_gemm(gemm_args(nullptr, q, qs, K, tiles, w_tab, s_tab, out, ldo, N, ntiles_dev, w_tab2, s_tab2, out2, glu),
                  ntiles, 0, st);
+}
+
+void mx_grouped_gemm_x(const bf16* x, int ldx, const int32_t* x_rows, int K, const Exl3Tile* tiles, int ntiles,
+                       const uint8_t* const* w_tab, const uint8_t* const* s_tab, bf16* out, int ldo, int N,
+                       hipStream_t st, const int* ntiles_dev, const uint8_t* const* w_tab2,
+                       const uint8_t* const* s_tab2, bf16* out2, const MxGlu& glu) {
+  MxGemvArgs a = gemm_args(x, nullptr, nullptr, K, tiles, w_tab, s_tab, out, ldo, N, ntiles_dev, w_tab2, s_tab2, out2,
+                           glu);
+  a.x_rows = x_rows;
+  a.ldx = ldx;
+  launch_mx_gemm(a, ntiles, 2, st);
 }
 
 void mx_grouped_gemm_glu(const bf16* xa, int K, const Exl3Tile* tiles, int ntiles, const uint8_t* const* w1_tab,
