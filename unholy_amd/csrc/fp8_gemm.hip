@@ -47,8 +47,8 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const bf16* __restrict__
     if (l == 0) static_cast<float*>(s)[size_t(r) * nb + b] = sc;
   } else {
     const Fp8Block blk = fp8_block_scale(am);
-    c0 = fp8_code(v0, blk.sc);
-    c1 = fp8_code(v1, blk.sc);
+    c0 = fp8_code(v0, blk);
+    c1 = fp8_code(v1, blk);
     if constexpr (MODE == 1) {
       xr[0] = f32_to_bf16(e4m3_to_f32(c0) * blk.sc);
       xr[1] = f32_to_bf16(e4m3_to_f32(c1) * blk.sc);

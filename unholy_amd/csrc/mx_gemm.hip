@@ -7,6 +7,7 @@
 // 32x32x16 bf16 MFMAs with fp32 accumulation. Weight columns are read from HBM once per tile; the activation tile is
 // shared by the tile's column blocks, which the block mapping keeps on one XCD (one L2).
 #include <algorithm>
+#include <cstdlib>
 
 #include "common.hpp"
 #include "numerics.hpp"
@@ -90,8 +91,8 @@ struct AStage {
           uint32_t ow[8];
 #pragma unroll
           for (int q = 0; q < 8; ++q)
-            ow[q] = uint32_t(f32_to_bf16(e4m3_to_f32(fp8_code(v[2 * q], blk.sc)) * blk.sc)) |
-                    uint32_t(f32_to_bf16(e4m3_to_f32(fp8_code(v[2 * q + 1], blk.sc)) * blk.sc)) << 16;
+            ow[q] = uint32_t(f32_to_bf16(e4m3_to_f32(fp8_code(v[2 * q], blk)) * blk.sc)) |
+                    uint32_t(f32_to_bf16(e4m3_to_f32(fp8_code(v[2 * q + 1], blk)) * blk.sc)) << 16;
           o0 = make_uint4(ow[0], ow[1], ow[2], ow[3]);
           o1 = make_uint4(ow[4], ow[5], ow[6], ow[7]);
         }
@@ -126,6 +127,17 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_barrier();
 }
 
+// Block -> (column block bx, tile by). Workgroups go round-robin over the 8 XCDs (lin % 8); XCD x runs tiles x,
+// x + 8, x + 16, ... in order, each tile's column blocks back to back, so they share that XCD's L2 and the tiles that
+// exist (the first *ntiles_dev of a grid sized for the maximum) are spread evenly over the XCDs. The launcher pads
+// the grid's tile count to a multiple of 8.
+__device__ __forceinline__ void tile_block(int nbx, int& bx, int& by) {
+  const int lin = blockIdx.y * nbx + blockIdx.x, k = lin >> 3;
+  by = (k / nbx) * 8 + (lin & 7);
+  bx = k % nbx;
+}
+__host__ inline dim3 tile_grid(int nbx, int ntiles) { return dim3(unsigned(nbx), unsigned((ntiles + 7) / 8 * 8)); }
+
 // NP 1: 4 waves = 2 row halves x 2 column halves (128 x 128); NP 2: 8 waves, the same for w1 (waves 0-3) and
 // w3 (waves 4-7), with the SwiGLU + fake-quantization epilogue over the workgroup's 128 columns (one quant block).
 template <int NP, int AM>
@@ -134,10 +146,9 @@ __global__ __launch_bounds__(256 * NP) void mx_gemm_kernel(MxGemvArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   // XCD-aware mapping: linear block ids go round-robin over the 8 XCDs; consecutive logical ids (the column blocks
   // of one tile, which read the same activation rows) are given to one XCD.
-  const int nbx = gridDim.x, total = gridDim.x * gridDim.y, lin = blockIdx.y * nbx + blockIdx.x;
-  const int logical = total % 8 == 0 ? (lin % 8) * (total / 8) + lin / 8 : lin;
-  const int bx = logical % nbx, by = logical / nbx;
-  if (a.ntiles_dev && by >= *a.ntiles_dev) return;
+  int bx, by;
+  tile_block(gridDim.x, bx, by);
+  if (by >= a.ntiles || (a.ntiles_dev && by >= *a.ntiles_dev)) return;
   const Exl3Tile tile = a.tiles[by];
   if (tile.rows <= 0) return;
   const uint8_t* wps[NP];
@@ -275,9 +286,8 @@ __global__ __launch_bounds__(256 * NP) void mx_gemm_kernel(MxGemvArgs a) {
         }
       }
     } else {
-      // 1. w3 waves: bf16(u) into the tile. 2. w1 waves: h = bf16(SwiGLU(bf16(g), u)) over u in place, and each row's
-      // amax over their 64 columns. 3. the whole workgroup: fake quantization of each row's 128 outputs (one block).
-      float* red = reinterpret_cast<float*>(smem + size_t(GM_BM) * LDC * 2);  // [2 column halves][128 rows]
+      // 1. w3 waves: bf16(u) into the tile. 2. w1 waves: h = bf16(SwiGLU(bf16(g), u)) over u in place. 3. the whole
+      // workgroup: each row's amax and fake quantization of its 128 outputs (one block).
       if (p == 1)
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
@@ -293,36 +303,38 @@ __global__ __launch_bounds__(256 * NP) void mx_gemm_kernel(MxGemvArgs a) {
           for (int i = 0; i < 16; ++i) {
             const int r = rh * 64 + rb * 32 + 8 * (i / 4) + 4 * h + (i % 4);
             const float w = a.gw && r < M ? a.gw[row0 + r] : 0.0f;
-            float am = 0.0f;
 #pragma unroll
             for (int cb = 0; cb < 2; ++cb) {
               uint16_t* cell = sc + r * LDC + chh * 64 + cb * 32 + l32;
               const float gv = round_bf16(acc[rb][cb][i]);
               const uint16_t u = *cell;
-              const float hval = round_bf16(swiglu_value(gv, bf16_to_f32(u), w, a.gw != nullptr, a.limit));
+              const float hval = swiglu_value(gv, bf16_to_f32(u), w, a.gw != nullptr, a.limit);
               if (r < M) {
                 if (a.out[0]) a.out[0][(row0 + r) * a.ldo + col0 + cb * 32 + l32] = f32_to_bf16(gv);
                 if (a.out[1]) a.out[1][(row0 + r) * a.ldo + col0 + cb * 32 + l32] = u;
               }
               *cell = f32_to_bf16(hval);
-              am = fmaxf(am, fabsf(hval));
             }
-            am = group_max<32>(am);  // the 32 lanes of this half hold the row's other columns
-            if (l32 == 0) red[chh * 128 + r] = am;
           }
       }
       __syncthreads();
-      for (int e = tid; e < M * 16; e += NT) {  // 8 outputs per item
-        const int r = e / 16, c8 = (e % 16) * 8;
-        const size_t row = row0 + r;
-        if (a.gs_tab && !a.gs_tab[a.grow_expert[row]]) continue;
-        const Fp8Block blk = fp8_block_scale(fmaxf(red[r], red[128 + r]));
+      // 16 consecutive threads take one row (8 outputs each): its amax is a DPP row max. The loop bound is
+      // uniform, so every 16-lane group is whole; threads past the tile's rows only take part in the max.
+      for (int e0 = 0; e0 < M * 16; e0 += NT) {
+        const int e = e0 + tid, r = min(e / 16, M - 1), c8 = (e % 16) * 8;
         const uint4 hv = *reinterpret_cast<const uint4*>(sc + r * LDC + c8);
         const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+        float am = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) am = fmaxf(am, fabsf(bf16_to_f32(uint16_t(hw[q / 2] >> (16 * (q % 2))))));
+        am = row16_max(am);
+        const size_t row = row0 + r;
+        if (e >= M * 16 || (a.gs_tab && !a.gs_tab[a.grow_expert[row]])) continue;
+        const Fp8Block blk = fp8_block_scale(am);
         uint32_t qb[2] = {0, 0}, fq[4];
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-          const uint8_t c = fp8_code(bf16_to_f32(uint16_t(hw[q / 2] >> (16 * (q % 2)))), blk.sc);
+          const uint8_t c = fp8_code(bf16_to_f32(uint16_t(hw[q / 2] >> (16 * (q % 2)))), blk);
           qb[q / 4] |= uint32_t(c) << (8 * (q % 4));
           const uint32_t f = f32_to_bf16(e4m3_to_f32(c) * blk.sc);
           fq[q / 2] = (q % 2) ? (fq[q / 2] | f << 16) : f;
@@ -336,18 +348,295 @@ __global__ __launch_bounds__(256 * NP) void mx_gemm_kernel(MxGemvArgs a) {
   }
 }
 
+// ---- Pipelined kernel for fp8 activation codes: a 4-stage LDS ring filled by direct global -> LDS loads ----
+//
+// Workgroup = 512 threads, one tile x 256 output columns: 128 columns each of w1 and w3 (NP 2, SwiGLU epilogue)
+// or 256 columns of one matrix (NP 1). Wave w owns 64 rows and columns 64 (w >> 1) .. + 63 of the
+// 256 (rows: see rh below). Per 128-input stage the ring slot holds
+//   A  16 KB: the tile's fp8 codes, row r's 16-byte piece p at slot r * 8 + (p ^ (r & 7)) (conflict-free MFMA reads);
+//   B  16 KB: 16 blocks of 1 KB = (projection or column half q, 64-input slab j, 32-column block c); slot h * 32 + n
+//      of a block holds input half h (32 codes) of its column n, so a wave's operand read is 1 KB contiguous;
+//   Bs  1 KB: the e8m0 weight scales of (q, j) in their global order (256 B each).
+// The loads are issued S - 1 stages ahead by every wave (5 per stage) and complete in order, so "stage s has landed"
+// is a vmcnt count. They are written as inline assembly: the compiler, seeing LDS writes from global loads, would
+// otherwise wait for every one of them before each LDS read and drain the ring. The activation scales of all stages
+// are copied to LDS once per row group.
+constexpr int GP_S = 4, GP_A = 128 * 128, GP_B = 16 * 1024, GP_BS = 1024;
+constexpr int GP_STAGE = GP_A + GP_B + GP_BS;
+constexpr int GP_RING = GP_S * GP_STAGE;
+constexpr int GP_MAX_KS = (160 * 1024 - GP_RING) / 128;  // activation scales [KS][128] after the ring
+
+// 64 lanes x 16 bytes from sbase + voff (per lane) to LDS lds .. lds + 1023 (lane order).
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  // readfirstlane returns int: go through uint32_t so the low word is zero-extended, not sign-extended.
+  const uint32_t lo = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(b))));
+  const uint32_t hi = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(b >> 32))));
+  const uint64_t sbase = uint64_t(lo) | uint64_t(hi) << 32;
+  lds = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+               : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N < 64);
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);  // vmcnt(N), no lgkm / exp wait
+}
+
+template <int NP>
+__global__ __launch_bounds__(512) void mx_gemm_pipe_kernel(MxGemvArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  int bx, by;
+  tile_block(gridDim.x, bx, by);
+  if (by >= a.ntiles || (a.ntiles_dev && by >= *a.ntiles_dev)) return;
+  const Exl3Tile tile = a.tiles[by];
+  if (tile.rows <= 0) return;
+  const uint8_t* wq[2];
+  const uint8_t* sq[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    wq[q] = a.w_tab[NP == 2 ? q : 0][tile.expert];
+    sq[q] = a.s_tab[NP == 2 ? q : 0][tile.expert];
+    if (!wq[q] || !sq[q]) return;
+  }
+  const int K = a.K, KS = K / 128, N = a.N, ntn = N / 16;
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: addresses derived from it stay scalar
+  // Waves w and w + 4 share a SIMD: give them opposite row halves, so a tile with fewer than 128 rows (the idle
+  // 32-row blocks are all in the upper half) loads every SIMD alike.
+  const int rh = (wave & 1) ^ (wave >> 2), cq = wave >> 1, q_own = cq >> 1;  // projection / column half: q_own
+  // First column (of the N) of projection or half q's 128 columns.
+  const int colq0 = NP == 2 ? bx * 128 : bx * 256, colq_step = NP == 2 ? 0 : 128;
+  const size_t cslab = size_t(ntn) * 512, sslab = size_t(ntn) * 32;
+  const uint32_t lds0 = uint32_t(size_t((__attribute__((address_space(3))) uint8_t*)smem));  // LDS byte address
+  uint8_t* const as_lds = smem + GP_RING;
+
+  // Per-lane DMA offsets, constant over the stages.
+  const uint32_t boff = uint32_t((l32 * 2 + h) * 16);                      // B block: slot h*32+n <- piece 2n+h
+  const bool sc_lane = (lane >> 3) == wave;                                 // 8 lanes per wave carry the scales
+  const uint32_t bsoff = uint32_t(((wave & 1) * 8 + (lane & 7)) * 16);     // piece 8w + lane%8 of (q, j) = w / 2
+  const int sc_q = wave >> 2, sc_j = (wave >> 1) & 1;
+
+  for (int rg = 0; rg < tile.rows; rg += 128) {
+    const int M = min(128, tile.rows - rg);
+    const size_t row0 = size_t(tile.row0) + rg;
+    __syncthreads();  // the previous row group's LDS use is over
+    for (int e = tid; e < 128 * KS; e += 512) {
+      const int r = min(e & 127, M - 1), s = e >> 7;
+      as_lds[e] = a.as[(row0 + r) * KS + s];
+    }
+    uint32_t aoff[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int slot = (wave * 2 + i) * 64 + lane, r = slot >> 3, p = (slot & 7) ^ (r & 7);
+      aoff[i] = uint32_t(min(r, M - 1)) * uint32_t(K) + uint32_t(p * 16);  // rows past the tile repeat its last
+    }
+    const uint8_t* arow = a.aq + row0 * size_t(K);
+    const auto issue = [&](int s) {
+      const uint32_t st = __builtin_amdgcn_readfirstlane(lds0 + uint32_t((s % GP_S) * GP_STAGE));
+      dma16(arow + s * 128, aoff[0], st + uint32_t(wave * 2) * 1024);
+      dma16(arow + s * 128, aoff[1], st + uint32_t(wave * 2 + 1) * 1024);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int u = wave * 2 + i, q = u >> 3, j = (u >> 2) & 1, c = u & 3;
+        const uint8_t* bb = wq[q] + size_t(2 * s + j) * cslab + size_t((colq0 + q * colq_step) / 16) * 512 + c * 1024;
+        dma16(bb, boff, st + uint32_t(GP_A + u * 1024));
+      }
+      const uint8_t* sb = sq[sc_q] + size_t(2 * s + sc_j) * sslab + size_t((colq0 + sc_q * colq_step) / 16) * 32;
+      if (sc_lane) dma16(sb, bsoff, st + uint32_t(GP_A + GP_B));
+    };
+    const int rb_live = __builtin_amdgcn_readfirstlane(min(2, max(0, (M - rh * 64 + 31) / 32)));
+    v16f_t acc[2][2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = v16f_t{};
+    const int pro = min(GP_S - 1, KS);
+    for (int s = 0; s < pro; ++s) issue(s);
+
+    for (int s = 0; s < KS; ++s) {
+      const int after = min(GP_S - 2, KS - 1 - s);  // stages issued after s (loads still allowed in flight)
+      if (after >= 2) wait_vm<10>();
+      else if (after == 1) wait_vm<5>();
+      else wait_vm<0>();
+      __syncthreads();  // every wave's part of stage s has landed; slot (s - 1) % S is free
+      if (s + GP_S - 1 < KS) issue(s + GP_S - 1);
+      const uint8_t* stb = smem + (s % GP_S) * GP_STAGE;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        v4i bq[2];
+        float bs[2];
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          const int c = (cq & 1) * 2 + cb, u = q_own * 8 + j * 4 + c, n = c * 32 + l32;
+          bq[cb] = *reinterpret_cast<const v4i*>(stb + GP_A + u * 1024 + (h * 32 + l32) * 16);
+          bs[cb] = __uint_as_float(uint32_t(stb[GP_A + GP_B + (q_own * 2 + j) * 256 + (n >> 4) * 32 + (n & 15) * 2 + h])
+                                   << 23);
+        }
+        v4i aq[2][2];
+        float asc[2];
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+          const int r = rh * 64 + rb * 32 + l32;
+#pragma unroll
+          for (int x = 0; x < 2; ++x)
+            aq[rb][x] = *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 * j + 2 * h + x) ^ (r & 7))) * 16);
+          asc[rb] = __uint_as_float(uint32_t(as_lds[s * 128 + r]) << 23);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          bf16x8 bf[2];
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb) bf[cb] = fp4x8_to_bf16(uint32_t(bq[cb][t]), bs[cb]);
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb) {
+            if (rb >= rb_live) break;
+            const bf16x8 af =
+                fp8x8_to_bf16(uint32_t(aq[rb][t >> 1][(t & 1) * 2]), uint32_t(aq[rb][t >> 1][(t & 1) * 2 + 1]), asc[rb]);
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = mfma32_bf16(af, bf[cb], acc[rb][cb]);
+          }
+        }
+      }
+    }
+
+    // ---- epilogue through LDS (the ring is free once every wave is past its last stage)
+    __syncthreads();
+    const auto row_of = [&](int rb, int i) { return rh * 64 + rb * 32 + 8 * (i / 4) + 4 * h + (i % 4); };
+    if constexpr (NP == 1) {
+      const int c0 = cq * 64;
+      if (a.out32) {
+        constexpr int LDF = 256 + 4;
+        float* sf = reinterpret_cast<float*>(smem);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sf[row_of(rb, i) * LDF + c0 + cb * 32 + l32] = acc[rb][cb][i];
+        __syncthreads();
+        for (int e = tid; e < M * 64; e += 512) {
+          const int r = e / 64, c4 = (e % 64) * 4;
+          *reinterpret_cast<float4*>(a.out32 + (row0 + r) * a.ldo + bx * 256 + c4) =
+              *reinterpret_cast<const float4*>(sf + r * LDF + c4);
+        }
+      } else {
+        constexpr int LDC = 256 + 8;
+        uint16_t* sc = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sc[row_of(rb, i) * LDC + c0 + cb * 32 + l32] = f32_to_bf16(acc[rb][cb][i]);
+        __syncthreads();
+        for (int e = tid; e < M * 32; e += 512) {
+          const int r = e / 32, c8 = (e % 32) * 8;
+          *reinterpret_cast<uint4*>(a.out[0] + (row0 + r) * a.ldo + bx * 256 + c8) =
+              *reinterpret_cast<const uint4*>(sc + r * LDC + c8);
+        }
+      }
+    } else {
+      // 1. w3 waves: bf16(u) into the 128-column tile. 2. w1 waves: h = bf16(SwiGLU(bf16(g), u)) in place. 3. the
+      // workgroup: each row's amax and fake quantization of its 128 outputs (one block).
+      constexpr int LDC = 128 + 8;
+      uint16_t* sc = reinterpret_cast<uint16_t*>(smem);
+      const int chh = cq & 1, col0 = bx * 128 + chh * 64;
+      if (q_own == 1)
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+              sc[row_of(rb, i) * LDC + chh * 64 + cb * 32 + l32] = f32_to_bf16(acc[rb][cb][i]);
+      __syncthreads();
+      if (q_own == 0) {
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int r = row_of(rb, i);
+            const float w = a.gw && r < M ? a.gw[row0 + r] : 0.0f;
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+              uint16_t* cell = sc + r * LDC + chh * 64 + cb * 32 + l32;
+              const float gv = round_bf16(acc[rb][cb][i]);
+              const uint16_t u = *cell;
+              const float hval = swiglu_value(gv, bf16_to_f32(u), w, a.gw != nullptr, a.limit);
+              if (r < M) {
+                if (a.out[0]) a.out[0][(row0 + r) * a.ldo + col0 + cb * 32 + l32] = f32_to_bf16(gv);
+                if (a.out[1]) a.out[1][(row0 + r) * a.ldo + col0 + cb * 32 + l32] = u;
+              }
+              *cell = f32_to_bf16(hval);
+            }
+          }
+      }
+      __syncthreads();
+      // 16 consecutive threads take one row (8 outputs each): its amax is a DPP row max. The loop bound is
+      // uniform, so every 16-lane group is whole; threads past the tile's rows only take part in the max.
+      for (int e0 = 0; e0 < M * 16; e0 += 512) {
+        const int e = e0 + tid, r = min(e / 16, M - 1), c8 = (e % 16) * 8;
+        const uint4 hv = *reinterpret_cast<const uint4*>(sc + r * LDC + c8);
+        const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+        float am = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) am = fmaxf(am, fabsf(bf16_to_f32(uint16_t(hw[q / 2] >> (16 * (q % 2))))));
+        am = row16_max(am);
+        const size_t row = row0 + r;
+        if (e >= M * 16 || (a.gs_tab && !a.gs_tab[a.grow_expert[row]])) continue;
+        const Fp8Block blk = fp8_block_scale(am);
+        uint32_t qb[2] = {0, 0}, fq[4];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const uint8_t c = fp8_code(bf16_to_f32(uint16_t(hw[q / 2] >> (16 * (q % 2)))), blk);
+          qb[q / 4] |= uint32_t(c) << (8 * (q % 4));
+          const uint32_t f = f32_to_bf16(e4m3_to_f32(c) * blk.sc);
+          fq[q / 2] = (q % 2) ? (fq[q / 2] | f << 16) : f;
+        }
+        const size_t o = row * N + size_t(bx) * 128 + c8;
+        if (a.hq) *reinterpret_cast<uint2*>(a.hq + o) = make_uint2(qb[0], qb[1]);
+        if (a.hh) *reinterpret_cast<uint4*>(a.hh + o) = make_uint4(fq[0], fq[1], fq[2], fq[3]);
+        if (a.hs && c8 == 0) a.hs[row * (N / 128) + bx] = blk.se;
+      }
+    }
+  }
+}
+
+template <int NP>
+void launch_pipe_t(const MxGemvArgs& a, int ntiles, hipStream_t st) {
+  const size_t lds = size_t(GP_RING) + size_t(128) * (a.K / 128);
+  auto* kern = &mx_gemm_pipe_kernel<NP>;
+  UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               int(lds)));
+  MxGemvArgs b = a;
+  b.ntiles = ntiles;
+  kern<<<tile_grid(a.N / (NP == 2 ? 128 : 256), ntiles), 512, lds, st>>>(b);
+  UH_CHECK_LAUNCH();
+}
+
 template <int NP, int AM>
 void launch_gemm_t(const MxGemvArgs& a, int ntiles, hipStream_t st) {
   const size_t lds = 2 * GM_ABUF;
   auto* kern = &mx_gemm_kernel<NP, AM>;
   UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                int(lds)));
-  const dim3 grid(unsigned(a.N / 128), unsigned(ntiles));
-  kern<<<grid, 256 * NP, lds, st>>>(a);
+  MxGemvArgs b = a;
+  b.ntiles = ntiles;
+  kern<<<tile_grid(a.N / 128, ntiles), 256 * NP, lds, st>>>(b);
   UH_CHECK_LAUNCH();
 }
 
 }  // namespace
+
+// UH_GEMM_PIPE=0 selects the register-staged kernel for fp8 codes too (comparison runs).
+static bool pipe_disabled() {
+  static const bool off = [] {
+    const char* e = std::getenv("UH_GEMM_PIPE");
+    return e && e[0] == '0';
+  }();
+  return off;
+}
 
 void launch_mx_gemm(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st) {
   if (ntiles <= 0) return;
@@ -377,8 +666,14 @@ void launch_mx_gemm(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st) 
   (amode == 2   ? launch_gemm_t<NP, 2>(a, ntiles, st)                   \
    : amode == 1 ? launch_gemm_t<NP, 1>(a, ntiles, st)                   \
                 : launch_gemm_t<NP, 0>(a, ntiles, st))
-  if (glu) UH_GM(2);
-  else UH_GM(1);
+  const bool pipe = amode == 0 && a.K / GM_KS <= GP_MAX_KS && !pipe_disabled();
+  if (glu) {
+    if (pipe) launch_pipe_t<2>(a, ntiles, st);
+    else UH_GM(2);
+  } else {
+    if (pipe && a.N % 256 == 0) launch_pipe_t<1>(a, ntiles, st);
+    else UH_GM(1);
+  }
 #undef UH_GM
 }
 

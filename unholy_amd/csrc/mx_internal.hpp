@@ -19,6 +19,7 @@ struct MxGemvArgs {
   int ldx;
   int K, N, ldo;
   const Exl3Tile* tiles;
+  int ntiles;  // tiles the grid covers (set by the launcher; the grid may be padded past it)
   const int* ntiles_dev;
   const uint8_t* const* w_tab[2];
   const uint8_t* const* s_tab[2];

@@ -64,7 +64,7 @@ __global__ __launch_bounds__(256) void mx_transform_kernel(const bf16* __restric
       v[1] = bf16_to_f32(uint16_t(raw >> 16));
     }
     const Fp8Block b = fp8_block_scale(wave_max(fmaxf(fabsf(v[0]), fabsf(v[1]))));
-    const uint8_t c0 = fp8_code(v[0], b.sc), c1 = fp8_code(v[1], b.sc);
+    const uint8_t c0 = fp8_code(v[0], b), c1 = fp8_code(v[1], b);
     if (out)
       *reinterpret_cast<uint32_t*>(out + size_t(r) * K + k0) =
           uint32_t(f32_to_bf16(e4m3_to_f32(c0) * b.sc)) | uint32_t(f32_to_bf16(e4m3_to_f32(c1) * b.sc)) << 16;
@@ -173,8 +173,8 @@ __global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(OCC))) vo
             se = blk.se;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-              lo |= uint32_t(fp8_code(v[t], blk.sc)) << (8 * t);
-              hi |= uint32_t(fp8_code(v[t + 4], blk.sc)) << (8 * t);
+              lo |= uint32_t(fp8_code(v[t], blk)) << (8 * t);
+              hi |= uint32_t(fp8_code(v[t + 4], blk)) << (8 * t);
             }
           }
           *reinterpret_cast<uint2*>(sA + m * ldA + c) = make_uint2(lo, hi);
@@ -275,7 +275,7 @@ __global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(OCC))) vo
         for (int w = 1; w < GV_WAVES; ++w) rm = fmaxf(rm, red[w][r]);
         const Fp8Block blk = fp8_block_scale(rm);
         const size_t col = size_t(nt) * 16 + nl;
-        const uint8_t c = fp8_code(h[i], blk.sc);
+        const uint8_t c = fp8_code(h[i], blk);
         if (a.hh) a.hh[row * N + col] = f32_to_bf16(e4m3_to_f32(c) * blk.sc);
         if (a.hq) a.hq[row * N + col] = c;
         if (a.hs && wave == 0 && nl == 0) a.hs[row * (N / 128) + blockIdx.x] = blk.se;

@@ -100,6 +100,19 @@ __device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v) {
   const uint32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
   return op(op(r0, r1), op(r2, r3));
 }
+// Max over each aligned group of 16 lanes (a DPP row), every lane of the group receiving it: two quad
+// permutations then rotations by 4 and 8 within the row. All 16 lanes of a group must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_max_step(float x) {
+  return fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), CTRL, 0xf, 0xf,
+                                                             false)));
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = dpp_max_step<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = dpp_max_step<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = dpp_max_step<0x124>(v);  // row_ror:4
+  return dpp_max_step<0x128>(v);  // row_ror:8
+}
 // A float's bits mapped so that unsigned order is float order.
 __device__ __forceinline__ uint32_t orderable(float f) {
   const uint32_t b = __float_as_uint(f);
@@ -108,16 +121,23 @@ __device__ __forceinline__ uint32_t orderable(float f) {
 
 // The reference's activation fake quantization of one value given its block's amax (ref_elem.hip:32-37):
 // amax floored at 1e-4, e8m0 scale 2^ceil(log2(amax / 448)), e4m3 RNE of the clamped quotient.
+// inv = 1 / sc exactly (se lies in [105, 247]: the amax floor and the fp32 range keep 2^(127 - se) normal), so
+// v * inv is the correctly rounded v / sc, the same value the division gives, without the IEEE division sequence.
 struct Fp8Block {
   uint8_t se;
   float sc;
+  float inv;
 };
 __device__ __forceinline__ Fp8Block fp8_block_scale(float amax) {
   const uint8_t se = pow2_ceil_e8m0(fmaxf(amax, 1e-4f) * (1.0f / 448.0f));
-  return {se, e8m0_to_f32(se)};
+  return {se, e8m0_to_f32(se), __uint_as_float(uint32_t(254 - se) << 23)};
 }
+// Any positive fp32 scale (the fp32-scale activation format): a true division.
 __device__ __forceinline__ uint8_t fp8_code(float v, float sc) {
   return f32_to_e4m3(fminf(fmaxf(v / sc, -448.0f), 448.0f));
+}
+__device__ __forceinline__ uint8_t fp8_code(float v, const Fp8Block& b) {
+  return f32_to_e4m3(fminf(fmaxf(v * b.inv, -448.0f), 448.0f));
 }
 
 // SwiGLU with the clamp and optional routing weight (ref_moe.hip:66-72): x = silu(min(g, l)) * clamp(u, +-l),
