@@ -2,6 +2,7 @@
 """Benchmark of the MXFP4 routed-expert FFN on one MI355X (gfx950).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
+    python bench.py --only {decode,single,verify,prefill,fp8,copy}   # one workload (for profilers), one JSON line
 
 A step is one routed-expert FFN over one batch of synthetic tokens: softmax top-6 routing of [T, 256] logits,
 dispatch, fp8 input transform, w1/w3 grouped GEMV with the SwiGLU epilogue, w2 grouped GEMV, combine to bf16
@@ -31,6 +32,9 @@ MAT_BYTES = I * D // 2 + I * D // 32  # 4,456,448: codes + e8m0 scales of one MX
 EXPERT_BYTES = 3 * MAT_BYTES
 LIMIT = 10.0
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the dominant kernel (w1/w3 GEMV, this seeded workload): FETCH_SIZE + WRITE_SIZE from two
+# rocprofv3 --pmc runs, scaled by the same counters on a 1 GiB device copy (profiles/hbm_traffic_pmc.md).
+GEMV_TRAFFIC_BYTES = 399.8e6
 BF16_PEAK_TFLOPS = 2500.0
 
 
@@ -206,6 +210,34 @@ def cpu_baseline(seconds=10.0, max_reps=5):
                        f"{dt:.1f} s on {threads} threads)")
 
 
+def run_only(name, args, rng):
+    """One workload alone, so that a profiler's kernel table holds only its kernels (plus weight generation)."""
+    if name == "copy":  # 1 GiB device-to-device copies: the reference for FETCH_SIZE / WRITE_SIZE counters
+        from unholy_amd.device import DeviceBuffer, synchronize
+        from unholy_amd._lib import call
+        n = 1 << 30
+        src, dst = DeviceBuffer(n), DeviceBuffer(n)
+        call("uh_fill_random_bytes", src, n, 1, 0, 255, None)
+        for _ in range(4):
+            call("uh_memcpy_d2d", dst, src, n, None)
+        synchronize()
+        return {"workload": "copy", "bytes_per_copy": n, "copies": 4}
+    if name == "fp8":
+        return {f"fp8_dense_M{M}": bench_fp8_dense(M, 100 if M < 4096 else 10, 10 if M < 4096 else 2, rng, c)
+                for M, c in ((1, 64), (64, 64), (4096, 4))}
+    w = Weights(seed=0)
+    if name == "single":
+        return {"single_gemv_M1_ms": bench_single_gemv(w, 500, 50, rng)}
+    if name == "decode":
+        d = bench_moe(w, 8, args.steps, args.warmup, rng)
+        return {"moe_decode_T8_ms": d["ms"], "distinct_experts": d["U"]}
+    if name == "verify":
+        d = bench_moe(w, 64, 50, 5, rng, bias=0.5)
+        return {"moe_verify_T64_ms": d["ms"], "distinct_experts": d["U"]}
+    d = bench_moe(w, 4096, 5, 1, rng, R=2)
+    return {"moe_prefill_T4096_ms": d["ms"]}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -213,6 +245,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=["decode", "single", "verify", "prefill", "fp8", "copy"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the MoE expert path runs on a single MI355X in this build "
@@ -221,6 +254,9 @@ def main():
     from unholy_amd.device import device_name
 
     rng = np.random.default_rng(0)
+    if args.only:
+        print(json.dumps(run_only(args.only, args, rng)))
+        return
     w = Weights(seed=0)
     dec = bench_moe(w, 8, args.steps, args.warmup, rng, stage=True)
     ms = dec["ms"]
@@ -251,7 +287,8 @@ def main():
                    "distinct_experts_per_step": U, "step_algorithmic_bytes": step_bytes,
                    "step_GBps": step_bytes / (ms * 1e-3) / 1e9, "device": device_name()},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": GEMV_TRAFFIC_BYTES,
+                     "traffic_source": "profiles/hbm_traffic_pmc.md (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)",
                      "kernel": "mx_gemv_kernel<2,true,false> (w1/w3 + SwiGLU)", "avg_launch_ms": g_ms,
                      "algorithmic_bytes_per_launch": float(np.mean(gemv_bytes))},
     }
