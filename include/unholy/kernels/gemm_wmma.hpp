@@ -1,5 +1,5 @@
 // Tiled fp8 W8A8 GEMM. Drop-in for gemm_w8a8_wmma of the reference's src/kernels/gemm_wmma.hpp:12-18 (there a
-// gfx12 WMMA kernel; here the gfx950 block-scaled MFMA). a e4m3 [M, K], sa e8m0 [M, K/128]; w e4m3 [N, K], sw
+// gfx12 WMMA kernel; here exact e4m3 -> bf16 dequantization and the gfx950 bf16 MFMA). a e4m3 [M, K], sa e8m0 [M, K/128]; w e4m3 [N, K], sw
 // e8m0 [ceil(N/128), K/128]; K % 128 == 0.
 #pragma once
 

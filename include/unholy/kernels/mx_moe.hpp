@@ -9,9 +9,10 @@
 //
 // Arithmetic: each expert product is sum over 32-blocks of (sum of e4m3(x) * e2m1(w)) * sa * sw with sa the
 // activation row's e8m0 scale per 128 inputs and sw the weight's per 32 (the reference's act_quant_fp8 +
-// gemm_a8w4, ref_gemm.hip:180-183). Here it runs on the CDNA4 block-scaled MFMA
-// (v_mfma_scale_f32_16x16x128_f8f6f4: A = e4m3 activation codes, B = e2m1 weight codes, per-32 e8m0 scales
-// on both operands) with fp32 accumulation: the same exact products summed in another fp32 order.
+// gemm_a8w4, ref_gemm.hip:180-183). Here both operands are dequantized exactly in registers (every e4m3 x 2^k
+// and e2m1 x 2^k value is a bf16 number) and multiplied on the bf16 MFMA with fp32 accumulation: the same exact
+// products summed in another fp32 order. (The block-scaled f8f6f4 MFMA is not used for results: its internal
+// sums lose bits, measured at ~3e-3 of the output against fp64 on this hardware.)
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -95,7 +96,7 @@ void mx_grouped_gemv(const bf16* xa, int K, const Exl3Tile* tiles, int ntiles, c
                      const MxGlu& glu = {}, const MxSums& sums = {});
 
 // ---- native fp8-activation forms (no reference counterpart: the activations stay as e4m3 codes + e8m0 scales
-// per 128, the operand format of the block-scaled MFMA, instead of fake-quantized bf16) -----------------------------
+// per 128, one byte per input, instead of fake-quantized bf16) -----------------------------
 // q [P, K] e4m3 + qs [P, K/128] e8m0: act_quant_fp8 of x[x_rows[r]] per 128 (rows of non-resident experts skipped).
 void mx_xform_in_fp8(const bf16* x, int ldx, const int32_t* row_expert, const uint8_t* const* s_tab, uint8_t* q,
                      uint8_t* qs, int P, int K, hipStream_t st, const int32_t* x_rows = nullptr);

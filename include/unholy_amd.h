@@ -104,6 +104,8 @@ int uh_mx_grouped_gemm_x(const uint16_t* x, int ldx, const int32_t* x_rows, int 
 int uh_mx_grouped_gemv_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const int32_t* tiles, int ntiles,
                                 const uint8_t* const* w_tab, const uint8_t* const* s_tab, float* out, int ldo, int N,
                                 void* stream, const int* ntiles_dev, int max_rows);
+/* No reference counterpart: the prefill GEMM on e4m3 activation codes q [P, K] + e8m0 qs [P, K/128] (the form the
+ * forward uses; same arguments as uh_mx_grouped_gemv_q). */
 int uh_mx_grouped_gemm_q(const uint8_t* q, const uint8_t* qs, int K, const int32_t* tiles, int ntiles,
                          const uint8_t* const* w_tab, const uint8_t* const* s_tab, uint16_t* out, int ldo, int N,
                          void* stream, const int* ntiles_dev, const uint8_t* const* w_tab2,
