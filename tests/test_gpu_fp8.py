@@ -22,7 +22,7 @@ def _weights_f32s(rng, N, K):
     return q.download((N, K), np.uint8), s.download(((N + 127) // 128, K // 128), np.float32), w
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (5, 384, 1024), (64, 512, 1024), (300, 256, 512)])
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (5, 384, 1024), (64, 512, 1024), (300, 256, 512), (3, 136, 384), (1000, 768, 1024), (129, 200, 256)])
 def test_fp8_f32_scales(M, N, K):
     """BASELINE config 4 form: A bf16 -> e4m3 per 1x128 with fp32 scales; W e4m3 with fp32 128x128 scales."""
     rng = np.random.default_rng(M + N)
@@ -47,7 +47,7 @@ def test_fp8_f32_scales(M, N, K):
     assert mr <= 1e-2
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (8, 1024, 512), (33, 256, 1024), (200, 512, 512)])
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (8, 1024, 512), (33, 256, 1024), (200, 512, 512), (17, 200, 640), (1000, 768, 1024)])
 def test_fp8_e8m0_scales(M, N, K):
     """The reference's W8A8 contract (gemm_w8a8 / gemv_w8a8 / gemm_w8a8_wmma): e8m0 scales on both sides."""
     rng = np.random.default_rng(M * 3 + K)

@@ -196,6 +196,106 @@ __global__ __launch_bounds__(DN_NT) void fp8_skinny_kernel(Fp8GemmArgs a) {
   }
 }
 
+// ---- fp8 dense, small M (<= 64 rows): bandwidth-shaped --------------------------------------------------------------
+// One workgroup per 16-column tile; its 8 waves split K (wave w takes 128-blocks w * per .. + per - 1), so the grid
+// covers every CU and each CU keeps 8 waves x 64 lanes x 128 B of weights in flight (four 128-blocks per wave are
+// loaded before any is used). Lane (nl, g) reads 32 weight bytes of column n0 + nl at inputs 32g .. + 31 of a block
+// and the same inputs of activation row nl (row tile mt: rows 16 mt + nl) from global memory (A is small and
+// cache-resident), dequantizes both exactly to bf16 (e8m0 scales folded in) and issues 16x16x32 bf16 MFMAs. With fp32
+// scales each block's MFMA chain starts from zero and is folded as acc += raw * (sa * sw). The 8 partial tiles are
+// summed in wave order through LDS.
+constexpr int FV_WAVES = 8, FV_CHUNK = 4;
+
+template <bool F32S, int MT>
+__global__ __launch_bounds__(64 * FV_WAVES) void fp8_gemv_kernel(Fp8GemmArgs a) {
+  __shared__ v4f red[FV_WAVES][MT][64];
+  const int K = a.K, KS = K / 128, N = a.N, M = a.M;
+  const int tid = threadIdx.x, lane = tid & 63, nl = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n0 = blockIdx.x * 16, n = min(n0 + nl, N - 1), nb = n0 / 128;  // a 16-column tile lies in one 128-block
+  const int per = (KS + FV_WAVES - 1) / FV_WAVES, b0 = min(KS, wave * per), b1 = min(KS, b0 + per);
+  const uint8_t* wrow = a.w + size_t(n) * K + g * 32;
+  v4f acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int kc = b0; kc < b1; kc += FV_CHUNK) {
+    v4i b[FV_CHUNK][2];
+#pragma unroll
+    for (int u = 0; u < FV_CHUNK; ++u) {  // unconditional (clamped) loads: all in flight before the first use
+      const int kb = min(kc + u, b1 - 1);
+      b[u][0] = *reinterpret_cast<gptr<v4i>>(as_global(wrow + kb * 128));
+      b[u][1] = *reinterpret_cast<gptr<v4i>>(as_global(wrow + kb * 128 + 16));
+    }
+#pragma unroll
+    for (int u = 0; u < FV_CHUNK; ++u) {
+      const int kb = kc + u;
+      if (kb >= b1) break;
+      const float swv = F32S ? a.sw32[size_t(nb) * KS + kb] : e8m0_to_f32(a.sw8[size_t(nb) * KS + kb]);
+      bf16x8 bf[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        bf[t] = fp8x8_to_bf16(uint32_t(b[u][t / 2][2 * (t % 2)]), uint32_t(b[u][t / 2][2 * (t % 2) + 1]),
+                              F32S ? 1.0f : swv);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if (mt * 16 >= M) break;
+        const int r = mt * 16 + nl;
+        bf16x8 af[4];
+        if (r < M) {
+          const uint8_t* ap = a.a + size_t(r) * K + kb * 128 + g * 32;
+          const v4i lo = *reinterpret_cast<gptr<v4i>>(as_global(ap));
+          const v4i hi = *reinterpret_cast<gptr<v4i>>(as_global(ap + 16));
+          const float sc = F32S ? 1.0f : e8m0_to_f32(a.sa8[size_t(r) * KS + kb]);
+          af[0] = fp8x8_to_bf16(lo[0], lo[1], sc);
+          af[1] = fp8x8_to_bf16(lo[2], lo[3], sc);
+          af[2] = fp8x8_to_bf16(hi[0], hi[1], sc);
+          af[3] = fp8x8_to_bf16(hi[2], hi[3], sc);
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) af[t] = bf16x8{};
+        }
+        if constexpr (F32S) {
+          v4f raw = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) raw = mfma_bf16(af[t], bf[t], raw);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int rr = mt * 16 + 4 * g + i;  // C row of value i
+            const float sav = rr < M ? a.sa32[size_t(rr) * KS + kb] : 0.0f;
+            acc[mt][i] += raw[i] * (sav * swv);
+          }
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) acc[mt] = mfma_bf16(af[t], bf[t], acc[mt]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) red[wave][mt][lane] = acc[mt];
+  __syncthreads();
+  // Wave w < MT stores row tile w: the sum of the 8 partials in wave order.
+  if (wave < MT && wave * 16 < M) {
+    v4f s = red[0][wave][lane];
+#pragma unroll
+    for (int w = 1; w < FV_WAVES; ++w) s += red[w][wave][lane];
+    if (n0 + nl < N)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = wave * 16 + 4 * g + i;
+        if (r < M) a.c[size_t(r) * a.ldc + n0 + nl] = f32_to_bf16(s[i]);
+      }
+  }
+}
+
+template <bool F32S>
+void launch_fp8_gemv_t(const Fp8GemmArgs& a, hipStream_t st) {
+  const dim3 grid(unsigned(cdiv(size_t(a.N), 16)));
+  if (a.M <= 16) fp8_gemv_kernel<F32S, 1><<<grid, 64 * FV_WAVES, 0, st>>>(a);
+  else fp8_gemv_kernel<F32S, 4><<<grid, 64 * FV_WAVES, 0, st>>>(a);
+  UH_CHECK_LAUNCH();
+}
+
 }  // namespace
 
 void launch_fp8_skinny(const Fp8GemmArgs& a0, hipStream_t st) {
@@ -220,6 +320,17 @@ void launch_fp8_skinny(const Fp8GemmArgs& a0, hipStream_t st) {
     fp8_skinny_kernel<false><<<grid, DN_NT, lds, st>>>(a);
   }
   UH_CHECK_LAUNCH();
+}
+
+void launch_fp8_gemv(const Fp8GemmArgs& a, hipStream_t st) {
+  if (a.M <= 0) return;
+  if (a.M > 64) throw std::runtime_error("fp8 gemv: M > 64");
+  if (a.K % 128 || a.K <= 0 || a.N <= 0) throw std::runtime_error("fp8 gemm: K % 128");
+  if (!a.a || !a.w || !a.c) throw std::runtime_error("fp8 gemm: null operand");
+  const bool f32s = a.sa32 != nullptr;
+  if (f32s ? !a.sw32 : (!a.sa8 || !a.sw8)) throw std::runtime_error("fp8 gemm: scales");
+  if (f32s) launch_fp8_gemv_t<true>(a, st);
+  else launch_fp8_gemv_t<false>(a, st);
 }
 
 // ---- entry points ---------------------------------------------------------------------------------------------------
@@ -279,7 +390,7 @@ void gemv_w8a8(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint
   g.M = M;
   g.N = N;
   g.K = K;
-  launch_fp8_skinny(g, st);
+  launch_fp8_gemm(g, st);
 }
 void gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw, bf16* c, int ldc, int M,
                    int N, int K, hipStream_t st) {

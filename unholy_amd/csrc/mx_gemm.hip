@@ -14,18 +14,14 @@
 #include "unholy/kernels/mx_moe.hpp"
 #include "mx_internal.hpp"
 #include "fp8_internal.hpp"
+#include "pipe.hpp"
 
 namespace unholy::kernels {
 
 using namespace uh;
+using namespace pipe;
 
 namespace {
-
-typedef float v16f_t __attribute__((ext_vector_type(16)));
-
-__device__ __forceinline__ v16f_t mfma32_bf16(bf16x8 a, bf16x8 b, v16f_t c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
 
 constexpr int GM_BM = 128, GM_KS = 128, GM_LDA = GM_KS + 8;  // LDS row: 128 bf16 + 16 bytes of padding
 constexpr size_t GM_ABUF = size_t(GM_BM) * GM_LDA * 2;       // one stage of A in LDS (bytes)
@@ -120,23 +116,6 @@ struct BStage {
   v4i q[2][2];
   uint32_t s[2][2];
 };
-
-// LDS barrier that does not wait for outstanding global loads (the next stage's prefetch stays in flight).
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-  __builtin_amdgcn_s_barrier();
-}
-
-// Block -> (column block bx, tile by). Workgroups go round-robin over the 8 XCDs (lin % 8); XCD x runs tiles x,
-// x + 8, x + 16, ... in order, each tile's column blocks back to back, so they share that XCD's L2 and the tiles that
-// exist (the first *ntiles_dev of a grid sized for the maximum) are spread evenly over the XCDs. The launcher pads
-// the grid's tile count to a multiple of 8.
-__device__ __forceinline__ void tile_block(int nbx, int& bx, int& by) {
-  const int lin = blockIdx.y * nbx + blockIdx.x, k = lin >> 3;
-  by = (k / nbx) * 8 + (lin & 7);
-  bx = k % nbx;
-}
-__host__ inline dim3 tile_grid(int nbx, int ntiles) { return dim3(unsigned(nbx), unsigned((ntiles + 7) / 8 * 8)); }
 
 // NP 1: 4 waves = 2 row halves x 2 column halves (128 x 128); NP 2: 8 waves, the same for w1 (waves 0-3) and
 // w3 (waves 4-7), with the SwiGLU + fake-quantization epilogue over the workgroup's 128 columns (one quant block).
@@ -366,23 +345,6 @@ constexpr int GP_STAGE = GP_A + GP_B + GP_BS;
 constexpr int GP_RING = GP_S * GP_STAGE;
 constexpr int GP_MAX_KS = (160 * 1024 - GP_RING) / 128;  // activation scales [KS][128] after the ring
 
-// 64 lanes x 16 bytes from sbase + voff (per lane) to LDS lds .. lds + 1023 (lane order).
-__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
-  const uint64_t b = reinterpret_cast<uint64_t>(base);
-  // readfirstlane returns int: go through uint32_t so the low word is zero-extended, not sign-extended.
-  const uint32_t lo = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(b))));
-  const uint32_t hi = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(b >> 32))));
-  const uint64_t sbase = uint64_t(lo) | uint64_t(hi) << 32;
-  lds = __builtin_amdgcn_readfirstlane(lds);
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
-               : "memory", "m0");
-}
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N < 64);
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);  // vmcnt(N), no lgkm / exp wait
-}
-
 template <int NP>
 __global__ __launch_bounds__(512) void mx_gemm_pipe_kernel(MxGemvArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
@@ -408,7 +370,7 @@ __global__ __launch_bounds__(512) void mx_gemm_pipe_kernel(MxGemvArgs a) {
   // First column (of the N) of projection or half q's 128 columns.
   const int colq0 = NP == 2 ? bx * 128 : bx * 256, colq_step = NP == 2 ? 0 : 128;
   const size_t cslab = size_t(ntn) * 512, sslab = size_t(ntn) * 32;
-  const uint32_t lds0 = uint32_t(size_t((__attribute__((address_space(3))) uint8_t*)smem));  // LDS byte address
+  const uint32_t lds0 = lds_addr(smem);
   uint8_t* const as_lds = smem + GP_RING;
 
   // Per-lane DMA offsets, constant over the stages.
@@ -677,7 +639,11 @@ void launch_mx_gemm(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st) 
 #undef UH_GM
 }
 
-void launch_fp8_gemm(const Fp8GemmArgs& a, hipStream_t st) { launch_fp8_skinny(a, st); }
+void launch_fp8_gemm(const Fp8GemmArgs& a, hipStream_t st) {
+  if (a.M <= 64) launch_fp8_gemv(a, st);
+  else if (fp8_tiled_fits(a)) launch_fp8_tiled(a, st);
+  else launch_fp8_skinny(a, st);
+}
 
 namespace {
 MxGemvArgs gemm_args(const bf16* xa, const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles,

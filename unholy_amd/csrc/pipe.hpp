@@ -1,0 +1,72 @@
+// Building blocks of the LDS-ring GEMM kernels (gfx950): direct global -> LDS loads, vmcnt waits, the XCD-aware
+// block mapping and the 32x32x16 bf16 MFMA.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "common.hpp"
+
+namespace unholy::kernels::pipe {
+
+typedef float v16f_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ v16f_t mfma32_bf16(uh::bf16x8 a, uh::bf16x8 b, v16f_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// The LDS byte address of a pointer into shared memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return uint32_t(size_t((const __attribute__((address_space(3))) uint8_t*)p));
+}
+
+__device__ __forceinline__ uint64_t uniform_ptr(const void* base) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  // readfirstlane returns int: go through uint32_t so the low word is zero-extended, not sign-extended.
+  const uint32_t lo = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(b))));
+  const uint32_t hi = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(b >> 32))));
+  return uint64_t(lo) | uint64_t(hi) << 32;
+}
+
+// The active lanes of a wave copy 16 bytes each from base + voff (per lane) to LDS lds + 16 * lane. The loads count
+// in vmcnt like any global load and complete in order. Issued as inline assembly: the compiler, seeing LDS written
+// by global loads, would otherwise wait for all of them before every LDS read and drain the ring.
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
+  const uint64_t sbase = uniform_ptr(base);
+  lds = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+               : "memory", "m0");
+}
+// The same with 4 bytes per lane (to LDS lds + 4 * lane): a gather of one dword per lane.
+__device__ __forceinline__ void dma4(const void* base, uint32_t voff, uint32_t lds) {
+  const uint64_t sbase = uniform_ptr(base);
+  lds = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+               : "memory", "m0");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N < 64);
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);  // vmcnt(N), no lgkm / exp wait
+}
+
+// LDS barrier that does not wait for outstanding global loads (a register prefetch stays in flight).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+}
+
+// Block -> (column block bx, tile by). Workgroups go round-robin over the 8 XCDs (lin % 8); XCD x runs tiles x,
+// x + 8, x + 16, ... in order, each tile's column blocks back to back, so they share that XCD's L2 and the tiles that
+// exist (the first *ntiles_dev of a grid sized for the maximum) are spread evenly over the XCDs. The launcher pads
+// the grid's tile count to a multiple of 8.
+__device__ __forceinline__ void tile_block(int nbx, int& bx, int& by) {
+  const int lin = blockIdx.y * nbx + blockIdx.x, k = lin >> 3;
+  by = (k / nbx) * 8 + (lin & 7);
+  bx = k % nbx;
+}
+inline dim3 tile_grid(int nbx, int ntiles) { return dim3(unsigned(nbx), unsigned((ntiles + 7) / 8 * 8)); }
+
+}  // namespace unholy::kernels::pipe
