@@ -72,6 +72,10 @@ struct MxGlu {
   uint32_t* counters = nullptr;
   uint8_t* hq = nullptr;
   uint8_t* hs = nullptr;
+  // Extension (no reference counterpart): SwiGLU rows h = bf16(w * silu(g) * u) [P, N] without the per-128 fp8
+  // requantization, for a consumer that quantizes them itself (mx_grouped_gemv_x on h gives the codes of hh exactly).
+  // Excludes hh / hq; the GEMV then needs no whole-block workgroups.
+  bf16* h = nullptr;
 };
 bool mx_gemm_glu();
 void mx_gemm_force_glu(int on);

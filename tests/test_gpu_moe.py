@@ -188,3 +188,44 @@ def test_dispatch_small_with_routing(mode):
     assert np.array_equal(bufs["pidx"].download((T, K), np.int32), ref["pidx"])
     assert plan[2] == ref["plan"][2]
     assert np.array_equal(bufs["tiles"].download((max_tiles, 3), np.int32)[: plan[2]], ref["tiles"])
+
+
+@pytest.mark.parametrize("T,E,K,D,I", [(8, 32, 6, 1024, 512), (64, 48, 6, 512, 256)])
+def test_forward_matches_composed_entry_points(T, E, K, D, I):
+    """uh_mx_moe_forward (T <= 64: SwiGLU rows h left unquantized, quantized by the w2 GEMV while staging) against
+    the flow composed from the public entry points with the requantizing epilogue (dispatch, w1/w3 GEMV writing
+    hq / hs, w2 GEMV on those codes, combine): bit for bit."""
+    rng = np.random.default_rng(5 * T + E)
+    limit = 10.0
+    experts, bufs, tab, x, logits = _moe_case(rng, T, E, K, D, I)
+    P, tile_rows = T * K, 16
+    ws_bytes = call("uh_mx_moe_workspace_size", T, K, E, D, I)
+    ws, out = DeviceBuffer(ws_bytes), DeviceBuffer(T * D * 2)
+    sel, wt = DeviceBuffer(P * 4), DeviceBuffer(P * 4)
+    dx = dev(x)
+    call("uh_mx_moe_forward", dx, dev(logits), T, K, E, D, I, tab.ptr, limit, ws.ptr, ws_bytes, out.ptr, sel.ptr,
+         wt.ptr, None)
+    max_tiles = P + E
+    b = dict(plan=DeviceBuffer(20), tiles=DeviceBuffer(max_tiles * 12), eidx=DeviceBuffer(P * 4),
+             ewt=DeviceBuffer(P * 4), row_expert=DeviceBuffer(P * 4), pidx=DeviceBuffer(P * 4))
+    if T <= 32:
+        call("uh_moe_dispatch_small", sel, wt, T, K, E, P, max_tiles, tile_rows, b["plan"].ptr, b["tiles"].ptr,
+             b["eidx"].ptr, b["ewt"].ptr, b["row_expert"].ptr, b["pidx"].ptr, None, None, None, 0.0, None, None,
+             None, None, None, 0, None)
+    else:
+        count, off, fill = DeviceBuffer(E * 4), DeviceBuffer(E * 4), DeviceBuffer(E * 4)
+        count.zero()
+        call("uh_moe_count", sel, T, K, count, E, None, None)
+        call("uh_moe_plan", count, None, E, P, b["plan"], b["tiles"], None, off, fill, max_tiles, None, tile_rows)
+        call("uh_moe_scatter", sel, wt, T, K, off, fill, b["eidx"], b["ewt"], b["row_expert"], b["pidx"], None)
+    nt = int(b["plan"].download(5, np.int32)[2])
+    w1, s1, w3, s3, w2, s2 = (pointer_table(lst) for lst in bufs)
+    hq, hs, pair = DeviceBuffer(P * I), DeviceBuffer(P * (I // 128)), DeviceBuffer(P * D * 2)
+    call("uh_mx_grouped_gemv_x", dx, D, b["eidx"], D, b["tiles"], nt, w1, s1, None, I, I, None, None, w3, s3, None,
+         tile_rows, b["ewt"], b["row_expert"], s2, None, hq, hs, limit)
+    call("uh_mx_grouped_gemv_q", hq, hs, I, b["tiles"], nt, w2, s2, pair, D, D, None, None, None, None, None,
+         tile_rows, None, None, None, None, None, None, 0.0)
+    comp = DeviceBuffer(T * D * 2)
+    call("uh_moe_combine", pair, b["pidx"], None, comp, T, K, D, None)
+    synchronize()
+    assert np.array_equal(out.download((T, D), np.uint16), comp.download((T, D), np.uint16))

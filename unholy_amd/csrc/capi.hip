@@ -72,6 +72,7 @@ struct MoeWs {
   int32_t *count, *off, *fill, *plan, *tiles, *eidx, *row_expert, *pidx, *sel;
   float *ewt, *wt;
   uint8_t *xq, *xs, *hq, *hs;
+  bf16* h;  // raw SwiGLU rows [P, I] (T <= 64 path); shares xq's bytes (P * D >= P * I * 2), which only prefill uses
   bf16* pair_out;
   size_t bytes;
   int max_tiles, tile_rows;
@@ -99,6 +100,8 @@ MoeWs carve(char* base, int T, int K, int E, int D, int I) {
   w.ewt = reinterpret_cast<float*>(take(P * 4));
   w.wt = reinterpret_cast<float*>(take(P * 4));
   w.xq = reinterpret_cast<uint8_t*>(take(P * D));
+  w.h = reinterpret_cast<bf16*>(w.xq);
+  if (size_t(D) < size_t(I) * 2) w.h = reinterpret_cast<bf16*>(take(P * I * 2));
   w.xs = reinterpret_cast<uint8_t*>(take(P * (D / 128)));
   w.hq = reinterpret_cast<uint8_t*>(take(P * I));
   w.hs = reinterpret_cast<uint8_t*>(take(P * (I / 128)));
@@ -473,13 +476,20 @@ int uh_mx_moe_forward_ev(const uint16_t* x, const float* logits, int T, int K, i
     }
     mark(1);
     const k::MxGlu glu{w.ewt, w.row_expert, t(2, 1), nullptr, limit, nullptr, w.hq, w.hs};
-    if (T <= 64) {  // the input quantization happens in the GEMV's staging
+    if (T <= 64) {
+      // Both GEMVs quantize their inputs while staging them: x rows per 128 for w1 / w3, and for w2 the raw SwiGLU
+      // rows h, whose act_quant codes are exactly those of the fake-quantized hh. A tile holds at most one row per
+      // token, so min(tile_rows, T) rows bound the staging.
+      k::MxGlu gh = glu;
+      gh.hq = gh.hs = nullptr;
+      gh.h = w.h;
+      const int rows = std::min(w.tile_rows, T);
       mark(2);
       k::mx_grouped_gemv_x(x, D, w.eidx, D, tiles, w.max_tiles, t(0, 0), t(0, 1), nullptr, I, I, st, ntd, t(1, 0),
-                           t(1, 1), nullptr, w.tile_rows, glu);
+                           t(1, 1), nullptr, rows, gh);
       mark(3);
-      k::mx_grouped_gemv_q(w.hq, w.hs, I, tiles, w.max_tiles, t(2, 0), t(2, 1), w.pair_out, D, D, st, ntd, nullptr,
-                           nullptr, nullptr, w.tile_rows);
+      k::mx_grouped_gemv_x(w.h, I, nullptr, I, tiles, w.max_tiles, t(2, 0), t(2, 1), w.pair_out, D, D, st, ntd,
+                           nullptr, nullptr, nullptr, rows, k::MxGlu{});
     } else {  // quantized once (each tile's rows are read by all its column blocks), then the fp8 GEMM
       k::mx_xform_in_fp8(x, D, w.row_expert, t(0, 1), w.xq, w.xs, P, D, st, w.eidx);
       mark(2);

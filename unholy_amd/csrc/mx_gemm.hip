@@ -651,6 +651,7 @@ MxGemvArgs gemm_args(const bf16* xa, const uint8_t* q, const uint8_t* qs, int K,
                      const int* ntiles_dev, const uint8_t* const* w_tab2, const uint8_t* const* s_tab2, bf16* out2,
                      const MxGlu& glu) {
   if (!w_tab || !s_tab) throw std::runtime_error("mx_grouped_gemm: null tables");
+  if (glu.h) throw std::runtime_error("mx_grouped_gemm: MxGlu h (raw rows) is a GEMV option");
   if (!w_tab2 != !s_tab2) throw std::runtime_error("mx_grouped_gemm: second projection tables");
   MxGemvArgs a{};
   a.xa = xa;

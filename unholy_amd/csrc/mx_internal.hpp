@@ -32,6 +32,7 @@ struct MxGemvArgs {
   uint16_t* hh;
   uint8_t* hq;
   uint8_t* hs;
+  uint16_t* hraw;  // SwiGLU rows as bf16, not requantized (MxGlu::h)
   float limit;
 };
 

@@ -90,9 +90,12 @@ constexpr int GV_WAVES = 8, GV_NT = 64 * GV_WAVES, GV_PAD = 16, GV_MAXROWS = 16,
 
 // AM: activation source -- 0: e4m3 codes + e8m0 scales (aq, as); 1: fake-quantized bf16 rows (xa), codes recovered
 // exactly; 2: raw bf16 token rows x[x_rows[r]] quantized here with the reference's act_quant (mx_xform_in_fp8 fused).
-// OCC: waves per SIMD the register budget is sized for (4: two workgroups per CU).
-template <int NP, bool GLU, int AM, int OCC>
-__global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(OCC))) void mx_gemv_kernel(MxGemvArgs a) {
+// GM: epilogue -- 0: plain outputs; 1: SwiGLU + fp8 requantization of each row's 128-output block (W = 8 waves
+// cover the block); 2: SwiGLU to raw bf16 rows h (no requantization: the consumer quantizes them while staging).
+// W: waves per workgroup (16 outputs each).
+template <int NP, int GM, int AM, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void mx_gemv_kernel(MxGemvArgs a) {
+  constexpr int NT = 64 * W;
   extern __shared__ __align__(16) uint8_t smem[];
   if (a.ntiles_dev && int(blockIdx.y) >= *a.ntiles_dev) return;
   const Exl3Tile tile = a.tiles[blockIdx.y];
@@ -112,7 +115,7 @@ __global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(OCC))) vo
   uint8_t* sA = smem;
   uint8_t* sS = smem + size_t(a.rows_cap) * ldA;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nl = lane & 15, g = lane >> 4;
-  const int nt = blockIdx.x * GV_WAVES + wave;
+  const int nt = blockIdx.x * W + wave;
   const bool active = nt < ntn;  // uniform per wave
   const int boff = nl * 32 + (g & 1) * 16, soff = nl * 2 + (g & 1);
   for (int rg = 0; rg < tile.rows; rg += a.rows_cap) {
@@ -126,9 +129,9 @@ __global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(OCC))) vo
     const uint32_t cstep = uint32_t(2 * ntn * 512), sstep = uint32_t(2 * ntn * 32);
     const auto load_step = [&](int s, int slot) {
 #pragma unroll
-      for (int p = 0; p < NP; ++p) {
-        bq[slot][p] = *reinterpret_cast<gptr<v4i>>(as_global(wp[p]) + (cofs + uint32_t(s) * cstep));
-        sq[slot][p] = *(as_global(sp[p]) + (sofs + uint32_t(s) * sstep));
+      for (int p = 0; p < NP; ++p) {  // streamed once per launch: nontemporal loads (~12% more read bandwidth)
+        bq[slot][p] = __builtin_nontemporal_load(reinterpret_cast<gptr<v4i>>(as_global(wp[p]) + (cofs + uint32_t(s) * cstep)));
+        sq[slot][p] = __builtin_nontemporal_load(as_global(sp[p]) + (sofs + uint32_t(s) * sstep));
       }
     };
     if (active)
@@ -138,7 +141,7 @@ __global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(OCC))) vo
     if constexpr (AM != 0) {
       // 8 values per thread; 16 consecutive threads hold one 128-block (K / 8 is a multiple of 16).
       const int total = M * (K / 8);
-      for (int base = 0; base < total; base += GV_NT) {
+      for (int base = 0; base < total; base += NT) {
         const int i = base + tid, m = i / (K / 8), c = (i % (K / 8)) * 8;
         const bool valid = i < total;
         float v[8];
@@ -183,11 +186,11 @@ __global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(OCC))) vo
       }
     } else {
       const int total = M * (K / 16);
-      for (int i = tid; i < total; i += GV_NT) {
+      for (int i = tid; i < total; i += NT) {
         const int m = i / (K / 16), c = (i % (K / 16)) * 16;
         *reinterpret_cast<uint4*>(sA + m * ldA + c) = *reinterpret_cast<const uint4*>(a.aq + (row0 + m) * K + c);
       }
-      for (int i = tid; i < M * KS; i += GV_NT) sS[i] = a.as[row0 * KS + i];
+      for (int i = tid; i < M * KS; i += NT) sS[i] = a.as[row0 * KS + i];
     }
     __syncthreads();
 
@@ -197,42 +200,44 @@ __global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(OCC))) vo
     const bool arow = nl < M;
     const uint8_t* ap = sA + nl * ldA + g * 32;
     const uint8_t* asp = sS + nl * KS;
+    // One step: the lane's activation inputs 32g .. 32g + 31 of step s (row nl), dequantized to bf16 once for both
+    // projections, then MFMA sub-step t on inputs 32g + 8t .. + 7 of both operands; weights from ring slot i.
+    const auto step = [&](int s, int i) {
+      bf16x8 af[4];
+      if (arow) {
+        const v4i lo = *reinterpret_cast<const v4i*>(ap + s * 128);
+        const v4i hi = *reinterpret_cast<const v4i*>(ap + s * 128 + 16);
+        const float sc = e8m0_to_f32(asp[s]);
+        af[0] = fp8x8_to_bf16(lo[0], lo[1], sc);
+        af[1] = fp8x8_to_bf16(lo[2], lo[3], sc);
+        af[2] = fp8x8_to_bf16(hi[0], hi[1], sc);
+        af[3] = fp8x8_to_bf16(hi[2], hi[3], sc);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) af[t] = bf16x8{};
+      }
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const float sc = __uint_as_float(sq[i][p] << 23);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[p] = mfma_bf16(af[t], fp4x8_to_bf16(uint32_t(bq[i][p][t]), sc), acc[p]);
+      }
+    };
     if (active)
       for (int s0 = 0; s0 < KS; s0 += GV_PF) {
 #pragma unroll
         for (int i = 0; i < GV_PF; ++i) {
-          const int s = s0 + i;
-          if (s < KS) {
-          // The lane's activation inputs 32g .. 32g + 31 of the step (row nl), dequantized to bf16 once for both
-          // projections; MFMA sub-step t takes inputs 32g + 8t .. + 7 on both operands.
-          bf16x8 af[4];
-          if (arow) {
-            const v4i lo = *reinterpret_cast<const v4i*>(ap + s * 128);
-            const v4i hi = *reinterpret_cast<const v4i*>(ap + s * 128 + 16);
-            const float sc = e8m0_to_f32(asp[s]);
-            af[0] = fp8x8_to_bf16(lo[0], lo[1], sc);
-            af[1] = fp8x8_to_bf16(lo[2], lo[3], sc);
-            af[2] = fp8x8_to_bf16(hi[0], hi[1], sc);
-            af[3] = fp8x8_to_bf16(hi[2], hi[3], sc);
-          } else {
-#pragma unroll
-            for (int t = 0; t < 4; ++t) af[t] = bf16x8{};
-          }
-#pragma unroll
-          for (int p = 0; p < NP; ++p) {
-            const float sc = __uint_as_float(sq[i][p] << 23);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) acc[p] = mfma_bf16(af[t], fp4x8_to_bf16(uint32_t(bq[i][p][t]), sc), acc[p]);
-          }
-          }
-          load_step(min(s + GV_PF, KS - 1), i);  // unconditional: past the end it re-reads the last step (cached)
-          // Keep each step's conversions and MFMAs together: interleaving the unrolled steps would only
-          // raise register pressure (the loads of later steps are already in flight).
+          if (s0 + i < KS) step(s0 + i, i);
+          // Unconditional (past the end it re-reads the last step): a conditional load would leave the compiler
+          // unsure how many loads are outstanding, and it would then wait for all of them at every round.
+          load_step(min(s0 + i + GV_PF, KS - 1), i);
+          // Keep each step's conversions and MFMAs together: interleaving the unrolled steps would only raise
+          // register pressure (the loads of later steps are already in flight).
           __builtin_amdgcn_sched_barrier(0);
         }
       }
 
-    if constexpr (!GLU) {
+    if constexpr (GM == 0) {
       if (active)
 #pragma unroll
         for (int p = 0; p < NP; ++p)
@@ -244,10 +249,23 @@ __global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(OCC))) vo
             if (p == 0 && a.out32) a.out32[o] = acc[p][i];
             else a.out[p][o] = f32_to_bf16(acc[p][i]);
           }
+    } else if constexpr (GM == 2) {
+      if (active)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 4 * g + i;
+          if (r >= M) continue;
+          const size_t row = row0 + r, col = size_t(nt) * 16 + nl;
+          if (a.gs_tab && !a.gs_tab[a.grow_expert[row]]) continue;
+          const float gv = round_bf16(acc[0][i]), uv = round_bf16(acc[NP - 1][i]);
+          if (a.out[0]) a.out[0][row * a.ldo + col] = f32_to_bf16(gv);
+          if (a.out[1]) a.out[1][row * a.ldo + col] = f32_to_bf16(uv);
+          a.hraw[row * N + col] = f32_to_bf16(swiglu_value(gv, uv, a.gw ? a.gw[row] : 0.0f, a.gw != nullptr, a.limit));
+        }
     } else {
       // SwiGLU of the bf16-rounded projections, then the fake quantization of each row's 128 outputs (the whole
       // workgroup: N % 128 == 0 is checked on the host) with the row's amax gathered over the 8 waves.
-      __shared__ float red[GV_WAVES][16];
+      __shared__ float red[W][16];
       float h[4], am[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -272,7 +290,7 @@ __global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(OCC))) vo
         if (a.gs_tab && !a.gs_tab[a.grow_expert[row]]) continue;
         float rm = red[0][r];
 #pragma unroll
-        for (int w = 1; w < GV_WAVES; ++w) rm = fmaxf(rm, red[w][r]);
+        for (int w = 1; w < W; ++w) rm = fmaxf(rm, red[w][r]);
         const Fp8Block blk = fp8_block_scale(rm);
         const size_t col = size_t(nt) * 16 + nl;
         const uint8_t c = fp8_code(h[i], blk);
@@ -363,22 +381,24 @@ void set_lds_limit(K kernel, size_t bytes) {
                                                   hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes)));
 }
 
-int gemv_occ() {
-  static const int v = [] {
-    const char* e = std::getenv("UH_GEMV_OCC");
-    return e ? std::atoi(e) : 2;
-  }();
-  return v;
-}
-
-template <int NP, bool GLU, int AM>
-void launch_gemv_t(const MxGemvArgs& a, int ntiles, hipStream_t st) {
+// Workgroup shape per launch: a requantizing epilogue needs a whole 128-output block (8 waves). Otherwise, when the
+// staged activations are small (decode tiles), 4-wave workgroups: twice as many, smaller work items, which balance
+// better over the CUs, with three workgroups per CU. Larger tiles keep 8 waves, so that two workgroups still fit a
+// CU's LDS.
+template <int NP, int GM, int AM, int W>
+void launch_gemv_w(const MxGemvArgs& a, int ntiles, hipStream_t st) {
   const size_t lds = size_t(a.rows_cap) * (a.K + GV_PAD) + size_t(a.rows_cap) * (a.K / 128);
-  auto* kern = gemv_occ() >= 4 ? &mx_gemv_kernel<NP, GLU, AM, 4> : &mx_gemv_kernel<NP, GLU, AM, 2>;
+  auto* kern = &mx_gemv_kernel<NP, GM, AM, W>;
   set_lds_limit(kern, lds);
-  const dim3 grid(cdiv(size_t(a.N) / 16, GV_WAVES), unsigned(ntiles), 1);
-  kern<<<grid, GV_NT, lds, st>>>(a);
+  const dim3 grid(cdiv(size_t(a.N) / 16, W), unsigned(ntiles), 1);
+  kern<<<grid, 64 * W, lds, st>>>(a);
   UH_CHECK_LAUNCH();
+}
+template <int NP, int GM, int AM>
+void launch_gemv_t(const MxGemvArgs& a, int ntiles, hipStream_t st) {
+  if constexpr (GM == 1) launch_gemv_w<NP, GM, AM, 8>(a, ntiles, st);
+  else if (size_t(a.rows_cap) * (a.K + GV_PAD) <= 36 * 1024) launch_gemv_w<NP, GM, AM, 4>(a, ntiles, st);
+  else launch_gemv_w<NP, GM, AM, 8>(a, ntiles, st);
 }
 
 }  // namespace
@@ -388,20 +408,24 @@ void launch_mx_gemv(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st) 
   if (ntiles <= 0) return;
   if (a.K % 128 || a.N % 16 || a.K <= 0 || a.N <= 0) throw std::runtime_error("mx_grouped_gemv: K % 128 or N % 16");
   if (a.rows_cap < 1 || a.rows_cap > GV_MAXROWS) throw std::runtime_error("mx_grouped_gemv: rows_cap");
-  const bool np2 = a.w_tab[1] != nullptr, glu = a.hh || a.hq;
+  const bool np2 = a.w_tab[1] != nullptr, glu = a.hh || a.hq, graw = a.hraw != nullptr;
+  if (glu && graw) throw std::runtime_error("mx_grouped_gemv: MxGlu h (raw) excludes hh / hq");
+  if (graw && !np2) throw std::runtime_error("mx_grouped_gemv: glu needs two projections");
   if (glu && (!np2 || a.N % 128)) throw std::runtime_error("mx_grouped_gemv: glu needs two projections, N % 128");
   if (glu && a.hq && !a.hs) throw std::runtime_error("mx_grouped_gemv: glu hq without hs");
   if (amode ? !a.xa : (!a.aq || !a.as)) throw std::runtime_error("mx_grouped_gemv: null activations");
   if (amode == 2 && a.ldx % 8) throw std::runtime_error("mx_grouped_gemv: ldx % 8 (16-byte row loads)");
-  if (!glu && ((!a.out[0] && !a.out32) || (np2 && !a.out[1]))) throw std::runtime_error("mx_grouped_gemv: null output");
+  if (!glu && !graw && ((!a.out[0] && !a.out32) || (np2 && !a.out[1])))
+    throw std::runtime_error("mx_grouped_gemv: null output");
   if (!a.tiles) throw std::runtime_error("mx_grouped_gemv: null tiles");
 #define UH_GV(NP, GLU)                                                       \
   (amode == 2   ? launch_gemv_t<NP, GLU, 2>(a, ntiles, st)                     \
    : amode == 1 ? launch_gemv_t<NP, GLU, 1>(a, ntiles, st)                     \
                 : launch_gemv_t<NP, GLU, 0>(a, ntiles, st))
-  if (glu) UH_GV(2, true);
-  else if (np2) UH_GV(2, false);
-  else UH_GV(1, false);
+  if (glu) UH_GV(2, 1);
+  else if (graw) UH_GV(2, 2);
+  else if (np2) UH_GV(2, 0);
+  else UH_GV(1, 0);
 #undef UH_GV
 }
 
@@ -516,8 +540,9 @@ MxGemvArgs gemv_args(const bf16* xa, const uint8_t* q, const uint8_t* qs, int K,
   a.hh = glu.hh;
   a.hq = glu.hq;
   a.hs = glu.hs;
+  a.hraw = glu.h;
   a.limit = glu.limit;
-  if ((a.hh || a.hq) && a.gs_tab && !a.grow_expert) throw std::runtime_error("MxGlu: s_tab without row_expert");
+  if ((a.hh || a.hq || a.hraw) && a.gs_tab && !a.grow_expert) throw std::runtime_error("MxGlu: s_tab without row_expert");
   if (!w_tab || !s_tab) throw std::runtime_error("mx grouped: null tables");
   if (!w_tab2 != !s_tab2) throw std::runtime_error("mx grouped: second projection tables");
   return a;
