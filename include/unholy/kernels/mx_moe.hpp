@@ -126,10 +126,11 @@ void mx_grouped_gemm_x(const bf16* x, int ldx, const int32_t* x_rows, int K, con
 void mx_grouped_gemv_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles, int ntiles,
                               const uint8_t* const* w_tab, const uint8_t* const* s_tab, float* out, int ldo, int N,
                               hipStream_t st, const int* ntiles_dev = nullptr, int max_rows = kMxGemvTileRows);
+// x_rows (optional): pair row r reads row x_rows[r] of q / qs (token rows quantized once, gathered by the loads).
 void mx_grouped_gemm_q(const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles, int ntiles,
                        const uint8_t* const* w_tab, const uint8_t* const* s_tab, bf16* out, int ldo, int N,
                        hipStream_t st, const int* ntiles_dev = nullptr, const uint8_t* const* w_tab2 = nullptr,
                        const uint8_t* const* s_tab2 = nullptr, bf16* out2 = nullptr, int max_rows = kExl3TileRows,
-                       const MxGlu& glu = {});
+                       const MxGlu& glu = {}, const int32_t* x_rows = nullptr);
 
 }  // namespace unholy::kernels

@@ -190,15 +190,16 @@ def test_dispatch_small_with_routing(mode):
     assert np.array_equal(bufs["tiles"].download((max_tiles, 3), np.int32)[: plan[2]], ref["tiles"])
 
 
-@pytest.mark.parametrize("T,E,K,D,I", [(8, 32, 6, 1024, 512), (64, 48, 6, 512, 256)])
+@pytest.mark.parametrize("T,E,K,D,I", [(8, 32, 6, 1024, 512), (64, 48, 6, 512, 256), (200, 16, 4, 512, 256)])
 def test_forward_matches_composed_entry_points(T, E, K, D, I):
-    """uh_mx_moe_forward (T <= 64: SwiGLU rows h left unquantized, quantized by the w2 GEMV while staging) against
-    the flow composed from the public entry points with the requantizing epilogue (dispatch, w1/w3 GEMV writing
-    hq / hs, w2 GEMV on those codes, combine): bit for bit."""
+    """uh_mx_moe_forward against the flow composed from the public entry points, bit for bit. T <= 64: the forward
+    leaves the SwiGLU rows h unquantized for the w2 GEMV to quantize while staging; the composed flow uses the
+    requantizing epilogue (w1/w3 GEMV writing hq / hs, w2 GEMV on those codes). T > 64: the forward quantizes each
+    token row once and the GEMM gathers the pair rows; the composed flow quantizes the gathered pair rows."""
     rng = np.random.default_rng(5 * T + E)
     limit = 10.0
     experts, bufs, tab, x, logits = _moe_case(rng, T, E, K, D, I)
-    P, tile_rows = T * K, 16
+    P, tile_rows = T * K, (16 if T <= 64 else 128)
     ws_bytes = call("uh_mx_moe_workspace_size", T, K, E, D, I)
     ws, out = DeviceBuffer(ws_bytes), DeviceBuffer(T * D * 2)
     sel, wt = DeviceBuffer(P * 4), DeviceBuffer(P * 4)
@@ -221,10 +222,18 @@ def test_forward_matches_composed_entry_points(T, E, K, D, I):
     nt = int(b["plan"].download(5, np.int32)[2])
     w1, s1, w3, s3, w2, s2 = (pointer_table(lst) for lst in bufs)
     hq, hs, pair = DeviceBuffer(P * I), DeviceBuffer(P * (I // 128)), DeviceBuffer(P * D * 2)
-    call("uh_mx_grouped_gemv_x", dx, D, b["eidx"], D, b["tiles"], nt, w1, s1, None, I, I, None, None, w3, s3, None,
-         tile_rows, b["ewt"], b["row_expert"], s2, None, hq, hs, limit)
-    call("uh_mx_grouped_gemv_q", hq, hs, I, b["tiles"], nt, w2, s2, pair, D, D, None, None, None, None, None,
-         tile_rows, None, None, None, None, None, None, 0.0)
+    if T <= 64:
+        call("uh_mx_grouped_gemv_x", dx, D, b["eidx"], D, b["tiles"], nt, w1, s1, None, I, I, None, None, w3, s3,
+             None, tile_rows, b["ewt"], b["row_expert"], s2, None, hq, hs, limit)
+        call("uh_mx_grouped_gemv_q", hq, hs, I, b["tiles"], nt, w2, s2, pair, D, D, None, None, None, None, None,
+             tile_rows, None, None, None, None, None, None, 0.0)
+    else:
+        xq, xs = DeviceBuffer(P * D), DeviceBuffer(P * (D // 128))
+        call("uh_mx_xform_in_fp8", dx, D, None, None, xq, xs, P, D, None, b["eidx"])
+        call("uh_mx_grouped_gemm_q", xq, xs, D, b["tiles"], nt, w1, s1, None, I, I, None, None, w3, s3, None,
+             tile_rows, b["ewt"], b["row_expert"], s2, None, hq, hs, limit)
+        call("uh_mx_grouped_gemm_q", hq, hs, I, b["tiles"], nt, w2, s2, pair, D, D, None, None, None, None, None,
+             tile_rows, None, None, None, None, None, None, 0.0)
     comp = DeviceBuffer(T * D * 2)
     call("uh_moe_combine", pair, b["pidx"], None, comp, T, K, D, None)
     synchronize()

@@ -490,11 +490,13 @@ int uh_mx_moe_forward_ev(const uint16_t* x, const float* logits, int T, int K, i
       mark(3);
       k::mx_grouped_gemv_x(w.h, I, nullptr, I, tiles, w.max_tiles, t(2, 0), t(2, 1), w.pair_out, D, D, st, ntd,
                            nullptr, nullptr, nullptr, rows, k::MxGlu{});
-    } else {  // quantized once (each tile's rows are read by all its column blocks), then the fp8 GEMM
-      k::mx_xform_in_fp8(x, D, w.row_expert, t(0, 1), w.xq, w.xs, P, D, st, w.eidx);
+    } else {
+      // Each token row quantized once (its K picks would otherwise be quantized K times); the GEMM's loads gather
+      // the pair rows' codes through eidx.
+      k::mx_xform_in_fp8(x, D, nullptr, nullptr, w.xq, w.xs, T, D, st, nullptr);
       mark(2);
       k::mx_grouped_gemm_q(w.xq, w.xs, D, tiles, w.max_tiles, t(0, 0), t(0, 1), nullptr, I, I, st, ntd, t(1, 0), t(1, 1),
-                           nullptr, w.tile_rows, glu);
+                           nullptr, w.tile_rows, glu, w.eidx);
       mark(3);
       k::mx_grouped_gemm_q(w.hq, w.hs, I, tiles, w.max_tiles, t(2, 0), t(2, 1), w.pair_out, D, D, st, ntd, nullptr,
                            nullptr, nullptr, w.tile_rows);

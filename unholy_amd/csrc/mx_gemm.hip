@@ -385,15 +385,17 @@ __global__ __launch_bounds__(512) void mx_gemm_pipe_kernel(MxGemvArgs a) {
     __syncthreads();  // the previous row group's LDS use is over
     for (int e = tid; e < 128 * KS; e += 512) {
       const int r = min(e & 127, M - 1), s = e >> 7;
-      as_lds[e] = a.as[(row0 + r) * KS + s];
+      as_lds[e] = a.as[size_t(a.x_rows ? a.x_rows[row0 + r] : int(row0 + r)) * KS + s];
     }
     uint32_t aoff[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int slot = (wave * 2 + i) * 64 + lane, r = slot >> 3, p = (slot & 7) ^ (r & 7);
-      aoff[i] = uint32_t(min(r, M - 1)) * uint32_t(K) + uint32_t(p * 16);  // rows past the tile repeat its last
+      // Rows past the tile repeat its last. With x_rows the loads gather token rows (offsets from q itself).
+      const int rr = min(r, M - 1);
+      aoff[i] = (a.x_rows ? uint32_t(a.x_rows[row0 + rr]) : uint32_t(rr)) * uint32_t(K) + uint32_t(p * 16);
     }
-    const uint8_t* arow = a.aq + row0 * size_t(K);
+    const uint8_t* arow = a.x_rows ? a.aq : a.aq + row0 * size_t(K);
     const auto issue = [&](int s) {
       const uint32_t st = __builtin_amdgcn_readfirstlane(lds0 + uint32_t((s % GP_S) * GP_STAGE));
       dma16(arow + s * 128, aoff[0], st + uint32_t(wave * 2) * 1024);
@@ -629,6 +631,8 @@ void launch_mx_gemm(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st) 
    : amode == 1 ? launch_gemm_t<NP, 1>(a, ntiles, st)                   \
                 : launch_gemm_t<NP, 0>(a, ntiles, st))
   const bool pipe = amode == 0 && a.K / GM_KS <= GP_MAX_KS && !pipe_disabled();
+  if (amode == 0 && a.x_rows && (!pipe || (!glu && a.N % 256)))
+    throw std::runtime_error("mx_grouped_gemm_q: x_rows needs the pipelined kernel (K <= 28672, N % 256 without glu)");
   if (glu) {
     if (pipe) launch_pipe_t<2>(a, ntiles, st);
     else UH_GM(2);
@@ -691,9 +695,10 @@ void mx_grouped_gemm(const bf16* xa, int K, const Exl3Tile* tiles, int ntiles, c
 void mx_grouped_gemm_q(const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles, int ntiles,
                        const uint8_t* const* w_tab, const uint8_t* const* s_tab, bf16* out, int ldo, int N,
                        hipStream_t st, const int* ntiles_dev, const uint8_t* const* w_tab2,
-                       const uint8_t* const* s_tab2, bf16* out2, int, const MxGlu& glu) {
-  launch_mx_gemm(gemm_args(nullptr, q, qs, K, tiles, w_tab, s_tab, out, ldo, N, ntiles_dev, w_tab2, s_tab2, out2, glu),
-                 ntiles, 0, st);
+                       const uint8_t* const* s_tab2, bf16* out2, int, const MxGlu& glu, const int32_t* x_rows) {
+  MxGemvArgs a = gemm_args(nullptr, q, qs, K, tiles, w_tab, s_tab, out, ldo, N, ntiles_dev, w_tab2, s_tab2, out2, glu);
+  a.x_rows = x_rows;
+  launch_mx_gemm(a, ntiles, 0, st);
 }
 
 void mx_grouped_gemm_x(const bf16* x, int ldx, const int32_t* x_rows, int K, const Exl3Tile* tiles, int ntiles,

@@ -75,6 +75,63 @@ __global__ __launch_bounds__(256) void mx_transform_kernel(const bf16* __restric
   }
 }
 
+// The same transforms with 8 values per thread: 16 consecutive threads cover one 128-value segment (16-byte loads,
+// 8- or 16-byte stores), its amax a DPP row max. The item loop has a uniform bound so that every 16-lane group is
+// whole; threads past the end work on the last item and store nothing. Needs 16-byte aligned rows (ldx % 8 == 0).
+template <int kMode>
+__global__ __launch_bounds__(256) void mx_transform8_kernel(const bf16* __restrict__ x, int ldx,
+                                                            const int32_t* __restrict__ x_rows,
+                                                            const bf16* __restrict__ u, const float* __restrict__ w,
+                                                            float limit, const int32_t* __restrict__ row_expert,
+                                                            const uint8_t* const* __restrict__ s_tab,
+                                                            bf16* __restrict__ out, uint8_t* __restrict__ q,
+                                                            uint8_t* __restrict__ qs, int K, int P) {
+  const int segs = K / 128;
+  const size_t per_row = size_t(segs) * 16, items = size_t(P) * per_row;
+  for (size_t base = size_t(blockIdx.x) * 256; base < items; base += size_t(gridDim.x) * 256) {
+    const size_t it = min(base + threadIdx.x, items - 1);
+    const int r = int(it / per_row), rem = int(it % per_row), seg = rem >> 4, k0 = seg * 128 + (rem & 15) * 8;
+    float v[8];
+    if constexpr (kMode == 2) {
+      const uint4 graw = *reinterpret_cast<const uint4*>(x + size_t(r) * ldx + k0);
+      const uint4 uraw = *reinterpret_cast<const uint4*>(u + size_t(r) * ldx + k0);
+      const uint32_t gw[4] = {graw.x, graw.y, graw.z, graw.w}, uw[4] = {uraw.x, uraw.y, uraw.z, uraw.w};
+      const float wr = w ? w[r] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        v[i] = round_bf16(swiglu_value(bf16_to_f32(uint16_t(gw[i / 2] >> (16 * (i % 2)))),
+                                       bf16_to_f32(uint16_t(uw[i / 2] >> (16 * (i % 2)))), wr, w != nullptr, limit));
+    } else {
+      const size_t src = x_rows ? size_t(x_rows[r]) : size_t(r);
+      const uint4 raw = *reinterpret_cast<const uint4*>(x + src * ldx + k0);
+      const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float(rw[i] << 16);
+        v[2 * i + 1] = __uint_as_float(rw[i] & 0xffff0000u);
+      }
+    }
+    float am = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
+    const Fp8Block b = fp8_block_scale(row16_max(am));
+    if (base + threadIdx.x >= items || (s_tab && !s_tab[row_expert[r]])) continue;
+    uint32_t c[2] = {0, 0}, h[4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint8_t code = fp8_code(v[i], b);
+      c[i / 4] |= uint32_t(code) << (8 * (i % 4));
+      const uint32_t f = f32_to_bf16(e4m3_to_f32(code) * b.sc);
+      h[i / 2] = (i % 2) ? (h[i / 2] | f << 16) : f;
+    }
+    if (out) *reinterpret_cast<uint4*>(out + size_t(r) * K + k0) = make_uint4(h[0], h[1], h[2], h[3]);
+    if (q) {
+      *reinterpret_cast<uint2*>(q + size_t(r) * K + k0) = make_uint2(c[0], c[1]);
+      if ((rem & 15) == 0) qs[size_t(r) * segs + seg] = b.se;
+    }
+  }
+}
+
 unsigned transform_blocks(int P, int K) { return unsigned(std::min<size_t>((size_t(P) * (K / 128) + 3) / 4, 16384)); }
 
 // ---- grouped GEMV ----------------------------------------------------------------------------------------------------
@@ -436,6 +493,16 @@ void launch_mx_transform(int mode, const bf16* x, int ldx, const int32_t* x_rows
   if (K % 128) throw std::runtime_error("mx transform: K % 128");
   if (ldx % 2) throw std::runtime_error("mx transform: ldx must be even (4-byte row pairs)");
   if (s_tab && !row_expert) throw std::runtime_error("mx transform: s_tab without row_expert");
+  if (ldx % 8 == 0) {  // 16-byte rows: the 8-values-per-thread kernel
+    const unsigned b8 = unsigned(std::min<size_t>((size_t(P) * (K / 8) + 255) / 256, 8192));
+    if (mode == 2)
+      mx_transform8_kernel<2><<<b8, 256, 0, st>>>(x, ldx, nullptr, u, w, limit, row_expert, s_tab, out, q, qs, K, P);
+    else
+      mx_transform8_kernel<0><<<b8, 256, 0, st>>>(x, ldx, x_rows, nullptr, nullptr, 0.0f, row_expert, s_tab, out, q, qs,
+                                                  K, P);
+    UH_CHECK_LAUNCH();
+    return;
+  }
   const unsigned blocks = transform_blocks(P, K);
   if (mode == 2)
     mx_transform_kernel<2><<<blocks, 256, 0, st>>>(x, ldx, nullptr, u, w, limit, row_expert, s_tab, out, q, qs, K, P);
