@@ -501,59 +501,49 @@ __global__ __launch_bounds__(512) void mx_gemm_pipe_kernel(MxGemvArgs a) {
         }
       }
     } else {
-      // 1. w3 waves: bf16(u) into the 128-column tile. 2. w1 waves: h = bf16(SwiGLU(bf16(g), u)) in place. 3. the
-      // workgroup: each row's amax and fake quantization of its 128 outputs (one block).
+      // 1. every wave: bf16 of its projection (g for w1, u for w3) into that projection's 128-column LDS tile.
+      // 2. the workgroup, 8 consecutive outputs of one row per thread: h = bf16(SwiGLU(g, u)), the row's amax over
+      //    its 128 outputs (16 threads: a DPP row max), fake quantization, 16-byte stores.
       constexpr int LDC = 128 + 8;
-      uint16_t* sc = reinterpret_cast<uint16_t*>(smem);
-      const int chh = cq & 1, col0 = bx * 128 + chh * 64;
-      if (q_own == 1)
+      uint16_t* const tg = reinterpret_cast<uint16_t*>(smem);
+      uint16_t* const tu = tg + 128 * LDC;
+      uint16_t* const mine = q_own ? tu : tg;
+      const int chh = cq & 1;
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
+      for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-          for (int cb = 0; cb < 2; ++cb)
+        for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-            for (int i = 0; i < 16; ++i)
-              sc[row_of(rb, i) * LDC + chh * 64 + cb * 32 + l32] = f32_to_bf16(acc[rb][cb][i]);
+          for (int i = 0; i < 16; ++i) mine[row_of(rb, i) * LDC + chh * 64 + cb * 32 + l32] = f32_to_bf16(acc[rb][cb][i]);
       __syncthreads();
-      if (q_own == 0) {
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int r = row_of(rb, i);
-            const float w = a.gw && r < M ? a.gw[row0 + r] : 0.0f;
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-              uint16_t* cell = sc + r * LDC + chh * 64 + cb * 32 + l32;
-              const float gv = round_bf16(acc[rb][cb][i]);
-              const uint16_t u = *cell;
-              const float hval = swiglu_value(gv, bf16_to_f32(u), w, a.gw != nullptr, a.limit);
-              if (r < M) {
-                if (a.out[0]) a.out[0][(row0 + r) * a.ldo + col0 + cb * 32 + l32] = f32_to_bf16(gv);
-                if (a.out[1]) a.out[1][(row0 + r) * a.ldo + col0 + cb * 32 + l32] = u;
-              }
-              *cell = f32_to_bf16(hval);
-            }
-          }
-      }
-      __syncthreads();
-      // 16 consecutive threads take one row (8 outputs each): its amax is a DPP row max. The loop bound is
-      // uniform, so every 16-lane group is whole; threads past the tile's rows only take part in the max.
+      // The loop bound is uniform, so every 16-lane group is whole; threads past the tile's rows only take part in
+      // the max.
       for (int e0 = 0; e0 < M * 16; e0 += 512) {
         const int e = e0 + tid, r = min(e / 16, M - 1), c8 = (e % 16) * 8;
-        const uint4 hv = *reinterpret_cast<const uint4*>(sc + r * LDC + c8);
-        const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
-        float am = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) am = fmaxf(am, fabsf(bf16_to_f32(uint16_t(hw[q / 2] >> (16 * (q % 2))))));
-        am = row16_max(am);
         const size_t row = row0 + r;
-        if (e >= M * 16 || (a.gs_tab && !a.gs_tab[a.grow_expert[row]])) continue;
+        const uint4 gv4 = *reinterpret_cast<const uint4*>(tg + r * LDC + c8);
+        const uint4 uv4 = *reinterpret_cast<const uint4*>(tu + r * LDC + c8);
+        const uint32_t gw4[4] = {gv4.x, gv4.y, gv4.z, gv4.w}, uw4[4] = {uv4.x, uv4.y, uv4.z, uv4.w};
+        const float w = a.gw ? a.gw[row] : 0.0f;
+        float hv[8], am = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          hv[q] = round_bf16(swiglu_value(bf16_to_f32(uint16_t(gw4[q / 2] >> (16 * (q % 2)))),
+                                          bf16_to_f32(uint16_t(uw4[q / 2] >> (16 * (q % 2)))), w, a.gw != nullptr,
+                                          a.limit));
+          am = fmaxf(am, fabsf(hv[q]));
+        }
+        am = row16_max(am);
+        if (e >= M * 16) continue;
+        const size_t oc = row * a.ldo + size_t(bx) * 128 + c8;
+        if (a.out[0]) *reinterpret_cast<uint4*>(a.out[0] + oc) = gv4;
+        if (a.out[1]) *reinterpret_cast<uint4*>(a.out[1] + oc) = uv4;
+        if (a.gs_tab && !a.gs_tab[a.grow_expert[row]]) continue;
         const Fp8Block blk = fp8_block_scale(am);
         uint32_t qb[2] = {0, 0}, fq[4];
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-          const uint8_t c = fp8_code(bf16_to_f32(uint16_t(hw[q / 2] >> (16 * (q % 2)))), blk);
+          const uint8_t c = fp8_code(hv[q], blk);
           qb[q / 4] |= uint32_t(c) << (8 * (q % 4));
           const uint32_t f = f32_to_bf16(e4m3_to_f32(c) * blk.sc);
           fq[q / 2] = (q % 2) ? (fq[q / 2] | f << 16) : f;
