@@ -170,6 +170,15 @@ int uh_gemm_w8a8_wmma(const uint8_t* a, const uint8_t* sa, const uint8_t* w, con
 /* gemv.hpp:23-24 */
 int uh_gemv_w8a8(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, uint16_t* c, int ldc,
                  int M, int N, int K, void* stream);
+/* gemv.hpp:40-52 (GemvPart, gemv_w8a8_parts): n (1..3) column ranges on one input, given as host arrays of n
+ * entries: device pointers w (e4m3 [N_i, K]), sw (e8m0 [ceil(N_i/128), K/128]), c (bf16 [M, ldc_i]); ints ldc, N. */
+int uh_gemv_w8a8_parts(const uint8_t* a, const uint8_t* sa, const void* const* w, const uint8_t* const* sw,
+                       void* const* c, const int* ldc, const int* N, int nparts, int M, int K, void* stream);
+/* gemv.hpp:31-35, 56-57 (GemvQuant, gemv_w8a8_glu): gate / up [M, I] into gate / up, then act_quant_fp8 of
+ * bf16(SwiGLU(gate, up)) into q [M, I] / qs [M, I/128]; counters [I/128] zero on entry, left zero (may be NULL). */
+int uh_gemv_w8a8_glu(const uint8_t* a, const uint8_t* sa, const uint8_t* w_gate, const uint8_t* sw_gate,
+                     uint16_t* gate, int ldg, const uint8_t* w_up, const uint8_t* sw_up, uint16_t* up, int ldu, int I,
+                     int M, int K, float limit, uint8_t* q, uint8_t* qs, uint32_t* counters, void* stream);
 /* kernel.py fp8_gemm with fp32 scales (scale_fmt=None); gemm_wmma.hip:89-100's fold */
 int uh_gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw, uint16_t* c, int ldc,
                      int M, int N, int K, void* stream);

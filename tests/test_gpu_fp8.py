@@ -82,3 +82,62 @@ def test_gemm_a8w4_reference_order_bit_exact(tiled):
     c = DeviceBuffer(M * N * 2)
     call("uh_gemm_a8w4_tiled" if tiled else "uh_gemm_a8w4", dev(q), dev(qs), dev(w), dev(s), c, N, M, N, K, None)
     assert np.array_equal(c.download((M, N), np.uint16), ref16)
+
+
+def _w8a8_weights(rng, N, K):
+    wq = rng.integers(0, 256, (N, K), dtype=np.uint8)
+    wq[(wq & 0x7F) == 0x7F] = 0  # no NaN codes
+    sw = rng.integers(118, 126, ((N + 127) // 128, K // 128), dtype=np.uint8)
+    return wq, sw
+
+
+def test_gemv_w8a8_parts():
+    """Ref gemv.hpp:40-52: three column ranges (one ragged) on one input in one launch, each against the oracle and
+    bit-identical to gemv_w8a8 on that range alone."""
+    rng = np.random.default_rng(21)
+    M, K, Ns = 5, 1024, (384, 256, 200)
+    x = randn_bf16(rng, (M, K))
+    q, sa = oracle.act_quant_fp8(x)
+    dq, dsa = dev(q), dev(sa)
+    ws = [_w8a8_weights(rng, n, K) for n in Ns]
+    dws = [(dev(w), dev(s)) for w, s in ws]
+    ldc = [n + 8 for n in Ns]
+    outs = [DeviceBuffer(M * l * 2) for l in ldc]
+    wp = np.array([d[0].ptr for d in dws], np.uint64)
+    sp = np.array([d[1].ptr for d in dws], np.uint64)
+    cp = np.array([o.ptr for o in outs], np.uint64)
+    ldc_a, n_a = np.array(ldc, np.int32), np.array(Ns, np.int32)  # host arrays: alive across the call
+    call("uh_gemv_w8a8_parts", dq, dsa, wp.ctypes.data, sp.ctypes.data, cp.ctypes.data, ldc_a.ctypes.data,
+         n_a.ctypes.data, 3, M, K, None)
+    for (w, s), (dw, ds), n, l, o in zip(ws, dws, Ns, ldc, outs):
+        got = o.download((M, l), np.uint16)[:, :n]
+        ref16, _ = oracle.gemm_w8a8(q, sa, w, s)
+        assert max_rel(from_bf16(got), from_bf16(ref16)) <= 1e-2
+        single = DeviceBuffer(M * n * 2)
+        call("uh_gemv_w8a8", dq, dsa, dw, ds, single, n, M, n, K, None)
+        assert np.array_equal(single.download((M, n), np.uint16), got)
+
+
+@pytest.mark.parametrize("M", [1, 3, 32])
+def test_gemv_w8a8_glu(M):
+    """Ref gemv.hpp:56-57 (the shared expert's gate / up): gate and up against the oracle, and the codes / scales
+    exactly act_quant_fp8(bf16(SwiGLU(gate, up))) of the outputs the launch wrote (forward_ref.hip:1231-1244's
+    alternative path: swiglu + act_quant_fp8)."""
+    rng = np.random.default_rng(M + 40)
+    I, K, limit = 512, 1024, 10.0
+    x = randn_bf16(rng, (M, K), 2.0)
+    q, sa = oracle.act_quant_fp8(x)
+    (w1, s1), (w3, s3) = _w8a8_weights(rng, I, K), _w8a8_weights(rng, I, K)
+    g, u = DeviceBuffer(M * I * 2), DeviceBuffer(M * I * 2)
+    hq, hs = DeviceBuffer(M * I), DeviceBuffer(M * I // 128)
+    counters = DeviceBuffer(I // 128 * 4)
+    counters.zero()
+    call("uh_gemv_w8a8_glu", dev(q), dev(sa), dev(w1), dev(s1), g, I, dev(w3), dev(s3), u, I, I, M, K, limit, hq, hs,
+         counters, None)
+    gg, uu = g.download((M, I), np.uint16), u.download((M, I), np.uint16)
+    for got, (w, s) in ((gg, (w1, s1)), (uu, (w3, s3))):
+        assert max_rel(from_bf16(got), from_bf16(oracle.gemm_w8a8(q, sa, w, s)[0])) <= 1e-2
+    q_ref, s_ref = oracle.act_quant_fp8(oracle.swiglu(gg, uu, None, limit))
+    assert np.array_equal(hq.download((M, I), np.uint8), q_ref)
+    assert np.array_equal(hs.download((M, I // 128), np.uint8), s_ref)
+    assert not counters.download(I // 128, np.uint32).any()

@@ -401,6 +401,24 @@ int uh_gemv_w8a8(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const ui
                  int M, int N, int K, void* st) {
   return guard([&] { k::gemv_w8a8(a, sa, w, sw, c, ldc, M, N, K, S(st)); });
 }
+int uh_gemv_w8a8_parts(const uint8_t* a, const uint8_t* sa, const void* const* w, const uint8_t* const* sw,
+                       void* const* c, const int* ldc, const int* N, int nparts, int M, int K, void* st) {
+  return guard([&] {
+    if (!w || !sw || !c || !ldc || !N || nparts < 1 || nparts > k::GemvParts::kMax)
+      throw std::runtime_error("uh_gemv_w8a8_parts: 1..3 parts");
+    k::GemvPart parts[k::GemvParts::kMax];
+    for (int i = 0; i < nparts; ++i) parts[i] = k::GemvPart{w[i], sw[i], c[i], ldc[i], N[i]};
+    k::gemv_w8a8_parts(a, sa, parts, nparts, M, K, S(st));
+  });
+}
+int uh_gemv_w8a8_glu(const uint8_t* a, const uint8_t* sa, const uint8_t* w_gate, const uint8_t* sw_gate,
+                     uint16_t* gate, int ldg, const uint8_t* w_up, const uint8_t* sw_up, uint16_t* up, int ldu, int I,
+                     int M, int K, float limit, uint8_t* q, uint8_t* qs, uint32_t* counters, void* st) {
+  return guard([&] {
+    const k::GemvPart parts[2] = {{w_gate, sw_gate, gate, ldg, I}, {w_up, sw_up, up, ldu, I}};
+    k::gemv_w8a8_glu(a, sa, parts, M, K, limit, k::GemvQuant{q, qs, counters}, S(st));
+  });
+}
 int uh_gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw, uint16_t* c, int ldc,
                      int M, int N, int K, void* st) {
   return guard([&] { k::gemm_fp8_f32s(a, sa, w, sw, c, ldc, M, N, K, S(st)); });

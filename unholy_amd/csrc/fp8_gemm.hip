@@ -13,6 +13,7 @@
 #include "unholy/kernels/gemv.hpp"
 #include "unholy/kernels/ref.hpp"
 #include "fp8_internal.hpp"
+#include "mx_internal.hpp"
 
 namespace unholy::kernels {
 
@@ -207,12 +208,23 @@ __global__ __launch_bounds__(DN_NT) void fp8_skinny_kernel(Fp8GemmArgs a) {
 constexpr int FV_WAVES = 8, FV_CHUNK = 4;
 
 template <bool F32S, int MT>
-__global__ __launch_bounds__(64 * FV_WAVES) void fp8_gemv_kernel(Fp8GemmArgs a) {
+__global__ __launch_bounds__(64 * FV_WAVES) void fp8_gemv_kernel(Fp8GemmArgs a, Fp8Parts pp) {
   __shared__ v4f red[FV_WAVES][MT][64];
+  int tile = blockIdx.x;
+  if (pp.n) {  // column ranges: this workgroup's range (uniform)
+    int p = 0;
+    while (p + 1 < pp.n && tile >= pp.t0[p + 1]) ++p;
+    tile -= pp.t0[p];
+    a.w = pp.w[p];
+    a.sw8 = pp.sw[p];
+    a.c = pp.c[p];
+    a.ldc = pp.ldc[p];
+    a.N = pp.N[p];
+  }
   const int K = a.K, KS = K / 128, N = a.N, M = a.M;
   const int tid = threadIdx.x, lane = tid & 63, nl = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n0 = blockIdx.x * 16, n = min(n0 + nl, N - 1), nb = n0 / 128;  // a 16-column tile lies in one 128-block
+  const int n0 = tile * 16, n = min(n0 + nl, N - 1), nb = n0 / 128;  // a 16-column tile lies in one 128-block
   const int per = (KS + FV_WAVES - 1) / FV_WAVES, b0 = min(KS, wave * per), b1 = min(KS, b0 + per);
   const uint8_t* wrow = a.w + size_t(n) * K + g * 32;
   v4f acc[MT];
@@ -289,10 +301,10 @@ __global__ __launch_bounds__(64 * FV_WAVES) void fp8_gemv_kernel(Fp8GemmArgs a) 
 }
 
 template <bool F32S>
-void launch_fp8_gemv_t(const Fp8GemmArgs& a, hipStream_t st) {
-  const dim3 grid(unsigned(cdiv(size_t(a.N), 16)));
-  if (a.M <= 16) fp8_gemv_kernel<F32S, 1><<<grid, 64 * FV_WAVES, 0, st>>>(a);
-  else fp8_gemv_kernel<F32S, 4><<<grid, 64 * FV_WAVES, 0, st>>>(a);
+void launch_fp8_gemv_t(const Fp8GemmArgs& a, hipStream_t st, const Fp8Parts& pp) {
+  const dim3 grid(unsigned(pp.n ? pp.t0[pp.n] : cdiv(size_t(a.N), 16)));
+  if (a.M <= 16) fp8_gemv_kernel<F32S, 1><<<grid, 64 * FV_WAVES, 0, st>>>(a, pp);
+  else fp8_gemv_kernel<F32S, 4><<<grid, 64 * FV_WAVES, 0, st>>>(a, pp);
   UH_CHECK_LAUNCH();
 }
 
@@ -322,15 +334,27 @@ void launch_fp8_skinny(const Fp8GemmArgs& a0, hipStream_t st) {
   UH_CHECK_LAUNCH();
 }
 
-void launch_fp8_gemv(const Fp8GemmArgs& a, hipStream_t st) {
+void launch_fp8_gemv(const Fp8GemmArgs& a, hipStream_t st, const Fp8Parts* parts) {
   if (a.M <= 0) return;
   if (a.M > 64) throw std::runtime_error("fp8 gemv: M > 64");
-  if (a.K % 128 || a.K <= 0 || a.N <= 0) throw std::runtime_error("fp8 gemm: K % 128");
-  if (!a.a || !a.w || !a.c) throw std::runtime_error("fp8 gemm: null operand");
+  Fp8Parts pp{};
+  if (parts) {
+    pp = *parts;
+    if (pp.n < 1 || pp.n > 3 || a.sa32 || !a.sa8) throw std::runtime_error("fp8 gemv parts: 1..3 ranges, e8m0 scales");
+    pp.t0[0] = 0;
+    for (int i = 0; i < pp.n; ++i) {
+      if (!pp.w[i] || !pp.sw[i] || !pp.c[i] || pp.N[i] <= 0) throw std::runtime_error("fp8 gemv parts: null part");
+      pp.t0[i + 1] = pp.t0[i] + int(cdiv(size_t(pp.N[i]), 16));
+    }
+  } else if (a.N <= 0 || !a.w || !a.c) {
+    throw std::runtime_error("fp8 gemm: null operand");
+  }
+  if (a.K % 128 || a.K <= 0) throw std::runtime_error("fp8 gemm: K % 128");
+  if (!a.a) throw std::runtime_error("fp8 gemm: null operand");
   const bool f32s = a.sa32 != nullptr;
-  if (f32s ? !a.sw32 : (!a.sa8 || !a.sw8)) throw std::runtime_error("fp8 gemm: scales");
-  if (f32s) launch_fp8_gemv_t<true>(a, st);
-  else launch_fp8_gemv_t<false>(a, st);
+  if (!parts && (f32s ? !a.sw32 : (!a.sa8 || !a.sw8))) throw std::runtime_error("fp8 gemm: scales");
+  if (f32s) launch_fp8_gemv_t<true>(a, st, pp);
+  else launch_fp8_gemv_t<false>(a, st, pp);
 }
 
 // ---- entry points ---------------------------------------------------------------------------------------------------
@@ -405,6 +429,44 @@ void gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const fl
   g.N = N;
   g.K = K;
   launch_fp8_gemm(g, st);
+}
+
+namespace {
+Fp8Parts to_parts(const GemvPart* parts, int nparts) {
+  if (!parts || nparts < 1 || nparts > GemvParts::kMax) throw std::runtime_error("gemv_w8a8_parts: 1..3 parts");
+  Fp8Parts pp{};
+  pp.n = nparts;
+  for (int i = 0; i < nparts; ++i) {
+    pp.w[i] = static_cast<const uint8_t*>(parts[i].w);
+    pp.sw[i] = parts[i].sw;
+    pp.c[i] = static_cast<uint16_t*>(parts[i].c);
+    pp.ldc[i] = parts[i].ldc;
+    pp.N[i] = parts[i].N;
+  }
+  return pp;
+}
+}  // namespace
+
+void gemv_w8a8_parts(const uint8_t* a, const uint8_t* sa, const GemvPart* parts, int nparts, int M, int K,
+                     hipStream_t st) {
+  if (M > kGemvRowsCap) throw std::runtime_error("gemv_w8a8_parts: M > 32");
+  const Fp8Parts pp = to_parts(parts, nparts);
+  Fp8GemmArgs g{};
+  g.a = a;
+  g.sa8 = sa;
+  g.M = M;
+  g.K = K;
+  launch_fp8_gemv(g, st, &pp);
+}
+
+void gemv_w8a8_glu(const uint8_t* a, const uint8_t* sa, const GemvPart* parts, int M, int K, float limit,
+                   const GemvQuant& gq, hipStream_t st) {
+  if (!parts || parts[0].N != parts[1].N || parts[0].N % 128)
+    throw std::runtime_error("gemv_w8a8_glu: two parts of one width (% 128)");
+  if (!gq.q || !gq.qs) throw std::runtime_error("gemv_w8a8_glu: null q / qs");
+  gemv_w8a8_parts(a, sa, parts, 2, M, K, st);
+  launch_swiglu_quant(static_cast<const uint16_t*>(parts[0].c), parts[0].ldc, static_cast<const uint16_t*>(parts[1].c),
+                      parts[1].ldc, M, parts[0].N, limit, nullptr, gq.q, gq.qs, st);
 }
 
 int gemv_max_rows() { return 8; }

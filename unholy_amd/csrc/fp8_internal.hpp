@@ -21,9 +21,19 @@ struct Fp8GemmArgs {
   int rows_cap;
 };
 
+// Up to three column ranges on one input (gemv_w8a8_parts): range i has its own weights, e8m0 scales, output, ldc
+// and width; t0[i] is its first 16-column tile in the grid (t0[n] = total tiles).
+struct Fp8Parts {
+  int n;
+  const uint8_t* w[3];
+  const uint8_t* sw[3];
+  uint16_t* c[3];
+  int ldc[3], N[3], t0[4];
+};
+
 void launch_fp8_skinny(const Fp8GemmArgs& a, hipStream_t st);
 // M <= 64: one workgroup per 16-column tile, K split over its 8 waves (bandwidth-shaped).
-void launch_fp8_gemv(const Fp8GemmArgs& a, hipStream_t st);
+void launch_fp8_gemv(const Fp8GemmArgs& a, hipStream_t st, const Fp8Parts* parts = nullptr);
 // M > 64: the LDS-ring MFMA GEMM (N % 256, K % 128, ldc % 8; fp8_tiled_fits says whether a shape qualifies).
 bool fp8_tiled_fits(const Fp8GemmArgs& a);
 void launch_fp8_tiled(const Fp8GemmArgs& a, hipStream_t st);

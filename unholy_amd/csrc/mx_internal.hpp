@@ -43,4 +43,9 @@ void launch_mx_transform(int mode, const uint16_t* x, int ldx, const int32_t* x_
                          const float* w, float limit, const int32_t* row_expert, const uint8_t* const* s_tab,
                          uint16_t* out, uint8_t* q, uint8_t* qs, int K, int P, hipStream_t st);
 
+// h = bf16(SwiGLU(g, u)) (no routing weight) of M rows x I, act_quant per 128 into q / qs (and / or fake-quantized
+// bf16 into hh): the second half of gemv_w8a8_glu.
+void launch_swiglu_quant(const uint16_t* g, int ldg, const uint16_t* u, int ldu, int M, int I, float limit,
+                         uint16_t* hh, uint8_t* q, uint8_t* qs, hipStream_t st);
+
 }  // namespace unholy::kernels

@@ -81,7 +81,8 @@ __global__ __launch_bounds__(256) void mx_transform_kernel(const bf16* __restric
 template <int kMode>
 __global__ __launch_bounds__(256) void mx_transform8_kernel(const bf16* __restrict__ x, int ldx,
                                                             const int32_t* __restrict__ x_rows,
-                                                            const bf16* __restrict__ u, const float* __restrict__ w,
+                                                            const bf16* __restrict__ u, int ldu,
+                                                            const float* __restrict__ w,
                                                             float limit, const int32_t* __restrict__ row_expert,
                                                             const uint8_t* const* __restrict__ s_tab,
                                                             bf16* __restrict__ out, uint8_t* __restrict__ q,
@@ -94,7 +95,7 @@ __global__ __launch_bounds__(256) void mx_transform8_kernel(const bf16* __restri
     float v[8];
     if constexpr (kMode == 2) {
       const uint4 graw = *reinterpret_cast<const uint4*>(x + size_t(r) * ldx + k0);
-      const uint4 uraw = *reinterpret_cast<const uint4*>(u + size_t(r) * ldx + k0);
+      const uint4 uraw = *reinterpret_cast<const uint4*>(u + size_t(r) * ldu + k0);
       const uint32_t gw[4] = {graw.x, graw.y, graw.z, graw.w}, uw[4] = {uraw.x, uraw.y, uraw.z, uraw.w};
       const float wr = w ? w[r] : 0.0f;
 #pragma unroll
@@ -496,10 +497,11 @@ void launch_mx_transform(int mode, const bf16* x, int ldx, const int32_t* x_rows
   if (ldx % 8 == 0) {  // 16-byte rows: the 8-values-per-thread kernel
     const unsigned b8 = unsigned(std::min<size_t>((size_t(P) * (K / 8) + 255) / 256, 8192));
     if (mode == 2)
-      mx_transform8_kernel<2><<<b8, 256, 0, st>>>(x, ldx, nullptr, u, w, limit, row_expert, s_tab, out, q, qs, K, P);
+      mx_transform8_kernel<2><<<b8, 256, 0, st>>>(x, ldx, nullptr, u, ldx, w, limit, row_expert, s_tab, out, q, qs, K,
+                                                  P);
     else
-      mx_transform8_kernel<0><<<b8, 256, 0, st>>>(x, ldx, x_rows, nullptr, nullptr, 0.0f, row_expert, s_tab, out, q, qs,
-                                                  K, P);
+      mx_transform8_kernel<0><<<b8, 256, 0, st>>>(x, ldx, x_rows, nullptr, 0, nullptr, 0.0f, row_expert, s_tab, out, q,
+                                                  qs, K, P);
     UH_CHECK_LAUNCH();
     return;
   }
@@ -511,6 +513,16 @@ void launch_mx_transform(int mode, const bf16* x, int ldx, const int32_t* x_rows
   else
     mx_transform_kernel<1><<<blocks, 256, 0, st>>>(x, ldx, x_rows, nullptr, nullptr, 0.0f, row_expert, s_tab, nullptr, q, qs,
                                                    K, P);
+  UH_CHECK_LAUNCH();
+}
+
+void launch_swiglu_quant(const bf16* g, int ldg, const bf16* u, int ldu, int M, int I, float limit, bf16* hh,
+                         uint8_t* q, uint8_t* qs, hipStream_t st) {
+  if (M <= 0) return;
+  if (I % 128 || ldg % 8 || ldu % 8) throw std::runtime_error("swiglu quant: I % 128, ldg % 8, ldu % 8");
+  const unsigned b8 = unsigned(std::min<size_t>((size_t(M) * (I / 8) + 255) / 256, 8192));
+  mx_transform8_kernel<2><<<b8, 256, 0, st>>>(g, ldg, nullptr, u, ldu, nullptr, limit, nullptr, nullptr, hh, q, qs, I,
+                                              M);
   UH_CHECK_LAUNCH();
 }
 
