@@ -126,6 +126,26 @@ def time_steps(fn, steps, warmup, timed_fn=None):
     return a.elapsed_ms(b)
 
 
+def time_graph(fn, steps, warmup, per_graph=32):
+    """Per-step ms of short steps: `per_graph` steps fn(i, stream) captured as one HIP graph (the host enqueues a
+    graph, not one launch per kernel, so the timing is the GPU's), replayed to cover `steps` (rounded up to whole
+    graphs) after `warmup` steps' worth of replays; events on the capture stream."""
+    from unholy_amd.device import Event, Graph, Stream
+    st = Stream()
+    g = Graph(st, lambda: [fn(i, st) for i in range(per_graph)])
+    reps = max(1, -(-steps // per_graph))
+    for _ in range(max(1, -(-warmup // per_graph))):
+        g.launch()
+    st.synchronize()
+    a, b = Event(), Event()
+    a.record(st)
+    for _ in range(reps):
+        g.launch()
+    b.record(st)
+    b.synchronize()
+    return a.elapsed_ms(b) / (reps * per_graph)
+
+
 def bench_moe(w, T, steps, warmup, rng, R=8, bias=0.0, stage=False):
     from unholy_amd.device import synchronize
     sets = routing_sets(rng, T, R, bias)
@@ -150,12 +170,11 @@ def bench_single_gemv(w, steps, warmup, rng):
     out = DeviceBuffer(I * 2)
     wt, st = w.table.ptr, w.table.ptr + 8 * E
 
-    def fn(i):
-        call("uh_mx_grouped_gemv_q", q, qs, D, tiles[i % E], 1, wt, st, out, I, I, None, None, None, None, None, 1,
-             None, None, None, None, None, None, 0.0)
+    def fn(i, stream):
+        call("uh_mx_grouped_gemv_q", q, qs, D, tiles[i % E], 1, wt, st, out, I, I, stream.handle, None, None, None, None,
+             1, None, None, None, None, None, None, 0.0)
 
-    ms = time_steps(fn, steps, warmup) / steps
-    return ms
+    return time_graph(fn, steps, warmup, per_graph=64)
 
 
 def bench_fp8_dense(M, steps, warmup, rng, copies):
@@ -174,11 +193,11 @@ def bench_fp8_dense(M, steps, warmup, rng, copies):
     q, sa = DeviceBuffer(M * K), DeviceBuffer(M * (K // 128) * 4)
     c = DeviceBuffer(M * N * 2)
 
-    def fn(i):
-        call("uh_act_quant_fp8_f32s", x, K, q, sa, M, K, 128, None)
-        call("uh_gemm_fp8_f32s", q, sa, wq[i % copies], ws, c, N, M, N, K, None)
+    def fn(i, stream):
+        call("uh_act_quant_fp8_f32s", x, K, q, sa, M, K, 128, stream.handle)
+        call("uh_gemm_fp8_f32s", q, sa, wq[i % copies], ws, c, N, M, N, K, stream.handle)
 
-    return time_steps(fn, steps, warmup) / steps
+    return time_graph(fn, steps, warmup, per_graph=copies)
 
 
 def cpu_baseline(seconds=10.0, max_reps=5):

@@ -41,6 +41,12 @@ int uh_event_record(void* ev, void* stream);
 int uh_event_synchronize(void* ev);
 int uh_event_elapsed_ms(float* ms, void* start, void* stop);
 /* Synthetic data on the device: n bytes of a splitmix64 stream (seed), each byte mapped to lo + (v % (hi-lo+1)). */
+/* HIP graphs of a created stream's work (launch-bound sequences of short kernels): capture begin / end (the end
+ * instantiates the graph and returns its executable), launch, destroy. */
+int uh_graph_capture_begin(void* stream);
+int uh_graph_capture_end(void* stream, void** exec);
+int uh_graph_launch(void* exec, void* stream);
+int uh_graph_destroy(void* exec);
 int uh_fill_random_bytes(void* dst, size_t n, uint64_t seed, uint32_t lo, uint32_t hi, void* stream);
 
 /* ---- MXFP4 layout and activation transforms (src/kernels/mx_moe.hpp) ---- */

@@ -184,6 +184,29 @@ int uh_event_synchronize(void* ev) {
 int uh_event_elapsed_ms(float* ms, void* a, void* b) {
   return guard([&] { UH_CHECK(hipEventElapsedTime(ms, static_cast<hipEvent_t>(a), static_cast<hipEvent_t>(b))); });
 }
+int uh_graph_capture_begin(void* st) {
+  return guard([&] {
+    if (!st) throw std::runtime_error("uh_graph_capture_begin: capture needs a created stream");
+    UH_CHECK(hipStreamBeginCapture(static_cast<hipStream_t>(st), hipStreamCaptureModeThreadLocal));
+  });
+}
+int uh_graph_capture_end(void* st, void** exec) {
+  return guard([&] {
+    hipGraph_t g = nullptr;
+    UH_CHECK(hipStreamEndCapture(static_cast<hipStream_t>(st), &g));
+    hipGraphExec_t e = nullptr;
+    const hipError_t r = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    UH_CHECK(r);
+    *exec = e;
+  });
+}
+int uh_graph_launch(void* exec, void* st) {
+  return guard([&] { UH_CHECK(hipGraphLaunch(static_cast<hipGraphExec_t>(exec), static_cast<hipStream_t>(st))); });
+}
+int uh_graph_destroy(void* exec) {
+  return guard([&] { UH_CHECK(hipGraphExecDestroy(static_cast<hipGraphExec_t>(exec))); });
+}
 int uh_fill_random_bytes(void* dst, size_t n, uint64_t seed, uint32_t lo, uint32_t hi, void* st) {
   return guard([&] {
     if (hi < lo || hi > 255) throw std::runtime_error("uh_fill_random_bytes: need lo <= hi <= 255");

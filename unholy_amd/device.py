@@ -111,6 +111,30 @@ class Event:
         return ms.value
 
 
+class Graph:
+    """The work `fn()` enqueues on `stream` (a created Stream), captured once as a HIP graph and replayed by launch()."""
+
+    def __init__(self, stream: "Stream", fn):
+        self.stream = stream
+        call("uh_graph_capture_begin", stream.handle)
+        p = ctypes.c_void_p()
+        try:
+            fn()
+        finally:
+            call("uh_graph_capture_end", stream.handle, ctypes.byref(p))
+        self.handle = p.value
+
+    def launch(self) -> None:
+        call("uh_graph_launch", self.handle, self.stream.handle)
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            try:
+                call("uh_graph_destroy", self.handle)
+            except Exception:
+                pass
+
+
 def fill_random_bytes(buf, n: int, seed: int, lo: int = 0, hi: int = 255, stream=None) -> None:
     call("uh_fill_random_bytes", ptr(buf), int(n), int(seed) & (2**64 - 1), lo, hi, stream)
 
