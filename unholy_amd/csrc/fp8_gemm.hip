@@ -60,11 +60,66 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const bf16* __restrict__
   *reinterpret_cast<uint16_t*>(q + size_t(r) * cols + size_t(b) * B + 2 * l) = uint16_t(c0 | uint32_t(c1) << 8);
 }
 
+// Block 128 with 8 values per thread: 16 consecutive threads per block (16-byte loads, 8-byte code stores), the amax a
+// DPP row max. The item loop bound is uniform so every 16-lane group is whole. Needs ldx % 8 == 0.
+template <int MODE>
+__global__ __launch_bounds__(256) void act_quant8_kernel(const bf16* __restrict__ x, int ldx, uint8_t* __restrict__ q,
+                                                         void* __restrict__ s, int rows, int cols) {
+  const int nb = cols / 128;
+  const size_t per_row = size_t(nb) * 16, items = size_t(rows) * per_row;
+  for (size_t base = size_t(blockIdx.x) * 256; base < items; base += size_t(gridDim.x) * 256) {
+    const size_t it = min(base + threadIdx.x, items - 1);
+    const int r = int(it / per_row), rem = int(it % per_row), b = rem >> 4, l = rem & 15;
+    bf16* xr = const_cast<bf16*>(x) + size_t(r) * ldx + size_t(b) * 128 + 8 * l;
+    const uint4 raw = *reinterpret_cast<const uint4*>(xr);
+    const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
+    float v[8], am = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(rw[i] << 16);
+      v[2 * i + 1] = __uint_as_float(rw[i] & 0xffff0000u);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
+    am = row16_max(am);
+    if (base + threadIdx.x >= items) continue;
+    uint32_t c[2] = {0, 0};
+    if constexpr (MODE == 2) {
+      const float sc = fmaxf(am, 1e-4f) * (1.0f / 448.0f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) c[i / 4] |= uint32_t(fp8_code(v[i], sc)) << (8 * (i % 4));
+      if (l == 0) static_cast<float*>(s)[size_t(r) * nb + b] = sc;
+    } else {
+      const Fp8Block blk = fp8_block_scale(am);
+      uint32_t h[4];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint8_t code = fp8_code(v[i], blk);
+        c[i / 4] |= uint32_t(code) << (8 * (i % 4));
+        const uint32_t f = f32_to_bf16(e4m3_to_f32(code) * blk.sc);
+        h[i / 2] = (i % 2) ? (h[i / 2] | f << 16) : f;
+      }
+      if constexpr (MODE == 1) {
+        *reinterpret_cast<uint4*>(xr) = make_uint4(h[0], h[1], h[2], h[3]);
+        continue;
+      }
+      if (l == 0) static_cast<uint8_t*>(s)[size_t(r) * nb + b] = blk.se;
+    }
+    *reinterpret_cast<uint2*>(q + size_t(r) * cols + size_t(b) * 128 + 8 * l) = make_uint2(c[0], c[1]);
+  }
+}
+
 template <int MODE>
 void launch_act_quant(const bf16* x, int ldx, uint8_t* q, void* s, int rows, int cols, int block, hipStream_t st) {
   if (rows <= 0) return;
   if (block != 32 && block != 64 && block != 128) throw std::runtime_error("act_quant: block in {32, 64, 128}");
   if (cols % block) throw std::runtime_error("act_quant: cols % block");
+  if (block == 128 && ldx % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && (MODE == 1 || cols % 8 == 0)) {
+    const unsigned grid = unsigned(std::min<size_t>(cdiv(size_t(rows) * (cols / 8), 256), 8192));
+    act_quant8_kernel<MODE><<<grid, 256, 0, st>>>(x, ldx, q, s, rows, cols);
+    UH_CHECK_LAUNCH();
+    return;
+  }
   const size_t threads = size_t(rows) * (cols / block) * (block / 2);
   const unsigned grid = cdiv(threads, 256);
   if (block == 32) act_quant_kernel<32, MODE><<<grid, 256, 0, st>>>(x, ldx, q, s, rows, cols);
