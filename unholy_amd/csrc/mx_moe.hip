@@ -175,26 +175,37 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nl = lane & 15, g = lane >> 4;
   const int nt = blockIdx.x * W + wave;
   const bool active = nt < ntn;  // uniform per wave
-  const int boff = nl * 32 + (g & 1) * 16, soff = nl * 2 + (g & 1);
+  const int boff = nl * 32 + (g & 1) * 16;
   for (int rg = 0; rg < tile.rows; rg += a.rows_cap) {
     const int M = min(a.rows_cap, tile.rows - rg);
     const size_t row0 = size_t(tile.row0) + rg;
     // Prefetch the first GV_PF steps of weights before staging the activations (independent of them).
     v4i bq[GV_PF][NP];
-    uint32_t sq[GV_PF][NP];
     // 32-bit offsets from the (uniform) matrix base: loads take the scalar-base + vector-offset form.
-    const uint32_t cofs = uint32_t(((g >> 1) * ntn + nt) * 512 + boff), sofs = uint32_t(((g >> 1) * ntn + nt) * 32 + soff);
-    const uint32_t cstep = uint32_t(2 * ntn * 512), sstep = uint32_t(2 * ntn * 32);
+    const uint32_t cofs = uint32_t(((g >> 1) * ntn + nt) * 512 + boff);
+    const uint32_t cstep = uint32_t(2 * ntn * 512);
     const auto load_step = [&](int s, int slot) {
 #pragma unroll
-      for (int p = 0; p < NP; ++p) {  // streamed once per launch: nontemporal loads (~12% more read bandwidth)
+      for (int p = 0; p < NP; ++p)  // streamed once per launch: nontemporal loads (~12% more read bandwidth)
         bq[slot][p] = __builtin_nontemporal_load(reinterpret_cast<gptr<v4i>>(as_global(wp[p]) + (cofs + uint32_t(s) * cstep)));
-        sq[slot][p] = __builtin_nontemporal_load(as_global(sp[p]) + (sofs + uint32_t(s) * sstep));
-      }
     };
-    if (active)
+    // Weight scales per round of GV_PF = 4 steps (8 slabs of 64 inputs): lane l loads dword l % 8 of slab l / 8's
+    // 32-byte scale chunk of the wave's 16 columns -- one load per projection per round instead of a byte per step.
+    // A step's byte is then taken from the owning lane with ds_bpermute (the lane crossbar, no memory access).
+    static_assert(GV_PF == 4, "a round's 8 slabs are one dword per lane");
+    uint32_t sq_cur[NP], sq_nxt[NP];
+    const auto load_scales = [&](int s0, uint32_t (&dst)[NP]) {
+      const uint32_t slab = uint32_t(min(2 * s0 + (lane >> 3), 2 * KS - 1));
+      const uint32_t so = (slab * uint32_t(ntn) + uint32_t(nt)) * 32u + uint32_t(lane & 7) * 4u;
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+        dst[p] = __builtin_nontemporal_load(reinterpret_cast<gptr<uint32_t>>(as_global(sp[p]) + so));
+    };
+    if (active) {
+      load_scales(0, sq_cur);
 #pragma unroll
       for (int i = 0; i < GV_PF; ++i) load_step(min(i, KS - 1), i);  // K < 128 * GV_PF: re-read the last step
+    }
     __syncthreads();
     if constexpr (AM != 0) {
       // 8 values per thread; 16 consecutive threads hold one 128-block (K / 8 is a multiple of 16).
@@ -276,7 +287,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
       }
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
-        const float sc = __uint_as_float(sq[i][p] << 23);
+        // the byte of slab 2i + g / 2, column nl, 32-block g % 2: dword nl / 2 of that slab, byte 2 (nl % 2) + g % 2
+        const int src = ((2 * i + (g >> 1)) * 8 + (nl >> 1)) * 4;
+        const uint32_t word = uint32_t(__builtin_amdgcn_ds_bpermute(src, int(sq_cur[p])));
+        const float sc = __uint_as_float(((word >> (8 * (2 * (nl & 1) + (g & 1)))) & 0xffu) << 23);
 #pragma unroll
         for (int t = 0; t < 4; ++t) acc[p] = mfma_bf16(af[t], fp4x8_to_bf16(uint32_t(bq[i][p][t]), sc), acc[p]);
       }
@@ -289,10 +303,13 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
           // Unconditional (past the end it re-reads the last step): a conditional load would leave the compiler
           // unsure how many loads are outstanding, and it would then wait for all of them at every round.
           load_step(min(s0 + i + GV_PF, KS - 1), i);
+          if (i == 0) load_scales(s0 + GV_PF, sq_nxt);  // next round's (past the end: re-reads the last slabs)
           // Keep each step's conversions and MFMAs together: interleaving the unrolled steps would only raise
           // register pressure (the loads of later steps are already in flight).
           __builtin_amdgcn_sched_barrier(0);
         }
+#pragma unroll
+        for (int p = 0; p < NP; ++p) sq_cur[p] = sq_nxt[p];
       }
 
     if constexpr (GM == 0) {
