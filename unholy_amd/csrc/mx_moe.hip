@@ -295,15 +295,17 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         for (int t = 0; t < 4; ++t) acc[p] = mfma_bf16(af[t], fp4x8_to_bf16(uint32_t(bq[i][p][t]), sc), acc[p]);
       }
     };
-    if (active)
-      for (int s0 = 0; s0 < KS; s0 += GV_PF) {
+    if (active) {
+      int s0 = 0;
+      // Every round but the last loads the next round's weights. The loads are unconditional (a conditional load
+      // would leave the compiler unsure how many are outstanding, and it would then wait for all of them each
+      // round); with K % 512 == 0 none of them is past the end (otherwise they re-read the last step).
+      for (; s0 + GV_PF < KS; s0 += GV_PF) {
 #pragma unroll
         for (int i = 0; i < GV_PF; ++i) {
           if (s0 + i < KS) step(s0 + i, i);
-          // Unconditional (past the end it re-reads the last step): a conditional load would leave the compiler
-          // unsure how many loads are outstanding, and it would then wait for all of them at every round.
           load_step(min(s0 + i + GV_PF, KS - 1), i);
-          if (i == 0) load_scales(s0 + GV_PF, sq_nxt);  // next round's (past the end: re-reads the last slabs)
+          if (i == 0) load_scales(s0 + GV_PF, sq_nxt);
           // Keep each step's conversions and MFMAs together: interleaving the unrolled steps would only raise
           // register pressure (the loads of later steps are already in flight).
           __builtin_amdgcn_sched_barrier(0);
@@ -311,6 +313,12 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
 #pragma unroll
         for (int p = 0; p < NP; ++p) sq_cur[p] = sq_nxt[p];
       }
+#pragma unroll
+      for (int i = 0; i < GV_PF; ++i) {  // the last round: nothing left to load
+        if (s0 + i < KS) step(s0 + i, i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
 
     if constexpr (GM == 0) {
       if (active)
