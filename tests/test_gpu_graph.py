@@ -43,9 +43,12 @@ def test_graph_replays_fp8_dense_step():
         st.synchronize()
 
 
-def test_graph_replays_decode_forward():
-    rng = np.random.default_rng(9)
-    T, E, K, D, I, limit = 8, 32, 6, 1024, 512, 10.0
+@pytest.mark.parametrize("T", [8, 48, 80])
+def test_graph_replays_decode_forward(T):
+    """T = 8: single-block dispatch + GEMVs; 48: multi-kernel dispatch (its counters cleared by a kernel) + GEMVs;
+    80: the prefill GEMM path."""
+    rng = np.random.default_rng(9 + T)
+    E, K, D, I, limit = 32, 6, 1024, 512, 10.0
     experts, bufs, tab, x, logits = _moe_case(rng, T, E, K, D, I)
     ws_bytes = call("uh_mx_moe_workspace_size", T, K, E, D, I)
     ws, out = DeviceBuffer(ws_bytes), DeviceBuffer(T * D * 2)

@@ -12,6 +12,7 @@
 #include "unholy/kernels/mx_moe.hpp"
 #include "unholy/kernels/ref.hpp"
 #include "unholy_amd.h"
+#include "mx_internal.hpp"
 
 namespace k = unholy::kernels;
 using uh::bf16;
@@ -509,7 +510,7 @@ int uh_mx_moe_forward_ev(const uint16_t* x, const float* logits, int T, int K, i
       a.softmax_logits = logits;  // routing in the same launch
       k::moe_dispatch_small(a, st);
     } else {
-      UH_CHECK(hipMemsetAsync(w.count, 0, size_t(E) * 4, st));
+      k::launch_zero_words(w.count, size_t(E), st);  // a kernel: no memset node if the caller captures a graph
       k::moe_count(s_sel, T, K, w.count, E, st);
       k::moe_plan(w.count, nullptr, E, P, reinterpret_cast<k::MoePlan*>(w.plan), tiles, nullptr, w.off, w.fill,
                   w.max_tiles, st, w.tile_rows);

@@ -12,6 +12,7 @@
 #include "numerics.hpp"
 #include "unholy/kernels/moe_dispatch.hpp"
 #include "unholy/kernels/ref.hpp"
+#include "mx_internal.hpp"
 
 namespace unholy::kernels {
 
@@ -496,6 +497,16 @@ void moe_scatter_e(const int32_t* sel, const float* wt, int T, int K, int E, con
 void moe_scatter(const int32_t* sel, const float* wt, int T, int K, const int32_t* off, int32_t*, int32_t* eidx,
                  float* ewt, int32_t* row_expert, int32_t* pidx, hipStream_t st) {
   moe_scatter_e(sel, wt, T, K, PLAN_NT, off, eidx, ewt, row_expert, pidx, st);
+}
+
+__global__ void zero_words_kernel(int32_t* p, size_t n) {
+  for (size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) p[i] = 0;
+}
+
+void launch_zero_words(int32_t* p, size_t n, hipStream_t st) {
+  if (!n) return;
+  zero_words_kernel<<<unsigned(std::min<size_t>(cdiv(n, 256), 1024)), 256, 0, st>>>(p, n);
+  UH_CHECK_LAUNCH();
 }
 
 void moe_dispatch_small(const MoeSmallArgs& a, hipStream_t st) {

@@ -38,6 +38,8 @@ struct MxGemvArgs {
 
 // amode: 0 e4m3 codes + scales, 1 fake-quantized bf16 rows, 2 raw bf16 token rows (act_quant in the kernel).
 void launch_mx_gemv(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st);
+// Zeroes n int32 words (a kernel, so that a captured graph records no memset node).
+void launch_zero_words(int32_t* p, size_t n, hipStream_t st);
 void launch_mx_gemm(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st);
 void launch_mx_transform(int mode, const uint16_t* x, int ldx, const int32_t* x_rows, const uint16_t* u,
                          const float* w, float limit, const int32_t* row_expert, const uint8_t* const* s_tab,
