@@ -34,7 +34,7 @@ LIMIT = 10.0
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the dominant kernel (w1/w3 GEMV, this seeded workload): FETCH_SIZE + WRITE_SIZE from two
 # rocprofv3 --pmc runs, scaled by the same counters on a 1 GiB device copy (profiles/hbm_traffic_pmc.md).
-GEMV_TRAFFIC_BYTES = 405.0e6
+GEMV_TRAFFIC_BYTES = 398.9e6
 BF16_PEAK_TFLOPS = 2500.0
 
 
@@ -308,7 +308,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": GEMV_TRAFFIC_BYTES,
                      "traffic_source": "profiles/hbm_traffic_pmc.md (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)",
-                     "kernel": "mx_gemv_kernel<2, 2, 2, 4> (w1/w3 grouped GEMV, SwiGLU epilogue)", "avg_launch_ms": g_ms,
+                     "kernel": "mx_gemv_kernel<2, 2, 2, 8> (w1/w3 grouped GEMV, SwiGLU epilogue)", "avg_launch_ms": g_ms,
                      "algorithmic_bytes_per_launch": float(np.mean(gemv_bytes))},
     }
     if not args.no_sweep:

@@ -144,6 +144,7 @@ unsigned transform_blocks(int P, int K) { return unsigned(std::min<size_t>((size
 // * 16: each half-wave reads one contiguous 512-byte chunk of the tile-major layout) and that 32-block's scale
 // byte, dequantizes them exactly to bf16 with the scaled conversion instructions and issues four bf16 MFMAs against
 // the matching activation inputs. The MFMA accumulates in fp32 with exact products; no cross-lane reductions.
+// GV_PF: weight steps in flight per wave (8 measured slower: the larger ring costs occupancy).
 constexpr int GV_WAVES = 8, GV_NT = 64 * GV_WAVES, GV_PAD = 16, GV_MAXROWS = 16, GV_PF = 4;
 
 // AM: activation source -- 0: e4m3 codes + e8m0 scales (aq, as); 1: fake-quantized bf16 rows (xa), codes recovered
@@ -189,17 +190,22 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
       for (int p = 0; p < NP; ++p)  // streamed once per launch: nontemporal loads (~12% more read bandwidth)
         bq[slot][p] = __builtin_nontemporal_load(reinterpret_cast<gptr<v4i>>(as_global(wp[p]) + (cofs + uint32_t(s) * cstep)));
     };
-    // Weight scales per round of GV_PF = 4 steps (8 slabs of 64 inputs): lane l loads dword l % 8 of slab l / 8's
-    // 32-byte scale chunk of the wave's 16 columns -- one load per projection per round instead of a byte per step.
-    // A step's byte is then taken from the owning lane with ds_bpermute (the lane crossbar, no memory access).
-    static_assert(GV_PF == 4, "a round's 8 slabs are one dword per lane");
-    uint32_t sq_cur[NP], sq_nxt[NP];
-    const auto load_scales = [&](int s0, uint32_t (&dst)[NP]) {
-      const uint32_t slab = uint32_t(min(2 * s0 + (lane >> 3), 2 * KS - 1));
-      const uint32_t so = (slab * uint32_t(ntn) + uint32_t(nt)) * 32u + uint32_t(lane & 7) * 4u;
+    // Weight scales per 4 steps (8 slabs of 64 inputs): lane l loads dword l % 8 of slab l / 8's 32-byte scale chunk
+    // of the wave's 16 columns -- one load per projection per 4 steps instead of a byte per step. A step's byte is
+    // then taken from the owning lane with ds_bpermute (the lane crossbar, no memory access). These loads go
+    // through the caches: the workgroup's waves read neighbouring 32-byte pieces of one 128-byte line (nontemporal
+    // 32-byte reads cost ~4% of the launch's time in a load-only measurement of this pattern).
+    constexpr int SW = GV_PF / 4;
+    static_assert(GV_PF % 4 == 0, "a scale dword per lane covers 4 steps");
+    uint32_t sq_cur[SW][NP], sq_nxt[SW][NP];
+    const auto load_scales = [&](int s0, uint32_t (&dst)[SW][NP]) {
 #pragma unroll
-      for (int p = 0; p < NP; ++p)
-        dst[p] = __builtin_nontemporal_load(reinterpret_cast<gptr<uint32_t>>(as_global(sp[p]) + so));
+      for (int j = 0; j < SW; ++j) {
+        const uint32_t slab = uint32_t(min(2 * (s0 + 4 * j) + (lane >> 3), 2 * KS - 1));
+        const uint32_t so = (slab * uint32_t(ntn) + uint32_t(nt)) * 32u + uint32_t(lane & 7) * 4u;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) dst[j][p] = *reinterpret_cast<gptr<uint32_t>>(as_global(sp[p]) + so);
+      }
     };
     if (active) {
       load_scales(0, sq_cur);
@@ -287,9 +293,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
       }
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
-        // the byte of slab 2i + g / 2, column nl, 32-block g % 2: dword nl / 2 of that slab, byte 2 (nl % 2) + g % 2
-        const int src = ((2 * i + (g >> 1)) * 8 + (nl >> 1)) * 4;
-        const uint32_t word = uint32_t(__builtin_amdgcn_ds_bpermute(src, int(sq_cur[p])));
+        // the byte of slab 2 (i % 4) + g / 2 of word i / 4, column nl, 32-block g % 2: dword nl / 2 of that slab,
+        // byte 2 (nl % 2) + g % 2
+        const int src = ((2 * (i % 4) + (g >> 1)) * 8 + (nl >> 1)) * 4;
+        const uint32_t word = uint32_t(__builtin_amdgcn_ds_bpermute(src, int(sq_cur[i / 4][p])));
         const float sc = __uint_as_float(((word >> (8 * (2 * (nl & 1) + (g & 1)))) & 0xffu) << 23);
 #pragma unroll
         for (int t = 0; t < 4; ++t) acc[p] = mfma_bf16(af[t], fp4x8_to_bf16(uint32_t(bq[i][p][t]), sc), acc[p]);
@@ -311,7 +318,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
           __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
-        for (int p = 0; p < NP; ++p) sq_cur[p] = sq_nxt[p];
+        for (int j = 0; j < SW; ++j)
+#pragma unroll
+          for (int p = 0; p < NP; ++p) sq_cur[j][p] = sq_nxt[j][p];
       }
 #pragma unroll
       for (int i = 0; i < GV_PF; ++i) {  // the last round: nothing left to load
@@ -464,10 +473,9 @@ void set_lds_limit(K kernel, size_t bytes) {
                                                   hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes)));
 }
 
-// Workgroup shape per launch: a requantizing epilogue needs a whole 128-output block (8 waves). Otherwise, when the
-// staged activations are small (decode tiles), 4-wave workgroups: twice as many, smaller work items, which balance
-// better over the CUs, with three workgroups per CU. Larger tiles keep 8 waves, so that two workgroups still fit a
-// CU's LDS.
+// Workgroup shape: 8 waves (128 outputs) for every launch. A requantizing epilogue needs a whole 128-output block;
+// for the others 8-wave workgroups measured 1% (decode) to 3% (verify) faster than 4-wave ones, whose smaller work
+// items were expected to balance better.
 template <int NP, int GM, int AM, int W>
 void launch_gemv_w(const MxGemvArgs& a, int ntiles, hipStream_t st) {
   const size_t lds = size_t(a.rows_cap) * (a.K + GV_PAD) + size_t(a.rows_cap) * (a.K / 128);
@@ -479,9 +487,7 @@ void launch_gemv_w(const MxGemvArgs& a, int ntiles, hipStream_t st) {
 }
 template <int NP, int GM, int AM>
 void launch_gemv_t(const MxGemvArgs& a, int ntiles, hipStream_t st) {
-  if constexpr (GM == 1) launch_gemv_w<NP, GM, AM, 8>(a, ntiles, st);
-  else if (size_t(a.rows_cap) * (a.K + GV_PAD) <= 36 * 1024) launch_gemv_w<NP, GM, AM, 4>(a, ntiles, st);
-  else launch_gemv_w<NP, GM, AM, 8>(a, ntiles, st);
+  launch_gemv_w<NP, GM, AM, GV_WAVES>(a, ntiles, st);
 }
 
 }  // namespace
