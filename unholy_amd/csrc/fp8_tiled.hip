@@ -4,8 +4,8 @@
 //
 // Workgroup = 512 threads, 128 rows x 256 columns; wave w owns 64 rows (the two waves sharing a SIMD take opposite
 // halves) and columns 64 (w >> 1) .. + 63. Per 128-input stage a 3-slot LDS ring holds
-//   A 16 KB: row r's 16-byte piece p at slot r * 8 + (p ^ (r & 7)),
-//   B 32 KB: column n's 16-byte piece p at slot n * 8 + (p ^ (n & 7)) (W is row-major like A),
+//   A 16 KB: row r's 16-byte piece p at slot r * 8 + (p ^ lds_swz(r)),
+//   B 32 KB: column n's 16-byte piece p at slot n * 8 + (p ^ lds_swz(n)) (W is row-major like A),
 //   S 512 B: fp32 activation scales of the 128 rows (fp32 form only, one gathered dword per row),
 // filled by direct global -> LDS loads issued two stages ahead (6 or 7 per wave per stage, counted with vmcnt).
 // Both operands are dequantized exactly to bf16 at the LDS read and multiplied on the 32x32x16 bf16 MFMA. e8m0
@@ -51,12 +51,12 @@ __global__ __launch_bounds__(512) void fp8_tiled_kernel(Fp8GemmArgs a) {
   uint32_t aoff[2], boff[4];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int slot = (wave * 2 + i) * 64 + lane, r = slot >> 3, p = (slot & 7) ^ (r & 7);
+    const int slot = (wave * 2 + i) * 64 + lane, r = slot >> 3, p = (slot & 7) ^ lds_swz(r);
     aoff[i] = uint32_t(min(r, Mt - 1)) * uint32_t(K) + uint32_t(p * 16);
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int slot = (wave * 4 + i) * 64 + lane, n = slot >> 3, p = (slot & 7) ^ (n & 7);
+    const int slot = (wave * 4 + i) * 64 + lane, n = slot >> 3, p = (slot & 7) ^ lds_swz(n);
     boff[i] = uint32_t(n) * uint32_t(K) + uint32_t(p * 16);
   }
   // fp32 activation scales: lanes 16 (w % 4) .. + 15 of wave w gather rows 64 (w / 4) + lane.
@@ -122,14 +122,14 @@ __global__ __launch_bounds__(512) void fp8_tiled_kernel(Fp8GemmArgs a) {
         const int n = cq * 64 + cb * 32 + l32;
 #pragma unroll
         for (int x = 0; x < 2; ++x)
-          bq[cb][x] = *reinterpret_cast<const v4i*>(stb + FT_A + (n * 8 + ((4 * j + 2 * h + x) ^ (n & 7))) * 16);
+          bq[cb][x] = *reinterpret_cast<const v4i*>(stb + FT_A + (n * 8 + ((4 * j + 2 * h + x) ^ lds_swz(n))) * 16);
       }
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
         const int r = rh * 64 + rb * 32 + l32;
 #pragma unroll
         for (int x = 0; x < 2; ++x)
-          aq[rb][x] = *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 * j + 2 * h + x) ^ (r & 7))) * 16);
+          aq[rb][x] = *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 * j + 2 * h + x) ^ lds_swz(r))) * 16);
       }
 #pragma unroll
       for (int t = 0; t < 4; ++t) {

@@ -332,7 +332,7 @@ __global__ __launch_bounds__(256 * NP) void mx_gemm_kernel(MxGemvArgs a) {
 // Workgroup = 512 threads, one tile x 256 output columns: 128 columns each of w1 and w3 (NP 2, SwiGLU epilogue)
 // or 256 columns of one matrix (NP 1). Wave w owns 64 rows and columns 64 (w >> 1) .. + 63 of the
 // 256 (rows: see rh below). Per 128-input stage the ring slot holds
-//   A  16 KB: the tile's fp8 codes, row r's 16-byte piece p at slot r * 8 + (p ^ (r & 7)) (conflict-free MFMA reads);
+//   A  16 KB: the tile's fp8 codes, row r's 16-byte piece p at slot r * 8 + (p ^ lds_swz(r)) (conflict-free MFMA reads);
 //   B  16 KB: 16 blocks of 1 KB = (projection or column half q, 64-input slab j, 32-column block c); slot h * 32 + n
 //      of a block holds input half h (32 codes) of its column n, so a wave's operand read is 1 KB contiguous;
 //   Bs  1 KB: the e8m0 weight scales of (q, j) in their global order (256 B each).
@@ -383,14 +383,10 @@ __global__ __launch_bounds__(512) void mx_gemm_pipe_kernel(MxGemvArgs a) {
     const int M = min(128, tile.rows - rg);
     const size_t row0 = size_t(tile.row0) + rg;
     __syncthreads();  // the previous row group's LDS use is over
-    for (int e = tid; e < 128 * KS; e += 512) {
-      const int r = min(e & 127, M - 1), s = e >> 7;
-      as_lds[e] = a.as[size_t(a.x_rows ? a.x_rows[row0 + r] : int(row0 + r)) * KS + s];
-    }
     uint32_t aoff[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int slot = (wave * 2 + i) * 64 + lane, r = slot >> 3, p = (slot & 7) ^ (r & 7);
+      const int slot = (wave * 2 + i) * 64 + lane, r = slot >> 3, p = (slot & 7) ^ lds_swz(r);
       // Rows past the tile repeat its last. With x_rows the loads gather token rows (offsets from q itself).
       const int rr = min(r, M - 1);
       aoff[i] = (a.x_rows ? uint32_t(a.x_rows[row0 + rr]) : uint32_t(rr)) * uint32_t(K) + uint32_t(p * 16);
@@ -417,6 +413,14 @@ __global__ __launch_bounds__(512) void mx_gemm_pipe_kernel(MxGemvArgs a) {
       for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = v16f_t{};
     const int pro = min(GP_S - 1, KS);
     for (int s = 0; s < pro; ++s) issue(s);
+    // The activation scales are preloaded after the first stages are in flight: their row indices are the ones the
+    // DMA offsets just read, and the preload's loads overlap the stages' (its wait also covers them, which stage 0
+    // needs anyway). Every thread keeps one row (512 % 128 == 0).
+    {
+      const int r = min(tid & 127, M - 1);
+      const uint8_t* srow = a.as + size_t(a.x_rows ? a.x_rows[row0 + r] : int(row0 + r)) * KS;
+      for (int e = tid; e < 128 * KS; e += 512) as_lds[e] = srow[e >> 7];
+    }
 
     for (int s = 0; s < KS; ++s) {
       const int after = min(GP_S - 2, KS - 1 - s);  // stages issued after s (loads still allowed in flight)
@@ -444,7 +448,7 @@ __global__ __launch_bounds__(512) void mx_gemm_pipe_kernel(MxGemvArgs a) {
           const int r = rh * 64 + rb * 32 + l32;
 #pragma unroll
           for (int x = 0; x < 2; ++x)
-            aq[rb][x] = *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 * j + 2 * h + x) ^ (r & 7))) * 16);
+            aq[rb][x] = *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 * j + 2 * h + x) ^ lds_swz(r))) * 16);
           asc[rb] = __uint_as_float(uint32_t(as_lds[s * 128 + r]) << 23);
         }
 #pragma unroll
@@ -540,17 +544,20 @@ __global__ __launch_bounds__(512) void mx_gemm_pipe_kernel(MxGemvArgs a) {
         if (a.out[1]) *reinterpret_cast<uint4*>(a.out[1] + oc) = uv4;
         if (a.gs_tab && !a.gs_tab[a.grow_expert[row]]) continue;
         const Fp8Block blk = fp8_block_scale(am);
-        uint32_t qb[2] = {0, 0}, fq[4];
+        uint32_t qb[2] = {0, 0};
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const uint8_t c = fp8_code(hv[q], blk);
-          qb[q / 4] |= uint32_t(c) << (8 * (q % 4));
-          const uint32_t f = f32_to_bf16(e4m3_to_f32(c) * blk.sc);
-          fq[q / 2] = (q % 2) ? (fq[q / 2] | f << 16) : f;
-        }
+        for (int q = 0; q < 8; ++q) qb[q / 4] |= uint32_t(fp8_code(hv[q], blk)) << (8 * (q % 4));
         const size_t o = row * N + size_t(bx) * 128 + c8;
         if (a.hq) *reinterpret_cast<uint2*>(a.hq + o) = make_uint2(qb[0], qb[1]);
-        if (a.hh) *reinterpret_cast<uint4*>(a.hh + o) = make_uint4(fq[0], fq[1], fq[2], fq[3]);
+        if (a.hh) {  // the fake-quantized bf16 rows, only when asked for
+          uint32_t fq[4];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const uint32_t f = f32_to_bf16(e4m3_to_f32(uint8_t(qb[q / 4] >> (8 * (q % 4)))) * blk.sc);
+            fq[q / 2] = (q % 2) ? (fq[q / 2] | f << 16) : f;
+          }
+          *reinterpret_cast<uint4*>(a.hh + o) = make_uint4(fq[0], fq[1], fq[2], fq[3]);
+        }
         if (a.hs && c8 == 0) a.hs[row * (N / 128) + bx] = blk.se;
       }
     }

@@ -58,6 +58,12 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_barrier();
 }
 
+// XOR swizzle of a 128-byte LDS row (8 pieces of 16 bytes): row r's piece p is stored at slot r * 8 + (p ^ lds_swz(r)).
+// gfx950's LDS has 64 banks of 4 bytes, and a 16-byte read serves 16 lanes per pass. The 16 rows an MFMA operand
+// read touches in one pass then cover the 64 banks once: rows r and r ^ 1 sit 32 banks apart (r * 128 bytes), and
+// (r >> 1) & 7 spreads the row pairs over the eight 16-byte bank groups.
+__device__ __forceinline__ int lds_swz(int r) { return (r >> 1) & 7; }
+
 // Block -> (column block bx, tile by). Workgroups go round-robin over the 8 XCDs (lin % 8); XCD x runs tiles x,
 // x + 8, x + 16, ... in order, each tile's column blocks back to back, so they share that XCD's L2 and the tiles that
 // exist (the first *ntiles_dev of a grid sized for the maximum) are spread evenly over the XCDs. The launcher pads
