@@ -7,6 +7,7 @@
 // 32x32x16 bf16 MFMAs with fp32 accumulation. Weight columns are read from HBM once per tile; the activation tile is
 // shared by the tile's column blocks, which the block mapping keeps on one XCD (one L2).
 #include <algorithm>
+#include <type_traits>
 #include <cstdlib>
 
 #include "common.hpp"
@@ -422,51 +423,60 @@ __global__ __launch_bounds__(512) void mx_gemm_pipe_kernel(MxGemvArgs a) {
       for (int e = tid; e < 128 * KS; e += 512) as_lds[e] = srow[e >> 7];
     }
 
-    for (int s = 0; s < KS; ++s) {
-      const int after = min(GP_S - 2, KS - 1 - s);  // stages issued after s (loads still allowed in flight)
-      if (after >= 2) wait_vm<10>();
-      else if (after == 1) wait_vm<5>();
-      else wait_vm<0>();
-      __syncthreads();  // every wave's part of stage s has landed; slot (s - 1) % S is free
-      if (s + GP_S - 1 < KS) issue(s + GP_S - 1);
-      const uint8_t* stb = smem + (s % GP_S) * GP_STAGE;
+    // The K loop, specialised on the wave's live 32-row blocks (constant over the row group): each stage is then one
+    // basic block that the compiler can interleave (conversions of the next step between the MFMAs of this one).
+    const auto kloop = [&](auto nrb) {
+      constexpr int RB = decltype(nrb)::value;
+      for (int s = 0; s < KS; ++s) {
+        const int after = min(GP_S - 2, KS - 1 - s);  // stages issued after s (loads still allowed in flight)
+        if (after >= 2) wait_vm<10>();
+        else if (after == 1) wait_vm<5>();
+        else wait_vm<0>();
+        __syncthreads();  // every wave's part of stage s has landed; slot (s - 1) % S is free
+        if (s + GP_S - 1 < KS) issue(s + GP_S - 1);
+        if constexpr (RB > 0) {
+          const uint8_t* stb = smem + (s % GP_S) * GP_STAGE;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        v4i bq[2];
-        float bs[2];
+          for (int j = 0; j < 2; ++j) {
+            v4i bq[2];
+            float bs[2];
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-          const int c = (cq & 1) * 2 + cb, u = q_own * 8 + j * 4 + c, n = c * 32 + l32;
-          bq[cb] = *reinterpret_cast<const v4i*>(stb + GP_A + u * 1024 + (h * 32 + l32) * 16);
-          bs[cb] = __uint_as_float(uint32_t(stb[GP_A + GP_B + (q_own * 2 + j) * 256 + (n >> 4) * 32 + (n & 15) * 2 + h])
-                                   << 23);
-        }
-        v4i aq[2][2];
-        float asc[2];
+            for (int cb = 0; cb < 2; ++cb) {
+              const int c = (cq & 1) * 2 + cb, u = q_own * 8 + j * 4 + c, n = c * 32 + l32;
+              bq[cb] = *reinterpret_cast<const v4i*>(stb + GP_A + u * 1024 + (h * 32 + l32) * 16);
+              bs[cb] = __uint_as_float(
+                  uint32_t(stb[GP_A + GP_B + (q_own * 2 + j) * 256 + (n >> 4) * 32 + (n & 15) * 2 + h]) << 23);
+            }
+            v4i aq[RB][2];
+            float asc[RB];
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-          const int r = rh * 64 + rb * 32 + l32;
+            for (int rb = 0; rb < RB; ++rb) {
+              const int r = rh * 64 + rb * 32 + l32;
 #pragma unroll
-          for (int x = 0; x < 2; ++x)
-            aq[rb][x] = *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 * j + 2 * h + x) ^ lds_swz(r))) * 16);
-          asc[rb] = __uint_as_float(uint32_t(as_lds[s * 128 + r]) << 23);
-        }
+              for (int x = 0; x < 2; ++x)
+                aq[rb][x] = *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 * j + 2 * h + x) ^ lds_swz(r))) * 16);
+              asc[rb] = __uint_as_float(uint32_t(as_lds[s * 128 + r]) << 23);
+            }
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          bf16x8 bf[2];
+            for (int t = 0; t < 4; ++t) {
+              bf16x8 bf[2];
 #pragma unroll
-          for (int cb = 0; cb < 2; ++cb) bf[cb] = fp4x8_to_bf16(uint32_t(bq[cb][t]), bs[cb]);
+              for (int cb = 0; cb < 2; ++cb) bf[cb] = fp4x8_to_bf16(uint32_t(bq[cb][t]), bs[cb]);
 #pragma unroll
-          for (int rb = 0; rb < 2; ++rb) {
-            if (rb >= rb_live) break;
-            const bf16x8 af =
-                fp8x8_to_bf16(uint32_t(aq[rb][t >> 1][(t & 1) * 2]), uint32_t(aq[rb][t >> 1][(t & 1) * 2 + 1]), asc[rb]);
+              for (int rb = 0; rb < RB; ++rb) {
+                const bf16x8 af = fp8x8_to_bf16(uint32_t(aq[rb][t >> 1][(t & 1) * 2]),
+                                                uint32_t(aq[rb][t >> 1][(t & 1) * 2 + 1]), asc[rb]);
 #pragma unroll
-            for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = mfma32_bf16(af, bf[cb], acc[rb][cb]);
+                for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = mfma32_bf16(af, bf[cb], acc[rb][cb]);
+              }
+            }
           }
         }
       }
-    }
+    };
+    if (rb_live == 2) kloop(std::integral_constant<int, 2>{});
+    else if (rb_live == 1) kloop(std::integral_constant<int, 1>{});
+    else kloop(std::integral_constant<int, 0>{});  // still takes part in the barriers and issues its DMA share
 
     // ---- epilogue through LDS (the ring is free once every wave is past its last stage)
     __syncthreads();
