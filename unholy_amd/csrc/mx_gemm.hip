@@ -345,6 +345,7 @@ constexpr int GP_S = 4, GP_A = 128 * 128, GP_B = 16 * 1024, GP_BS = 1024;
 constexpr int GP_STAGE = GP_A + GP_B + GP_BS;
 constexpr int GP_RING = GP_S * GP_STAGE;
 constexpr int GP_MAX_KS = (160 * 1024 - GP_RING) / 128;  // activation scales [KS][128] after the ring
+static_assert(GP_RING >= 8 * 16 * 1024, "the K-half exchange reuses the ring: 16 KB per wave");
 
 template <int NP>
 __global__ __launch_bounds__(512) void mx_gemm_pipe_kernel(MxGemvArgs a) {
@@ -365,9 +366,12 @@ __global__ __launch_bounds__(512) void mx_gemm_pipe_kernel(MxGemvArgs a) {
   const int K = a.K, KS = K / 128, N = a.N, ntn = N / 16;
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: addresses derived from it stay scalar
-  // Waves w and w + 4 share a SIMD: give them opposite row halves, so a tile with fewer than 128 rows (the idle
-  // 32-row blocks are all in the upper half) loads every SIMD alike.
-  const int rh = (wave & 1) ^ (wave >> 2), cq = wave >> 1, q_own = cq >> 1;  // projection / column half: q_own
+  // Wave w computes column quarter cq = w % 4 (64 columns; q_own: the projection or column half) over all of the
+  // tile's rows, for K-half jw = w / 4 of every 128-input stage. Waves w and w + 4 share a SIMD and split the
+  // stage's inputs between them, so both have the same work whatever the tile's row count (a split by rows left the
+  // upper-half wave idle at every stage barrier when the tile has fewer than 128 rows). After the K loop each pair
+  // exchanges partial sums: wave jw finishes rows 64 jw .. 64 jw + 63.
+  const int jw = wave >> 2, cq = wave & 3, q_own = cq >> 1;
   // First column (of the N) of projection or half q's 128 columns.
   const int colq0 = NP == 2 ? bx * 128 : bx * 256, colq_step = NP == 2 ? 0 : 128;
   const size_t cslab = size_t(ntn) * 512, sslab = size_t(ntn) * 32;
@@ -406,10 +410,10 @@ __global__ __launch_bounds__(512) void mx_gemm_pipe_kernel(MxGemvArgs a) {
       const uint8_t* sb = sq[sc_q] + size_t(2 * s + sc_j) * sslab + size_t((colq0 + sc_q * colq_step) / 16) * 32;
       if (sc_lane) dma16(sb, bsoff, st + uint32_t(GP_A + GP_B));
     };
-    const int rb_live = __builtin_amdgcn_readfirstlane(min(2, max(0, (M - rh * 64 + 31) / 32)));
-    v16f_t acc[2][2];
+    const int rb_live = __builtin_amdgcn_readfirstlane((M + 31) / 32);  // 32-row blocks with rows: 1 .. 4
+    v16f_t acc[4][2];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
       for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = v16f_t{};
     const int pro = min(GP_S - 1, KS);
@@ -434,49 +438,79 @@ __global__ __launch_bounds__(512) void mx_gemm_pipe_kernel(MxGemvArgs a) {
         else wait_vm<0>();
         __syncthreads();  // every wave's part of stage s has landed; slot (s - 1) % S is free
         if (s + GP_S - 1 < KS) issue(s + GP_S - 1);
-        if constexpr (RB > 0) {
-          const uint8_t* stb = smem + (s % GP_S) * GP_STAGE;
+        const uint8_t* stb = smem + (s % GP_S) * GP_STAGE;
+        v4i bq[2];
+        float bs[2];
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            v4i bq[2];
-            float bs[2];
+        for (int cb = 0; cb < 2; ++cb) {
+          const int c = (cq & 1) * 2 + cb, u = q_own * 8 + jw * 4 + c, n = c * 32 + l32;
+          bq[cb] = *reinterpret_cast<const v4i*>(stb + GP_A + u * 1024 + (h * 32 + l32) * 16);
+          bs[cb] = __uint_as_float(uint32_t(stb[GP_A + GP_B + (q_own * 2 + jw) * 256 + (n >> 4) * 32 + (n & 15) * 2 + h])
+                                   << 23);
+        }
+        v4i aq[RB][2];
+        float asc[RB];
 #pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-              const int c = (cq & 1) * 2 + cb, u = q_own * 8 + j * 4 + c, n = c * 32 + l32;
-              bq[cb] = *reinterpret_cast<const v4i*>(stb + GP_A + u * 1024 + (h * 32 + l32) * 16);
-              bs[cb] = __uint_as_float(
-                  uint32_t(stb[GP_A + GP_B + (q_own * 2 + j) * 256 + (n >> 4) * 32 + (n & 15) * 2 + h]) << 23);
-            }
-            v4i aq[RB][2];
-            float asc[RB];
+        for (int rb = 0; rb < RB; ++rb) {
+          const int r = rb * 32 + l32;
 #pragma unroll
-            for (int rb = 0; rb < RB; ++rb) {
-              const int r = rh * 64 + rb * 32 + l32;
+          for (int x = 0; x < 2; ++x)
+            aq[rb][x] = *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 * jw + 2 * h + x) ^ lds_swz(r))) * 16);
+          asc[rb] = __uint_as_float(uint32_t(as_lds[s * 128 + r]) << 23);
+        }
 #pragma unroll
-              for (int x = 0; x < 2; ++x)
-                aq[rb][x] = *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 * j + 2 * h + x) ^ lds_swz(r))) * 16);
-              asc[rb] = __uint_as_float(uint32_t(as_lds[s * 128 + r]) << 23);
-            }
+        for (int t = 0; t < 4; ++t) {
+          bf16x8 bf[2];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              bf16x8 bf[2];
+          for (int cb = 0; cb < 2; ++cb) bf[cb] = fp4x8_to_bf16(uint32_t(bq[cb][t]), bs[cb]);
 #pragma unroll
-              for (int cb = 0; cb < 2; ++cb) bf[cb] = fp4x8_to_bf16(uint32_t(bq[cb][t]), bs[cb]);
+          for (int rb = 0; rb < RB; ++rb) {
+            const bf16x8 af = fp8x8_to_bf16(uint32_t(aq[rb][t >> 1][(t & 1) * 2]),
+                                            uint32_t(aq[rb][t >> 1][(t & 1) * 2 + 1]), asc[rb]);
 #pragma unroll
-              for (int rb = 0; rb < RB; ++rb) {
-                const bf16x8 af = fp8x8_to_bf16(uint32_t(aq[rb][t >> 1][(t & 1) * 2]),
-                                                uint32_t(aq[rb][t >> 1][(t & 1) * 2 + 1]), asc[rb]);
-#pragma unroll
-                for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = mfma32_bf16(af, bf[cb], acc[rb][cb]);
-              }
-            }
+            for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = mfma32_bf16(af, bf[cb], acc[rb][cb]);
           }
         }
       }
     };
-    if (rb_live == 2) kloop(std::integral_constant<int, 2>{});
-    else if (rb_live == 1) kloop(std::integral_constant<int, 1>{});
-    else kloop(std::integral_constant<int, 0>{});  // still takes part in the barriers and issues its DMA share
+    if (rb_live == 4) kloop(std::integral_constant<int, 4>{});
+    else if (rb_live == 3) kloop(std::integral_constant<int, 3>{});
+    else if (rb_live == 2) kloop(std::integral_constant<int, 2>{});
+    else kloop(std::integral_constant<int, 1>{});
+
+    // ---- partial sums of the two K halves: wave jw sends its sums for the partner's rows (64 (1 - jw) ..) through
+    // the ring's LDS (free once every wave is past its last stage) and adds the partner's for its own rows; its rows
+    // then sit in acc[0..1]. Blocks without rows hold zeros.
+    __syncthreads();
+    {
+      float* const xbuf = reinterpret_cast<float*>(smem);  // [wave][2 rb][2 cb][16][64 lanes]: 16 KB per wave
+      const int partner = wave ^ 4;
+      if (jw == 0) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) xbuf[(((wave * 2 + k) * 2 + cb) * 16 + i) * 64 + lane] = acc[2 + k][cb][i];
+      } else {
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) xbuf[(((wave * 2 + k) * 2 + cb) * 16 + i) * 64 + lane] = acc[k][cb][i];
+            acc[k][cb] = acc[2 + k][cb];
+          }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc[k][cb][i] += xbuf[(((partner * 2 + k) * 2 + cb) * 16 + i) * 64 + lane];
+    }
+    const int rh = jw;
 
     // ---- epilogue through LDS (the ring is free once every wave is past its last stage)
     __syncthreads();
