@@ -328,27 +328,32 @@ __global__ __launch_bounds__(256 * NP) void mx_gemm_kernel(MxGemvArgs a) {
   }
 }
 
-// ---- Pipelined kernel for fp8 activation codes: a 4-stage LDS ring filled by direct global -> LDS loads ----
+// ---- Pipelined kernel for fp8 activation codes: an LDS ring filled by direct global -> LDS loads ----------------
 //
-// Workgroup = 512 threads, one tile x 256 output columns: 128 columns each of w1 and w3 (NP 2, SwiGLU epilogue)
-// or 256 columns of one matrix (NP 1). Wave w owns 64 rows and columns 64 (w >> 1) .. + 63 of the
-// 256 (rows: see rh below). Per 128-input stage the ring slot holds
+// Workgroup = 256 threads (4 waves), one tile x 256 output columns: 128 columns each of w1 and w3 (NP 2, SwiGLU
+// epilogue) or 256 columns of one matrix (NP 1). Wave w computes columns 64 w .. 64 w + 63 over all of the tile's
+// rows: 4 x 2 MFMA blocks of 32 x 32, 3 conversions per MFMA. Per 128-input stage a ring slot holds
 //   A  16 KB: the tile's fp8 codes, row r's 16-byte piece p at slot r * 8 + (p ^ lds_swz(r)) (conflict-free MFMA reads);
 //   B  16 KB: 16 blocks of 1 KB = (projection or column half q, 64-input slab j, 32-column block c); slot h * 32 + n
 //      of a block holds input half h (32 codes) of its column n, so a wave's operand read is 1 KB contiguous;
 //   Bs  1 KB: the e8m0 weight scales of (q, j) in their global order (256 B each).
-// The loads are issued S - 1 stages ahead by every wave (5 per stage) and complete in order, so "stage s has landed"
-// is a vmcnt count. They are written as inline assembly: the compiler, seeing LDS writes from global loads, would
-// otherwise wait for every one of them before each LDS read and drain the ring. The activation scales of all stages
-// are copied to LDS once per row group.
-constexpr int GP_S = 4, GP_A = 128 * 128, GP_B = 16 * 1024, GP_BS = 1024;
+// Two slots (66 KB) plus the activation scales of all stages (copied once per row group) keep a workgroup within
+// 80 KB of LDS, so two workgroups share a CU. Each has its own stage barriers: while one waits at a barrier or for
+// its first operands, the other's MFMAs run. (One 8-wave workgroup per CU with a 4-slot ring stalled both waves of
+// every SIMD at each barrier and measured 12-16% slower.) Every wave issues 4 A, 4 B and 1 scale load per stage;
+// stage s + 1 is issued right after stage s's barrier, so only stage s is in flight when it is waited for. The loads
+// are inline assembly: the compiler, seeing LDS written from global loads, would otherwise wait for every one of
+// them before each LDS read.
+constexpr int GP_A = 128 * 128, GP_B = 16 * 1024, GP_BS = 1024;
 constexpr int GP_STAGE = GP_A + GP_B + GP_BS;
-constexpr int GP_RING = GP_S * GP_STAGE;
-constexpr int GP_MAX_KS = (160 * 1024 - GP_RING) / 128;  // activation scales [KS][128] after the ring
-static_assert(GP_RING >= 8 * 16 * 1024, "the K-half exchange reuses the ring: 16 KB per wave");
+constexpr int GP_S = 2, GP_RING = GP_S * GP_STAGE;
+constexpr int GP_MAX_KS = (80 * 1024 - GP_RING) / 128;  // activation scales [KS][128] after the ring
+constexpr int GP_LDC1 = 256 + 8, GP_LDC2 = 128 + 8;
+constexpr int GP_C1 = 128 * GP_LDC1 * 2, GP_C2 = 2 * 128 * GP_LDC2 * 2;
+static_assert(GP_C1 <= GP_RING, "the bf16 C tile reuses the ring");
 
 template <int NP>
-__global__ __launch_bounds__(512) void mx_gemm_pipe_kernel(MxGemvArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mx_gemm_pipe_kernel(MxGemvArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   int bx, by;
   tile_block(gridDim.x, bx, by);
@@ -365,110 +370,92 @@ __global__ __launch_bounds__(512) void mx_gemm_pipe_kernel(MxGemvArgs a) {
   }
   const int K = a.K, KS = K / 128, N = a.N, ntn = N / 16;
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: addresses derived from it stay scalar
-  // Wave w computes column quarter cq = w % 4 (64 columns; q_own: the projection or column half) over all of the
-  // tile's rows, for K-half jw = w / 4 of every 128-input stage. Waves w and w + 4 share a SIMD and split the
-  // stage's inputs between them, so both have the same work whatever the tile's row count (a split by rows left the
-  // upper-half wave idle at every stage barrier when the tile has fewer than 128 rows). After the K loop each pair
-  // exchanges partial sums: wave jw finishes rows 64 jw .. 64 jw + 63.
-  const int jw = wave >> 2, cq = wave & 3, q_own = cq >> 1;
-  // First column (of the N) of projection or half q's 128 columns.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // column quarter
+  const int cq = wave, q_own = cq >> 1;
   const int colq0 = NP == 2 ? bx * 128 : bx * 256, colq_step = NP == 2 ? 0 : 128;
   const size_t cslab = size_t(ntn) * 512, sslab = size_t(ntn) * 32;
   const uint32_t lds0 = lds_addr(smem);
   uint8_t* const as_lds = smem + GP_RING;
-
-  // Per-lane DMA offsets, constant over the stages.
-  const uint32_t boff = uint32_t((l32 * 2 + h) * 16);                      // B block: slot h*32+n <- piece 2n+h
-  const bool sc_lane = (lane >> 3) == wave;                                 // 8 lanes per wave carry the scales
-  const uint32_t bsoff = uint32_t(((wave & 1) * 8 + (lane & 7)) * 16);     // piece 8w + lane%8 of (q, j) = w / 2
-  const int sc_q = wave >> 2, sc_j = (wave >> 1) & 1;
+  const uint32_t boff = uint32_t((l32 * 2 + h) * 16);  // B block: slot h*32+n <- piece 2n+h
+  const int sc_q = wave >> 1, sc_j = wave & 1;         // this wave's 256-byte scale run (q, j)
 
   for (int rg = 0; rg < tile.rows; rg += 128) {
     const int M = min(128, tile.rows - rg);
     const size_t row0 = size_t(tile.row0) + rg;
     __syncthreads();  // the previous row group's LDS use is over
-    uint32_t aoff[2];
+    uint32_t aoff[4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int slot = (wave * 2 + i) * 64 + lane, r = slot >> 3, p = (slot & 7) ^ lds_swz(r);
-      // Rows past the tile repeat its last. With x_rows the loads gather token rows (offsets from q itself).
-      const int rr = min(r, M - 1);
+    for (int i = 0; i < 4; ++i) {
+      const int slot = (wave * 4 + i) * 64 + lane, r = slot >> 3, p = (slot & 7) ^ lds_swz(r);
+      const int rr = min(r, M - 1);  // rows past the tile repeat its last
       aoff[i] = (a.x_rows ? uint32_t(a.x_rows[row0 + rr]) : uint32_t(rr)) * uint32_t(K) + uint32_t(p * 16);
     }
     const uint8_t* arow = a.x_rows ? a.aq : a.aq + row0 * size_t(K);
     const auto issue = [&](int s) {
       const uint32_t st = __builtin_amdgcn_readfirstlane(lds0 + uint32_t((s % GP_S) * GP_STAGE));
-      dma16(arow + s * 128, aoff[0], st + uint32_t(wave * 2) * 1024);
-      dma16(arow + s * 128, aoff[1], st + uint32_t(wave * 2 + 1) * 1024);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int u = wave * 2 + i, q = u >> 3, j = (u >> 2) & 1, c = u & 3;
+      for (int i = 0; i < 4; ++i) dma16(arow + s * 128, aoff[i], st + uint32_t(wave * 4 + i) * 1024);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int u = wave * 4 + i, q = u >> 3, j = (u >> 2) & 1, c = u & 3;
         const uint8_t* bb = wq[q] + size_t(2 * s + j) * cslab + size_t((colq0 + q * colq_step) / 16) * 512 + c * 1024;
         dma16(bb, boff, st + uint32_t(GP_A + u * 1024));
       }
       const uint8_t* sb = sq[sc_q] + size_t(2 * s + sc_j) * sslab + size_t((colq0 + sc_q * colq_step) / 16) * 32;
-      if (sc_lane) dma16(sb, bsoff, st + uint32_t(GP_A + GP_B));
+      if (lane < 16) dma16(sb, uint32_t(lane) * 16, st + uint32_t(GP_A + GP_B + (sc_q * 2 + sc_j) * 256));
     };
-    const int rb_live = __builtin_amdgcn_readfirstlane((M + 31) / 32);  // 32-row blocks with rows: 1 .. 4
+    const int rb_live = __builtin_amdgcn_readfirstlane((M + 31) / 32);
     v16f_t acc[4][2];
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
       for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = v16f_t{};
-    const int pro = min(GP_S - 1, KS);
-    for (int s = 0; s < pro; ++s) issue(s);
-    // The activation scales are preloaded after the first stages are in flight: their row indices are the ones the
-    // DMA offsets just read, and the preload's loads overlap the stages' (its wait also covers them, which stage 0
-    // needs anyway). Every thread keeps one row (512 % 128 == 0).
-    {
+    issue(0);
+    {  // activation scales, after stage 0 is in flight (every thread keeps one row: 256 % 128 == 0)
       const int r = min(tid & 127, M - 1);
       const uint8_t* srow = a.as + size_t(a.x_rows ? a.x_rows[row0 + r] : int(row0 + r)) * KS;
-      for (int e = tid; e < 128 * KS; e += 512) as_lds[e] = srow[e >> 7];
+      for (int e = tid; e < 128 * KS; e += 256) as_lds[e] = srow[e >> 7];
     }
-
-    // The K loop, specialised on the wave's live 32-row blocks (constant over the row group): each stage is then one
-    // basic block that the compiler can interleave (conversions of the next step between the MFMAs of this one).
     const auto kloop = [&](auto nrb) {
       constexpr int RB = decltype(nrb)::value;
       for (int s = 0; s < KS; ++s) {
-        const int after = min(GP_S - 2, KS - 1 - s);  // stages issued after s (loads still allowed in flight)
-        if (after >= 2) wait_vm<10>();
-        else if (after == 1) wait_vm<5>();
-        else wait_vm<0>();
-        __syncthreads();  // every wave's part of stage s has landed; slot (s - 1) % S is free
-        if (s + GP_S - 1 < KS) issue(s + GP_S - 1);
+        wait_vm<0>();     // this wave's part of stage s (the only stage in flight)
+        __syncthreads();  // every wave's part has landed; the other slot (stage s - 1) is free
+        if (s + 1 < KS) issue(s + 1);
         const uint8_t* stb = smem + (s % GP_S) * GP_STAGE;
-        v4i bq[2];
-        float bs[2];
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-          const int c = (cq & 1) * 2 + cb, u = q_own * 8 + jw * 4 + c, n = c * 32 + l32;
-          bq[cb] = *reinterpret_cast<const v4i*>(stb + GP_A + u * 1024 + (h * 32 + l32) * 16);
-          bs[cb] = __uint_as_float(uint32_t(stb[GP_A + GP_B + (q_own * 2 + jw) * 256 + (n >> 4) * 32 + (n & 15) * 2 + h])
-                                   << 23);
-        }
-        v4i aq[RB][2];
-        float asc[RB];
+        for (int j = 0; j < 2; ++j) {
+          v4i bq[2];
+          float bs[2];
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-          const int r = rb * 32 + l32;
-#pragma unroll
-          for (int x = 0; x < 2; ++x)
-            aq[rb][x] = *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 * jw + 2 * h + x) ^ lds_swz(r))) * 16);
-          asc[rb] = __uint_as_float(uint32_t(as_lds[s * 128 + r]) << 23);
-        }
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          bf16x8 bf[2];
-#pragma unroll
-          for (int cb = 0; cb < 2; ++cb) bf[cb] = fp4x8_to_bf16(uint32_t(bq[cb][t]), bs[cb]);
+          for (int cb = 0; cb < 2; ++cb) {
+            const int c = (cq & 1) * 2 + cb, u = q_own * 8 + j * 4 + c, n = c * 32 + l32;
+            bq[cb] = *reinterpret_cast<const v4i*>(stb + GP_A + u * 1024 + (h * 32 + l32) * 16);
+            bs[cb] = __uint_as_float(
+                uint32_t(stb[GP_A + GP_B + (q_own * 2 + j) * 256 + (n >> 4) * 32 + (n & 15) * 2 + h]) << 23);
+          }
+          v4i aq[RB][2];
+          float asc[RB];
 #pragma unroll
           for (int rb = 0; rb < RB; ++rb) {
-            const bf16x8 af = fp8x8_to_bf16(uint32_t(aq[rb][t >> 1][(t & 1) * 2]),
-                                            uint32_t(aq[rb][t >> 1][(t & 1) * 2 + 1]), asc[rb]);
+            const int r = rb * 32 + l32;
 #pragma unroll
-            for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = mfma32_bf16(af, bf[cb], acc[rb][cb]);
+            for (int x = 0; x < 2; ++x)
+              aq[rb][x] = *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 * j + 2 * h + x) ^ lds_swz(r))) * 16);
+            asc[rb] = __uint_as_float(uint32_t(as_lds[s * 128 + r]) << 23);
+          }
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            bf16x8 bf[2];
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) bf[cb] = fp4x8_to_bf16(uint32_t(bq[cb][t]), bs[cb]);
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+              const bf16x8 af = fp8x8_to_bf16(uint32_t(aq[rb][t >> 1][(t & 1) * 2]),
+                                              uint32_t(aq[rb][t >> 1][(t & 1) * 2 + 1]), asc[rb]);
+#pragma unroll
+              for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = mfma32_bf16(af, bf[cb], acc[rb][cb]);
+            }
           }
         }
       }
@@ -478,99 +465,67 @@ __global__ __launch_bounds__(512) void mx_gemm_pipe_kernel(MxGemvArgs a) {
     else if (rb_live == 2) kloop(std::integral_constant<int, 2>{});
     else kloop(std::integral_constant<int, 1>{});
 
-    // ---- partial sums of the two K halves: wave jw sends its sums for the partner's rows (64 (1 - jw) ..) through
-    // the ring's LDS (free once every wave is past its last stage) and adds the partner's for its own rows; its rows
-    // then sit in acc[0..1]. Blocks without rows hold zeros.
+    // ---- epilogue (the ring is free once every wave is past its last stage)
     __syncthreads();
-    {
-      float* const xbuf = reinterpret_cast<float*>(smem);  // [wave][2 rb][2 cb][16][64 lanes]: 16 KB per wave
-      const int partner = wave ^ 4;
-      if (jw == 0) {
-#pragma unroll
-        for (int k = 0; k < 2; ++k)
-#pragma unroll
-          for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) xbuf[(((wave * 2 + k) * 2 + cb) * 16 + i) * 64 + lane] = acc[2 + k][cb][i];
-      } else {
-#pragma unroll
-        for (int k = 0; k < 2; ++k)
-#pragma unroll
-          for (int cb = 0; cb < 2; ++cb) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) xbuf[(((wave * 2 + k) * 2 + cb) * 16 + i) * 64 + lane] = acc[k][cb][i];
-            acc[k][cb] = acc[2 + k][cb];
-          }
-      }
-      __syncthreads();
-#pragma unroll
-      for (int k = 0; k < 2; ++k)
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) acc[k][cb][i] += xbuf[(((partner * 2 + k) * 2 + cb) * 16 + i) * 64 + lane];
-    }
-    const int rh = jw;
-
-    // ---- epilogue through LDS (the ring is free once every wave is past its last stage)
-    __syncthreads();
-    const auto row_of = [&](int rb, int i) { return rh * 64 + rb * 32 + 8 * (i / 4) + 4 * h + (i % 4); };
+    const auto row_of = [&](int rb, int i) { return rb * 32 + 8 * (i / 4) + 4 * h + (i % 4); };
     if constexpr (NP == 1) {
       const int c0 = cq * 64;
-      if (a.out32) {
+      if (a.out32) {  // fp32 outputs (accuracy checks): two passes of 64 rows through the ring
         constexpr int LDF = 256 + 4;
+        static_assert(64 * LDF * 4 <= GP_RING, "a 64-row fp32 half tile fits the ring");
         float* sf = reinterpret_cast<float*>(smem);
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
+        for (int half = 0; half < 2; ++half) {
+          if (half) __syncthreads();  // the first half's stores have read the tile
 #pragma unroll
-          for (int cb = 0; cb < 2; ++cb)
+          for (int k = 0; k < 2; ++k)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) sf[row_of(rb, i) * LDF + c0 + cb * 32 + l32] = acc[rb][cb][i];
-        __syncthreads();
-        for (int e = tid; e < M * 64; e += 512) {
-          const int r = e / 64, c4 = (e % 64) * 4;
-          *reinterpret_cast<float4*>(a.out32 + (row0 + r) * a.ldo + bx * 256 + c4) =
-              *reinterpret_cast<const float4*>(sf + r * LDF + c4);
+            for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+              for (int i = 0; i < 16; ++i)
+                sf[(row_of(k, i)) * LDF + c0 + cb * 32 + l32] = acc[2 * half + k][cb][i];
+          __syncthreads();
+          for (int e = tid; e < min(64, M - 64 * half) * 64; e += 256) {
+            const int r = e / 64, c4 = (e % 64) * 4;
+            *reinterpret_cast<float4*>(a.out32 + (row0 + 64 * half + r) * a.ldo + bx * 256 + c4) =
+                *reinterpret_cast<const float4*>(sf + r * LDF + c4);
+          }
         }
       } else {
-        constexpr int LDC = 256 + 8;
         uint16_t* sc = reinterpret_cast<uint16_t*>(smem);
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
+        for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
           for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) sc[row_of(rb, i) * LDC + c0 + cb * 32 + l32] = f32_to_bf16(acc[rb][cb][i]);
+            for (int i = 0; i < 16; ++i) sc[row_of(rb, i) * GP_LDC1 + c0 + cb * 32 + l32] = f32_to_bf16(acc[rb][cb][i]);
         __syncthreads();
-        for (int e = tid; e < M * 32; e += 512) {
+        for (int e = tid; e < M * 32; e += 256) {
           const int r = e / 32, c8 = (e % 32) * 8;
           *reinterpret_cast<uint4*>(a.out[0] + (row0 + r) * a.ldo + bx * 256 + c8) =
-              *reinterpret_cast<const uint4*>(sc + r * LDC + c8);
+              *reinterpret_cast<const uint4*>(sc + r * GP_LDC1 + c8);
         }
       }
     } else {
-      // 1. every wave: bf16 of its projection (g for w1, u for w3) into that projection's 128-column LDS tile.
-      // 2. the workgroup, 8 consecutive outputs of one row per thread: h = bf16(SwiGLU(g, u)), the row's amax over
-      //    its 128 outputs (16 threads: a DPP row max), fake quantization, 16-byte stores.
-      constexpr int LDC = 128 + 8;
+      // bf16 g (w1) and u (w3) tiles in LDS, then 8 consecutive outputs of one row per thread: h = bf16(SwiGLU(g, u)),
+      // the row's amax over its 128 outputs (16 threads: a DPP row max), fake quantization, 16-byte stores.
       uint16_t* const tg = reinterpret_cast<uint16_t*>(smem);
-      uint16_t* const tu = tg + 128 * LDC;
+      uint16_t* const tu = tg + 128 * GP_LDC2;
       uint16_t* const mine = q_own ? tu : tg;
       const int chh = cq & 1;
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
+      for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) mine[row_of(rb, i) * LDC + chh * 64 + cb * 32 + l32] = f32_to_bf16(acc[rb][cb][i]);
+          for (int i = 0; i < 16; ++i)
+            mine[row_of(rb, i) * GP_LDC2 + chh * 64 + cb * 32 + l32] = f32_to_bf16(acc[rb][cb][i]);
       __syncthreads();
-      // The loop bound is uniform, so every 16-lane group is whole; threads past the tile's rows only take part in
-      // the max.
-      for (int e0 = 0; e0 < M * 16; e0 += 512) {
+      for (int e0 = 0; e0 < M * 16; e0 += 256) {  // uniform bound: every 16-lane group is whole
         const int e = e0 + tid, r = min(e / 16, M - 1), c8 = (e % 16) * 8;
         const size_t row = row0 + r;
-        const uint4 gv4 = *reinterpret_cast<const uint4*>(tg + r * LDC + c8);
-        const uint4 uv4 = *reinterpret_cast<const uint4*>(tu + r * LDC + c8);
+        const uint4 gv4 = *reinterpret_cast<const uint4*>(tg + r * GP_LDC2 + c8);
+        const uint4 uv4 = *reinterpret_cast<const uint4*>(tu + r * GP_LDC2 + c8);
         const uint32_t gw4[4] = {gv4.x, gv4.y, gv4.z, gv4.w}, uw4[4] = {uv4.x, uv4.y, uv4.z, uv4.w};
         const float w = a.gw ? a.gw[row] : 0.0f;
         float hv[8], am = 0.0f;
@@ -593,7 +548,7 @@ __global__ __launch_bounds__(512) void mx_gemm_pipe_kernel(MxGemvArgs a) {
         for (int q = 0; q < 8; ++q) qb[q / 4] |= uint32_t(fp8_code(hv[q], blk)) << (8 * (q % 4));
         const size_t o = row * N + size_t(bx) * 128 + c8;
         if (a.hq) *reinterpret_cast<uint2*>(a.hq + o) = make_uint2(qb[0], qb[1]);
-        if (a.hh) {  // the fake-quantized bf16 rows, only when asked for
+        if (a.hh) {
           uint32_t fq[4];
 #pragma unroll
           for (int q = 0; q < 8; ++q) {
@@ -610,13 +565,13 @@ __global__ __launch_bounds__(512) void mx_gemm_pipe_kernel(MxGemvArgs a) {
 
 template <int NP>
 void launch_pipe_t(const MxGemvArgs& a, int ntiles, hipStream_t st) {
-  const size_t lds = size_t(GP_RING) + size_t(128) * (a.K / 128);
+  const size_t lds = std::max<size_t>(size_t(GP_RING) + size_t(128) * (a.K / 128), NP == 2 ? GP_C2 : GP_C1);
   auto* kern = &mx_gemm_pipe_kernel<NP>;
   UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                int(lds)));
   MxGemvArgs b = a;
   b.ntiles = ntiles;
-  kern<<<tile_grid(a.N / (NP == 2 ? 128 : 256), ntiles), 512, lds, st>>>(b);
+  kern<<<tile_grid(a.N / (NP == 2 ? 128 : 256), ntiles), 256, lds, st>>>(b);
   UH_CHECK_LAUNCH();
 }
 
@@ -642,6 +597,7 @@ static bool pipe_disabled() {
   }();
   return off;
 }
+
 
 void launch_mx_gemm(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st) {
   if (ntiles <= 0) return;
@@ -673,7 +629,7 @@ void launch_mx_gemm(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st) 
                 : launch_gemm_t<NP, 0>(a, ntiles, st))
   const bool pipe = amode == 0 && a.K / GM_KS <= GP_MAX_KS && !pipe_disabled();
   if (amode == 0 && a.x_rows && (!pipe || (!glu && a.N % 256)))
-    throw std::runtime_error("mx_grouped_gemm_q: x_rows needs the pipelined kernel (K <= 28672, N % 256 without glu)");
+    throw std::runtime_error("mx_grouped_gemm_q: x_rows needs the pipelined kernel (K <= 14336, N % 256 without glu)");
   if (glu) {
     if (pipe) launch_pipe_t<2>(a, ntiles, st);
     else UH_GM(2);
