@@ -2,12 +2,13 @@
 // gemm_w8a8, the reference's ref_gemm.hip:130-137 / gemm_wmma.hip:51-183; fp32 for the 1x128 / 128x128 format of
 // tools/ref/oracle/kernel.py:81-118).
 //
-// Workgroup = 512 threads, 128 rows x 256 columns; wave w owns 64 rows (the two waves sharing a SIMD take opposite
-// halves) and columns 64 (w >> 1) .. + 63. Per 128-input stage a 3-slot LDS ring holds
+// Workgroup = 256 threads, 128 rows x 128 columns; wave w owns rows 64 (w & 1) .. + 63 and columns 64 (w >> 1) .. + 63.
+// Per 128-input stage a 2-slot LDS ring holds
 //   A 16 KB: row r's 16-byte piece p at slot r * 8 + (p ^ lds_swz(r)),
-//   B 32 KB: column n's 16-byte piece p at slot n * 8 + (p ^ lds_swz(n)) (W is row-major like A),
+//   B 16 KB: column n's 16-byte piece p at slot n * 8 + (p ^ lds_swz(n)) (W is row-major like A),
 //   S 512 B: fp32 activation scales of the 128 rows (fp32 form only, one gathered dword per row),
-// filled by direct global -> LDS loads issued two stages ahead (6 or 7 per wave per stage, counted with vmcnt).
+// filled by direct global -> LDS loads: stage s + 1 is issued right after stage s's barrier. A workgroup stays under
+// 80 KB of LDS, so two share a CU and one's barriers and operand waits overlap the other's MFMAs.
 // Both operands are dequantized exactly to bf16 at the LDS read and multiplied on the 32x32x16 bf16 MFMA. e8m0
 // scales are folded into the conversions (exact) and the MFMA accumulates across blocks; with fp32 scales each
 // block's MFMA chain starts from zero and is folded as acc += raw * (sa * sw), the reference's order of scaling.
@@ -25,66 +26,63 @@ using namespace pipe;
 
 namespace {
 
-constexpr int FT_S = 3, FT_A = 128 * 128, FT_B = 256 * 128, FT_SA = 128 * 4;
+constexpr int FT_S = 2, FT_A = 128 * 128, FT_B = 128 * 128, FT_SA = 128 * 4;
 constexpr int FT_STAGE = FT_A + FT_B + FT_SA;
 constexpr int FT_RING = FT_S * FT_STAGE;
+constexpr int FT_LDC = 128 + 8;
+static_assert(128 * FT_LDC * 2 <= FT_RING, "the bf16 C tile reuses the ring");
+size_t tiled_lds(int K, bool f32s) { return size_t(FT_RING) + size_t(4 + (f32s ? 0 : 128)) * (K / 128); }
 
 template <bool F32S>
-__global__ __launch_bounds__(512) void fp8_tiled_kernel(Fp8GemmArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void fp8_tiled_kernel(Fp8GemmArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   int bx, by;
   tile_block(gridDim.x, bx, by);
   const int K = a.K, KS = K / 128, M = a.M;
   const int row0 = by * 128;
   if (row0 >= M) return;  // padding of the grid's row-tile count
-  const int Mt = min(128, M - row0), col0 = bx * 256;
+  const int Mt = min(128, M - row0), col0 = bx * 128;
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int rh = (wave & 1) ^ (wave >> 2), cq = wave >> 1;
+  const int rh = wave & 1, ch = wave >> 1;
   const uint32_t lds0 = lds_addr(smem);
-  // After the ring: the weight scales of the workgroup's two 128-column blocks [2][KS] as fp32, then (e8m0 form) the
+  // After the ring: the weight scales of the workgroup's 128-column block [KS] as fp32, then (e8m0 form) the
   // activation scales [KS][128]. Copied once, so the stage loop issues no global loads besides the ring's.
   float* const sw_lds = reinterpret_cast<float*>(smem + FT_RING);
-  uint8_t* const sa_lds = smem + FT_RING + 8 * KS;
+  uint8_t* const sa_lds = smem + FT_RING + 4 * KS;
 
   // Per-lane load offsets (constant over the stages). Rows past the tile repeat its last row (never stored).
-  uint32_t aoff[2], boff[4];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int slot = (wave * 2 + i) * 64 + lane, r = slot >> 3, p = (slot & 7) ^ lds_swz(r);
-    aoff[i] = uint32_t(min(r, Mt - 1)) * uint32_t(K) + uint32_t(p * 16);
-  }
+  uint32_t aoff[4], boff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int slot = (wave * 4 + i) * 64 + lane, n = slot >> 3, p = (slot & 7) ^ lds_swz(n);
-    boff[i] = uint32_t(n) * uint32_t(K) + uint32_t(p * 16);
+    const int slot = (wave * 4 + i) * 64 + lane, r = slot >> 3, p = (slot & 7) ^ lds_swz(r);
+    aoff[i] = uint32_t(min(r, Mt - 1)) * uint32_t(K) + uint32_t(p * 16);
+    boff[i] = uint32_t(r) * uint32_t(K) + uint32_t(p * 16);  // columns: the same slot geometry
   }
-  // fp32 activation scales: lanes 16 (w % 4) .. + 15 of wave w gather rows 64 (w / 4) + lane.
-  const bool sa_lane = (lane >> 4) == (wave & 3);
-  const uint32_t saoff = uint32_t(min((wave >> 2) * 64 + lane, Mt - 1)) * uint32_t(KS) * 4u;
+  // fp32 activation scales: waves 0 and 1 gather rows 64 w + lane.
+  const uint32_t saoff = uint32_t(min((wave & 1) * 64 + lane, Mt - 1)) * uint32_t(KS) * 4u;
 
-  for (int e = tid; e < 2 * KS; e += 512) {
-    const size_t i = size_t(col0 / 128 + e / KS) * KS + e % KS;
-    sw_lds[e] = F32S ? a.sw32[i] : e8m0_to_f32(a.sw8[i]);
-  }
-  if constexpr (!F32S) {
-    for (int e = tid; e < 128 * KS; e += 512) {
-      const int r = min(e & 127, Mt - 1), s = e >> 7;
-      sa_lds[e] = a.sa8[size_t(row0 + r) * KS + s];
-    }
-  }
   const uint8_t* arow = a.a + size_t(row0) * K;
   const uint8_t* wcol = a.w + size_t(col0) * K;
   const auto issue = [&](int s) {
     const uint32_t st = lds0 + uint32_t((s % FT_S) * FT_STAGE);
-    dma16(arow + s * 128, aoff[0], st + uint32_t(wave * 2) * 1024);
-    dma16(arow + s * 128, aoff[1], st + uint32_t(wave * 2 + 1) * 1024);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma16(arow + s * 128, aoff[i], st + uint32_t(wave * 4 + i) * 1024);
 #pragma unroll
     for (int i = 0; i < 4; ++i) dma16(wcol + s * 128, boff[i], st + uint32_t(FT_A + (wave * 4 + i) * 1024));
     if constexpr (F32S)
-      if (sa_lane) dma4(a.sa32 + size_t(row0) * KS + s, saoff, st + uint32_t(FT_A + FT_B + (wave >> 2) * 256));
+      if (wave < 2) dma4(a.sa32 + size_t(row0) * KS + s, saoff, st + uint32_t(FT_A + FT_B + wave * 256));
   };
-  constexpr int PER = F32S ? 7 : 6;  // loads per wave per stage
+  issue(0);
+  // Scales, after stage 0 is in flight.
+  for (int e = tid; e < KS; e += 256) {
+    const size_t i = size_t(col0 / 128) * KS + e;
+    sw_lds[e] = F32S ? a.sw32[i] : e8m0_to_f32(a.sw8[i]);
+  }
+  if constexpr (!F32S) {
+    const int r = min(tid & 127, Mt - 1);
+    for (int e = tid; e < 128 * KS; e += 256) sa_lds[e] = a.sa8[size_t(row0 + r) * KS + (e >> 7)];
+  }
 
   const int rb_live = __builtin_amdgcn_readfirstlane(min(2, max(0, (Mt - rh * 64 + 31) / 32)));
   v16f_t acc[2][2];
@@ -92,17 +90,13 @@ __global__ __launch_bounds__(512) void fp8_tiled_kernel(Fp8GemmArgs a) {
   for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = v16f_t{};
-  const float* swq = sw_lds + (cq >> 1) * KS;  // the wave's 64 columns lie in one 128-column scale block
-  const int pro = min(FT_S - 1, KS);
-  for (int s = 0; s < pro; ++s) issue(s);
 
   for (int s = 0; s < KS; ++s) {
-    if (s + 1 < KS) wait_vm<PER>();  // stage s + 1 may stay in flight
-    else wait_vm<0>();
-    __syncthreads();  // stage s has landed for every wave; slot (s - 1) % S is free
-    if (s + FT_S - 1 < KS) issue(s + FT_S - 1);
+    wait_vm<0>();     // this wave's part of stage s (the only stage in flight)
+    __syncthreads();  // every wave's part has landed; the other slot (stage s - 1) is free
+    if (s + 1 < KS) issue(s + 1);
     const uint8_t* stb = smem + (s % FT_S) * FT_STAGE;
-    const float swv = swq[s];
+    const float swv = sw_lds[s];
     float asc[2];
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
@@ -119,7 +113,7 @@ __global__ __launch_bounds__(512) void fp8_tiled_kernel(Fp8GemmArgs a) {
       v4i aq[2][2], bq[2][2];
 #pragma unroll
       for (int cb = 0; cb < 2; ++cb) {
-        const int n = cq * 64 + cb * 32 + l32;
+        const int n = ch * 64 + cb * 32 + l32;
 #pragma unroll
         for (int x = 0; x < 2; ++x)
           bq[cb][x] = *reinterpret_cast<const v4i*>(stb + FT_A + (n * 8 + ((4 * j + 2 * h + x) ^ lds_swz(n))) * 16);
@@ -170,9 +164,8 @@ __global__ __launch_bounds__(512) void fp8_tiled_kernel(Fp8GemmArgs a) {
     }
   }
 
-  // ---- epilogue through LDS: 128 x 256 bf16, then 16-byte row stores
+  // ---- epilogue through LDS: 128 x 128 bf16, then 16-byte row stores
   __syncthreads();
-  constexpr int LDC = 256 + 8;
   uint16_t* sc = reinterpret_cast<uint16_t*>(smem);
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb)
@@ -180,36 +173,36 @@ __global__ __launch_bounds__(512) void fp8_tiled_kernel(Fp8GemmArgs a) {
     for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
       for (int i = 0; i < 16; ++i)
-        sc[(rh * 64 + rb * 32 + 8 * (i / 4) + 4 * h + (i % 4)) * LDC + cq * 64 + cb * 32 + l32] =
+        sc[(rh * 64 + rb * 32 + 8 * (i / 4) + 4 * h + (i % 4)) * FT_LDC + ch * 64 + cb * 32 + l32] =
             f32_to_bf16(acc[rb][cb][i]);
   __syncthreads();
-  for (int e = tid; e < Mt * 32; e += 512) {
-    const int r = e / 32, c8 = (e % 32) * 8;
+  for (int e = tid; e < Mt * 16; e += 256) {
+    const int r = e / 16, c8 = (e % 16) * 8;
     *reinterpret_cast<uint4*>(a.c + size_t(row0 + r) * a.ldc + col0 + c8) =
-        *reinterpret_cast<const uint4*>(sc + r * LDC + c8);
+        *reinterpret_cast<const uint4*>(sc + r * FT_LDC + c8);
   }
 }
 
 template <bool F32S>
 void launch_tiled_t(const Fp8GemmArgs& a, hipStream_t st) {
-  const size_t lds = size_t(FT_RING) + size_t(8 + (F32S ? 0 : 128)) * (a.K / 128);
+  const size_t lds = tiled_lds(a.K, F32S);
   auto* kern = &fp8_tiled_kernel<F32S>;
   UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                int(lds)));
-  kern<<<tile_grid(a.N / 256, (a.M + 127) / 128), 512, lds, st>>>(a);
+  kern<<<tile_grid(a.N / 128, (a.M + 127) / 128), 256, lds, st>>>(a);
   UH_CHECK_LAUNCH();
 }
 
 }  // namespace
 
 bool fp8_tiled_fits(const Fp8GemmArgs& a) {
-  const size_t lds = size_t(FT_RING) + size_t(8 + (a.sa32 ? 0 : 128)) * (a.K / 128);
-  return a.N % 256 == 0 && a.K % 128 == 0 && a.ldc % 8 == 0 && lds <= 160 * 1024;
+  // two workgroups per CU: 80 KB of LDS each
+  return a.N % 128 == 0 && a.K % 128 == 0 && a.ldc % 8 == 0 && tiled_lds(a.K, a.sa32 != nullptr) <= 80 * 1024;
 }
 
 void launch_fp8_tiled(const Fp8GemmArgs& a, hipStream_t st) {
   if (a.M <= 0) return;
-  if (!fp8_tiled_fits(a)) throw std::runtime_error("fp8 tiled gemm: N % 256, K % 128, ldc % 8");
+  if (!fp8_tiled_fits(a)) throw std::runtime_error("fp8 tiled gemm: N % 128, K % 128, ldc % 8");
   if (!a.a || !a.w || !a.c) throw std::runtime_error("fp8 gemm: null operand");
   if (a.sa32) {
     if (!a.sw32) throw std::runtime_error("fp8 gemm: scales");
