@@ -57,6 +57,26 @@ __global__ void moe_count_kernel(const int32_t* __restrict__ sel, int n, int32_t
   if (hist) atomicAdd(&hist[sel[i]], 1u);
 }
 
+// The same counts for E <= 1024: a histogram of CNT_PER picks in LDS per workgroup, then one global add per nonzero
+// bin (integer sums: the result does not depend on the order). One global atomic per pick on a few hundred counters
+// serialises at the counters.
+constexpr int CNT_NT = 1024, CNT_PER = 4 * CNT_NT;
+__global__ __launch_bounds__(CNT_NT) void moe_count_lds_kernel(const int32_t* __restrict__ sel, int n, int E,
+                                                               int32_t* count, uint32_t* hist) {
+  __shared__ int bins[1024];
+  for (int e = threadIdx.x; e < E; e += CNT_NT) bins[e] = 0;
+  __syncthreads();
+  const int i0 = blockIdx.x * CNT_PER, i1 = min(n, i0 + CNT_PER);
+  for (int i = i0 + threadIdx.x; i < i1; i += CNT_NT) atomicAdd(&bins[sel[i]], 1);
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += CNT_NT) {
+    const int c = bins[e];
+    if (!c) continue;
+    atomicAdd(&count[e], c);
+    if (hist) atomicAdd(&hist[e], uint32_t(c));
+  }
+}
+
 // Offsets and tiles for E <= 1024 experts: resident experts first, then the others, each in ascending id
 // (ref moe_dispatch.hip:39-79 semantics; scans here are wave shuffles plus one LDS pass).
 constexpr int PLAN_NT = 1024;
@@ -95,8 +115,9 @@ __global__ __launch_bounds__(PLAN_NT) void moe_plan_kernel(int32_t* count, const
 
 // Block e: the tokens that picked e, in token order, get rows off[e], off[e] + 1, ...; each gets pidx at its
 // position among its own picks sorted by expert id (the number of its picks below e; equal picks stay in
-// selection order).
-constexpr int SC_NT = 256;
+// selection order). A thread per token, SC_NT tokens per pass (one block scan); the next pass's picks are loaded
+// before this pass's scan, so their latency overlaps it.
+constexpr int SC_NT = 1024;
 __global__ __launch_bounds__(SC_NT) void moe_scatter_kernel(const int32_t* __restrict__ sel, const float* __restrict__ wt,
                                                             int T, int K, const int32_t* __restrict__ off,
                                                             int32_t* eidx, float* ewt, int32_t* row_expert,
@@ -104,22 +125,29 @@ __global__ __launch_bounds__(SC_NT) void moe_scatter_kernel(const int32_t* __res
   __shared__ int lds[SC_NT / 64 + 1];
   const int e = blockIdx.x;
   int run = 0, base_row = -1;
+  int cur[kMaxK], nxt[kMaxK];
+  const auto load = [&](int t, int (&v)[kMaxK]) {
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) v[j] = (t < T && j < K) ? sel[size_t(t) * K + j] : -1;
+  };
+  load(threadIdx.x, cur);
   for (int t0 = 0; t0 < T; t0 += SC_NT) {
     const int t = t0 + threadIdx.x;
+    load(t + SC_NT, nxt);
     int c = 0, below = 0;
-    if (t < T)
-      for (int j = 0; j < K; ++j) {
-        const int v = sel[size_t(t) * K + j];
-        c += v == e;
-        below += v < e;
-      }
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) {
+      c += cur[j] == e;
+      below += cur[j] >= 0 && cur[j] < e;
+    }
     int tot;
     const int pre = block_exclusive_scan<SC_NT>(c, &tot, lds);
     if (c) {
       if (base_row < 0) base_row = off[e];
       int d = 0;
-      for (int j = 0; j < K; ++j)
-        if (sel[size_t(t) * K + j] == e) {
+#pragma unroll
+      for (int j = 0; j < kMaxK; ++j)
+        if (cur[j] == e) {
           const int p = base_row + run + pre + d;
           eidx[p] = t;
           ewt[p] = wt ? wt[size_t(t) * K + j] : 1.0f;
@@ -129,6 +157,8 @@ __global__ __launch_bounds__(SC_NT) void moe_scatter_kernel(const int32_t* __res
         }
     }
     run += tot;
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) cur[j] = nxt[j];
   }
 }
 
@@ -468,10 +498,11 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const bf16* __restrict
 }  // namespace
 
 // ---- entry points ---------------------------------------------------------------------------------------------------
-void moe_count(const int32_t* sel, int T, int K, int32_t* count, int, hipStream_t st, uint32_t* hist) {
+void moe_count(const int32_t* sel, int T, int K, int32_t* count, int E, hipStream_t st, uint32_t* hist) {
   const int n = T * K;
   if (n <= 0) return;
-  moe_count_kernel<<<cdiv(size_t(n), 256), 256, 0, st>>>(sel, n, count, hist);
+  if (E > 0 && E <= 1024) moe_count_lds_kernel<<<cdiv(size_t(n), CNT_PER), CNT_NT, 0, st>>>(sel, n, E, count, hist);
+  else moe_count_kernel<<<cdiv(size_t(n), 256), 256, 0, st>>>(sel, n, count, hist);
   UH_CHECK_LAUNCH();
 }
 
