@@ -63,6 +63,9 @@ int uh_mx_xform_in_fp8(const uint16_t* x, int ldx, const int32_t* row_expert, co
 /* mx_moe.hpp:41-42 */
 int uh_mx_swiglu(const uint16_t* g, const uint16_t* u, const float* w, const int32_t* row_expert,
                  const uint8_t* const* s_tab, uint16_t* hh, int P, int I, float limit, void* stream);
+/* No reference counterpart: exhaustive check of the hardware e4m3 encode (v_cvt_pk_fp8_f32) against the
+ * software round-to-nearest-even encode on every fp32 value in [-448, 448]; *bad = mismatching codes. */
+int uh_check_fp8_encode(unsigned long long* bad, unsigned long long* total);
 /* mx_moe.hpp:61: exhaustive MFMA block-scaled decode check; *bad = mismatches among normal results. */
 int uh_mx_check_dequant(unsigned long long* bad, unsigned long long* total);
 

@@ -30,6 +30,17 @@ def test_check_dequant_exhaustive():
     assert bad.value == 0
 
 
+def test_check_fp8_encode_exhaustive():
+    """The hardware e4m3 encode used by the quantizers equals the software round-to-nearest-even encode (itself
+    pinned against brute force in the oracle tests) on every fp32 value the encoders feed it."""
+    bad = ctypes.c_ulonglong(0)
+    total = ctypes.c_ulonglong(0)
+    call("uh_check_fp8_encode", ctypes.byref(bad), ctypes.byref(total))
+    print(f"e4m3 encode check: {bad.value} mismatches of {total.value}")
+    assert total.value == 2 * (0x43E00000 + 1)
+    assert bad.value == 0
+
+
 @pytest.mark.parametrize("N,K", [(16, 64), (64, 256), (2048, 4096)])
 def test_repack_matches_oracle(N, K):
     rng = np.random.default_rng(1)

@@ -236,6 +236,10 @@ int uh_mx_swiglu(const uint16_t* g, const uint16_t* u, const float* w, const int
                  const uint8_t* const* s_tab, uint16_t* hh, int P, int I, float limit, void* st) {
   return guard([&] { k::mx_swiglu(g, u, w, row_expert, s_tab, hh, P, I, limit, S(st)); });
 }
+int uh_check_fp8_encode(unsigned long long* bad, unsigned long long* total) {
+  return guard([&] { *bad = k::fp8_check_encode(total); });
+}
+
 int uh_mx_check_dequant(unsigned long long* bad, unsigned long long* total) {
   return guard([&] { *bad = k::mx_check_dequant(total); });
 }

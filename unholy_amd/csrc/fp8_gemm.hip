@@ -83,24 +83,16 @@ __global__ __launch_bounds__(256) void act_quant8_kernel(const bf16* __restrict_
     for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
     am = row16_max(am);
     if (base + threadIdx.x >= items) continue;
-    uint32_t c[2] = {0, 0};
+    uint32_t c[2];
     if constexpr (MODE == 2) {
       const float sc = fmaxf(am, 1e-4f) * (1.0f / 448.0f);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) c[i / 4] |= uint32_t(fp8_code(v[i], sc)) << (8 * (i % 4));
+      fp8_codes8(v, sc, c[0], c[1]);
       if (l == 0) static_cast<float*>(s)[size_t(r) * nb + b] = sc;
     } else {
       const Fp8Block blk = fp8_block_scale(am);
-      uint32_t h[4];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint8_t code = fp8_code(v[i], blk);
-        c[i / 4] |= uint32_t(code) << (8 * (i % 4));
-        const uint32_t f = f32_to_bf16(e4m3_to_f32(code) * blk.sc);
-        h[i / 2] = (i % 2) ? (h[i / 2] | f << 16) : f;
-      }
-      if constexpr (MODE == 1) {
-        *reinterpret_cast<uint4*>(xr) = make_uint4(h[0], h[1], h[2], h[3]);
+      fp8_codes8(v, blk, c[0], c[1]);
+      if constexpr (MODE == 1) {  // the fake-quantized values: the codes decoded back (exact)
+        *reinterpret_cast<uint4*>(xr) = __builtin_bit_cast(uint4, fp8x8_to_bf16(c[0], c[1], blk.sc));
         continue;
       }
       if (l == 0) static_cast<uint8_t*>(s)[size_t(r) * nb + b] = blk.se;

@@ -543,20 +543,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
         if (a.out[1]) *reinterpret_cast<uint4*>(a.out[1] + oc) = uv4;
         if (a.gs_tab && !a.gs_tab[a.grow_expert[row]]) continue;
         const Fp8Block blk = fp8_block_scale(am);
-        uint32_t qb[2] = {0, 0};
-#pragma unroll
-        for (int q = 0; q < 8; ++q) qb[q / 4] |= uint32_t(fp8_code(hv[q], blk)) << (8 * (q % 4));
+        uint32_t qb[2];
+        fp8_codes8(hv, blk, qb[0], qb[1]);
         const size_t o = row * N + size_t(bx) * 128 + c8;
         if (a.hq) *reinterpret_cast<uint2*>(a.hq + o) = make_uint2(qb[0], qb[1]);
-        if (a.hh) {
-          uint32_t fq[4];
-#pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            const uint32_t f = f32_to_bf16(e4m3_to_f32(uint8_t(qb[q / 4] >> (8 * (q % 4)))) * blk.sc);
-            fq[q / 2] = (q % 2) ? (fq[q / 2] | f << 16) : f;
-          }
-          *reinterpret_cast<uint4*>(a.hh + o) = make_uint4(fq[0], fq[1], fq[2], fq[3]);
-        }
+        if (a.hh)  // the fake-quantized rows (the codes decoded back, exact), only when asked for
+          *reinterpret_cast<uint4*>(a.hh + o) = __builtin_bit_cast(uint4, fp8x8_to_bf16(qb[0], qb[1], blk.sc));
         if (a.hs && c8 == 0) a.hs[row * (N / 128) + bx] = blk.se;
       }
     }

@@ -38,6 +38,9 @@ struct MxGemvArgs {
 
 // amode: 0 e4m3 codes + scales, 1 fake-quantized bf16 rows, 2 raw bf16 token rows (act_quant in the kernel).
 void launch_mx_gemv(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st);
+// Exhaustive check of the hardware e4m3 encode against the software one on [-448, 448]; returns the mismatches
+// (*total: values compared).
+unsigned long long fp8_check_encode(unsigned long long* total);
 // Zeroes n int32 words (a kernel, so that a captured graph records no memset node).
 void launch_zero_words(int32_t* p, size_t n, hipStream_t st);
 void launch_mx_gemm(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st);

@@ -117,15 +117,10 @@ __global__ __launch_bounds__(256) void mx_transform8_kernel(const bf16* __restri
     for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
     const Fp8Block b = fp8_block_scale(row16_max(am));
     if (base + threadIdx.x >= items || (s_tab && !s_tab[row_expert[r]])) continue;
-    uint32_t c[2] = {0, 0}, h[4];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint8_t code = fp8_code(v[i], b);
-      c[i / 4] |= uint32_t(code) << (8 * (i % 4));
-      const uint32_t f = f32_to_bf16(e4m3_to_f32(code) * b.sc);
-      h[i / 2] = (i % 2) ? (h[i / 2] | f << 16) : f;
-    }
-    if (out) *reinterpret_cast<uint4*>(out + size_t(r) * K + k0) = make_uint4(h[0], h[1], h[2], h[3]);
+    uint32_t c[2];
+    fp8_codes8(v, b, c[0], c[1]);
+    if (out)  // the fake-quantized values: the codes decoded back (exact)
+      *reinterpret_cast<uint4*>(out + size_t(r) * K + k0) = __builtin_bit_cast(uint4, fp8x8_to_bf16(c[0], c[1], b.sc));
     if (q) {
       *reinterpret_cast<uint2*>(q + size_t(r) * K + k0) = make_uint2(c[0], c[1]);
       if ((rem & 15) == 0) qs[size_t(r) * segs + seg] = b.se;
@@ -237,23 +232,16 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         am = group_max<16>(am);
         if (valid) {
           uint8_t se;
-          uint32_t lo = 0, hi = 0;
+          uint32_t lo, hi;
           if constexpr (AM == 1) {
             se = uint8_t(min(max(int(exact_fp8_scale(am)), 1), 254));
             const float inv = e8m0_to_f32(uint8_t(254 - se));  // 2^(127 - se), exact
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              lo |= uint32_t(f32_to_e4m3(v[t] * inv)) << (8 * t);
-              hi |= uint32_t(f32_to_e4m3(v[t + 4] * inv)) << (8 * t);
-            }
+            lo = e4m3x4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);  // exact values: |v * inv| <= 448
+            hi = e4m3x4(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
           } else {
             const Fp8Block blk = fp8_block_scale(am);
             se = blk.se;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              lo |= uint32_t(fp8_code(v[t], blk)) << (8 * t);
-              hi |= uint32_t(fp8_code(v[t + 4], blk)) << (8 * t);
-            }
+            fp8_codes8(v, blk, lo, hi);
           }
           *reinterpret_cast<uint2*>(sA + m * ldA + c) = make_uint2(lo, hi);
           if ((c & 127) == 0) sS[m * KS + c / 128] = se;
@@ -419,6 +407,21 @@ __device__ __forceinline__ void put_a8(v8i& a, int g, int k, int code) {
   const int byte = (k / 64) * 16 + k % 16;
   a[byte / 4] |= code << (8 * (byte % 4));
 }
+// Exhaustive check of the hardware e4m3 encode (v_cvt_pk_fp8_f32: round to nearest even, OCP e4m3fn on gfx950)
+// against f32_to_e4m3 on every fp32 value in [-448, 448] (both signs in one conversion), the domain every encoder
+// here feeds it after clamping. cnt[0] += mismatching codes.
+constexpr uint32_t kE4m3MaxBits = 0x43E00000u;  // 448.0f
+__global__ __launch_bounds__(256) void fp8_check_encode_kernel(unsigned long long* cnt) {
+  unsigned long long bad = 0;
+  for (uint32_t u = blockIdx.x * 256u + threadIdx.x; u <= kE4m3MaxBits; u += gridDim.x * 256u) {
+    const float x = __uint_as_float(u);
+    const uint32_t hw = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(x, -x, 0, false));
+    bad += (hw & 0xffu) != f32_to_e4m3(x);
+    bad += ((hw >> 8) & 0xffu) != f32_to_e4m3(-x);
+  }
+  if (bad) atomicAdd(&cnt[0], bad);
+}
+
 __global__ __launch_bounds__(64) void mx_check_dequant_kernel(unsigned long long* cnt) {
   const int sv = blockIdx.x, lane = threadIdx.x, nl = lane & 15, g = lane >> 4;
   {  // weight side
@@ -609,6 +612,19 @@ bool mx_gemm_glu() {
   return g_glu < 0 ? env : g_glu > 0;
 }
 void mx_gemm_force_glu(int on) { g_glu = on; }
+
+unsigned long long fp8_check_encode(unsigned long long* total) {
+  unsigned long long* cnt = nullptr;
+  UH_CHECK(hipMalloc(&cnt, sizeof(unsigned long long)));
+  UH_CHECK(hipMemset(cnt, 0, sizeof(unsigned long long)));
+  fp8_check_encode_kernel<<<2048, 256>>>(cnt);
+  UH_CHECK_LAUNCH();
+  unsigned long long bad = 0;
+  UH_CHECK(hipMemcpy(&bad, cnt, sizeof(bad), hipMemcpyDeviceToHost));
+  UH_CHECK(hipFree(cnt));
+  if (total) *total = 2ull * (kE4m3MaxBits + 1ull);
+  return bad;
+}
 
 unsigned long long mx_check_dequant(unsigned long long* total) {
   unsigned long long* cnt = nullptr;

@@ -132,12 +132,28 @@ __device__ __forceinline__ Fp8Block fp8_block_scale(float amax) {
   const uint8_t se = pow2_ceil_e8m0(fmaxf(amax, 1e-4f) * (1.0f / 448.0f));
   return {se, e8m0_to_f32(se), __uint_as_float(uint32_t(254 - se) << 23)};
 }
-// Any positive fp32 scale (the fp32-scale activation format): a true division.
-__device__ __forceinline__ uint8_t fp8_code(float v, float sc) {
-  return f32_to_e4m3(fminf(fmaxf(v / sc, -448.0f), 448.0f));
+// e4m3 codes (round to nearest even) of values already in [-448, 448] with the hardware encode v_cvt_pk_fp8_f32:
+// on that range it gives exactly the codes of f32_to_e4m3 (fp8_check_encode compares every fp32 value of it).
+// Byte i of e4m3x4 is value i.
+__device__ __forceinline__ uint8_t e4m3_hw(float x) {
+  return uint8_t(__builtin_amdgcn_cvt_pk_fp8_f32(x, 0.0f, 0, false));
 }
-__device__ __forceinline__ uint8_t fp8_code(float v, const Fp8Block& b) {
-  return f32_to_e4m3(fminf(fmaxf(v * b.inv, -448.0f), 448.0f));
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true));
+}
+__device__ __forceinline__ float clamp448(float v) { return fminf(fmaxf(v, -448.0f), 448.0f); }
+// Any positive fp32 scale (the fp32-scale activation format): a true division.
+__device__ __forceinline__ uint8_t fp8_code(float v, float sc) { return e4m3_hw(clamp448(v / sc)); }
+__device__ __forceinline__ uint8_t fp8_code(float v, const Fp8Block& b) { return e4m3_hw(clamp448(v * b.inv)); }
+// The codes of 8 values of one block, lowest byte first.
+__device__ __forceinline__ void fp8_codes8(const float (&v)[8], const Fp8Block& b, uint32_t& lo, uint32_t& hi) {
+  lo = e4m3x4(clamp448(v[0] * b.inv), clamp448(v[1] * b.inv), clamp448(v[2] * b.inv), clamp448(v[3] * b.inv));
+  hi = e4m3x4(clamp448(v[4] * b.inv), clamp448(v[5] * b.inv), clamp448(v[6] * b.inv), clamp448(v[7] * b.inv));
+}
+__device__ __forceinline__ void fp8_codes8(const float (&v)[8], float sc, uint32_t& lo, uint32_t& hi) {
+  lo = e4m3x4(clamp448(v[0] / sc), clamp448(v[1] / sc), clamp448(v[2] / sc), clamp448(v[3] / sc));
+  hi = e4m3x4(clamp448(v[4] / sc), clamp448(v[5] / sc), clamp448(v[6] / sc), clamp448(v[7] / sc));
 }
 
 // SwiGLU with the clamp and optional routing weight (ref_moe.hip:66-72): x = silu(min(g, l)) * clamp(u, +-l),
