@@ -41,6 +41,16 @@ def test_check_fp8_encode_exhaustive():
     assert bad.value == 0
 
 
+def test_check_bf16_encode_exhaustive():
+    """The hardware bf16 rounding the kernels use for fp32 -> bf16 equals the software round-to-nearest-even (the
+    reference's rounding) at every non-NaN fp32 input; NaN inputs stay NaN (payloads may differ)."""
+    bad = ctypes.c_ulonglong(0)
+    nan_bad = ctypes.c_ulonglong(0)
+    call("uh_check_bf16_encode", ctypes.byref(bad), ctypes.byref(nan_bad))
+    print(f"bf16 rounding check: {bad.value} mismatches at non-NaN inputs, {nan_bad.value} at NaN inputs")
+    assert bad.value == 0
+
+
 @pytest.mark.parametrize("N,K", [(16, 64), (64, 256), (2048, 4096)])
 def test_repack_matches_oracle(N, K):
     rng = np.random.default_rng(1)

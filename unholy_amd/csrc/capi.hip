@@ -240,6 +240,10 @@ int uh_check_fp8_encode(unsigned long long* bad, unsigned long long* total) {
   return guard([&] { *bad = k::fp8_check_encode(total); });
 }
 
+int uh_check_bf16_encode(unsigned long long* bad, unsigned long long* nan_bad) {
+  return guard([&] { *bad = k::bf16_check_encode(nan_bad); });
+}
+
 int uh_mx_check_dequant(unsigned long long* bad, unsigned long long* total) {
   return guard([&] { *bad = k::mx_check_dequant(total); });
 }

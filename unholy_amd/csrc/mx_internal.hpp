@@ -41,6 +41,9 @@ void launch_mx_gemv(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st);
 // Exhaustive check of the hardware e4m3 encode against the software one on [-448, 448]; returns the mismatches
 // (*total: values compared).
 unsigned long long fp8_check_encode(unsigned long long* total);
+// Exhaustive check of the hardware bf16 rounding against f32_to_bf16 over all fp32 bit patterns; returns the
+// mismatches at non-NaN inputs (*nan_bad: at NaN inputs).
+unsigned long long bf16_check_encode(unsigned long long* nan_bad);
 // Zeroes n int32 words (a kernel, so that a captured graph records no memset node).
 void launch_zero_words(int32_t* p, size_t n, hipStream_t st);
 void launch_mx_gemm(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st);

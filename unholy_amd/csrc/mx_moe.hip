@@ -422,6 +422,24 @@ __global__ __launch_bounds__(256) void fp8_check_encode_kernel(unsigned long lon
   if (bad) atomicAdd(&cnt[0], bad);
 }
 
+// Exhaustive check of the hardware bf16 rounding (v_cvt_pk_bf16_f32, what a float -> __bf16 conversion compiles to)
+// against f32_to_bf16_sw on every fp32 bit pattern: cnt[0] += mismatches at non-NaN inputs, cnt[1] += at NaN inputs.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__global__ __launch_bounds__(256) void bf16_check_encode_kernel(unsigned long long* cnt) {
+  unsigned long long bad = 0, bad_nan = 0;
+  for (uint64_t u = blockIdx.x * 256ull + threadIdx.x; u < (1ull << 31); u += gridDim.x * 256ull) {
+    const float x = __uint_as_float(uint32_t(u)), y = __uint_as_float(uint32_t(u) | 0x80000000u);
+    const bf16x2_t v = {__bf16(x), __bf16(y)};
+    const uint32_t hw = __builtin_bit_cast(uint32_t, v);
+    const bool nan = (uint32_t(u) & 0x7fffffffu) > 0x7f800000u;
+    const unsigned m = ((hw & 0xffffu) != f32_to_bf16_sw(x)) + ((hw >> 16) != f32_to_bf16_sw(y));
+    if (nan) bad_nan += m;
+    else bad += m;
+  }
+  if (bad) atomicAdd(&cnt[0], bad);
+  if (bad_nan) atomicAdd(&cnt[1], bad_nan);
+}
+
 __global__ __launch_bounds__(64) void mx_check_dequant_kernel(unsigned long long* cnt) {
   const int sv = blockIdx.x, lane = threadIdx.x, nl = lane & 15, g = lane >> 4;
   {  // weight side
@@ -624,6 +642,19 @@ unsigned long long fp8_check_encode(unsigned long long* total) {
   UH_CHECK(hipFree(cnt));
   if (total) *total = 2ull * (kE4m3MaxBits + 1ull);
   return bad;
+}
+
+unsigned long long bf16_check_encode(unsigned long long* nan_bad) {
+  unsigned long long* cnt = nullptr;
+  UH_CHECK(hipMalloc(&cnt, 2 * sizeof(unsigned long long)));
+  UH_CHECK(hipMemset(cnt, 0, 2 * sizeof(unsigned long long)));
+  bf16_check_encode_kernel<<<4096, 256>>>(cnt);
+  UH_CHECK_LAUNCH();
+  unsigned long long h[2] = {};
+  UH_CHECK(hipMemcpy(h, cnt, sizeof(h), hipMemcpyDeviceToHost));
+  UH_CHECK(hipFree(cnt));
+  if (nan_bad) *nan_bad = h[1];
+  return h[0];
 }
 
 unsigned long long mx_check_dequant(unsigned long long* total) {

@@ -15,13 +15,17 @@ using bf16 = uint16_t;
 
 __device__ __forceinline__ float bf16_to_f32(bf16 v) { return __uint_as_float(uint32_t(v) << 16); }
 
-// Round to nearest even; NaN stays a quiet NaN (dev.hip.hpp:43-48).
-__device__ __forceinline__ bf16 f32_to_bf16(float f) {
+// Round to nearest even; NaN stays a quiet NaN (dev.hip.hpp:43-48), written out: the reference for the check of the
+// hardware conversion below.
+__device__ __forceinline__ bf16 f32_to_bf16_sw(float f) {
   uint32_t u = __float_as_uint(f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return bf16((u >> 16) | 0x40);
   u += 0x7fffu + ((u >> 16) & 1u);
   return bf16(u >> 16);
 }
+// The same rounding in one instruction (v_cvt_pk_bf16_f32): identical to f32_to_bf16_sw on all 2^32 inputs, NaNs
+// included (bf16_check_encode compares every one).
+__device__ __forceinline__ bf16 f32_to_bf16(float f) { return __builtin_bit_cast(bf16, __bf16(f)); }
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
 // OCP e4m3fn decode (dev.hip.hpp:59-63).
