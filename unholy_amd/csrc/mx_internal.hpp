@@ -34,6 +34,9 @@ struct MxGemvArgs {
   uint8_t* hs;
   uint16_t* hraw;  // SwiGLU rows as bf16, not requantized (MxGlu::h)
   float limit;
+  // > 0: one matrix, two column streams per wave: projection 1 is projection 0's matrix from 16-column tile `split`
+  // on (codes, scales and outputs offset by split tiles); the grid covers split tiles.
+  int split;
 };
 
 // amode: 0 e4m3 codes + scales, 1 fake-quantized bf16 rows, 2 raw bf16 token rows (act_quant in the kernel).

@@ -159,8 +159,13 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
   wp[0] = a.w_tab[0][tile.expert];
   sp[0] = a.s_tab[0][tile.expert];
   if constexpr (NP == 2) {
-    wp[1] = a.w_tab[1][tile.expert];
-    sp[1] = a.s_tab[1][tile.expert];
+    if (a.split) {  // the same matrix from column tile `split` on
+      wp[1] = wp[0] ? wp[0] + size_t(a.split) * 512 : nullptr;
+      sp[1] = sp[0] ? sp[0] + size_t(a.split) * 32 : nullptr;
+    } else {
+      wp[1] = a.w_tab[1][tile.expert];
+      sp[1] = a.s_tab[1][tile.expert];
+    }
   }
 #pragma unroll
   for (int p = 0; p < NP; ++p)
@@ -170,7 +175,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
   uint8_t* sS = smem + size_t(a.rows_cap) * ldA;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nl = lane & 15, g = lane >> 4;
   const int nt = blockIdx.x * W + wave;
-  const bool active = nt < ntn;  // uniform per wave
+  const bool active = nt < (a.split ? a.split : ntn);  // uniform per wave
   const int boff = nl * 32 + (g & 1) * 16;
   for (int rg = 0; rg < tile.rows; rg += a.rows_cap) {
     const int M = min(a.rows_cap, tile.rows - rg);
@@ -502,7 +507,7 @@ void launch_gemv_w(const MxGemvArgs& a, int ntiles, hipStream_t st) {
   const size_t lds = size_t(a.rows_cap) * (a.K + GV_PAD) + size_t(a.rows_cap) * (a.K / 128);
   auto* kern = &mx_gemv_kernel<NP, GM, AM, W>;
   set_lds_limit(kern, lds);
-  const dim3 grid(cdiv(size_t(a.N) / 16, W), unsigned(ntiles), 1);
+  const dim3 grid(cdiv(a.split ? size_t(a.split) : size_t(a.N) / 16, W), unsigned(ntiles), 1);
   kern<<<grid, 64 * W, lds, st>>>(a);
   UH_CHECK_LAUNCH();
 }
@@ -514,6 +519,14 @@ void launch_gemv_t(const MxGemvArgs& a, int ntiles, hipStream_t st) {
 }  // namespace
 
 // ---- internal launchers (mx_internal.hpp) -----------------------------------------------------------------------------
+static bool gemv_split_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("UH_GEMV_SPLIT");
+    return !v || std::string(v) != "0";
+  }();
+  return on;
+}
+
 void launch_mx_gemv(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st) {
   if (ntiles <= 0) return;
   if (a.K % 128 || a.N % 16 || a.K <= 0 || a.N <= 0) throw std::runtime_error("mx_grouped_gemv: K % 128 or N % 16");
@@ -535,7 +548,17 @@ void launch_mx_gemv(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st) 
   if (glu) UH_GV(2, 1);
   else if (graw) UH_GV(2, 2);
   else if (np2) UH_GV(2, 0);
-  else UH_GV(1, 0);
+  else if (!a.out32 && a.N % 32 == 0 && gemv_split_enabled()) {
+    // One matrix as two column streams per wave: twice the weight bytes behind each workgroup's start-up (the
+    // staging of its rows and the first loads), half the workgroups.
+    MxGemvArgs b = a;
+    b.split = a.N / 32;
+    b.w_tab[1] = a.w_tab[0];
+    b.s_tab[1] = a.s_tab[0];
+    b.out[1] = a.out[0] + a.N / 2;
+    const MxGemvArgs& a = b;
+    UH_GV(2, 0);
+  } else UH_GV(1, 0);
 #undef UH_GV
 }
 
