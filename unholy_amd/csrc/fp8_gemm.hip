@@ -277,38 +277,52 @@ __global__ __launch_bounds__(64 * FV_WAVES) void fp8_gemv_kernel(Fp8GemmArgs a, 
   v4f acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  const int mlive = (M + 15) / 16;  // row tiles with rows (uniform)
   for (int kc = b0; kc < b1; kc += FV_CHUNK) {
-    v4i b[FV_CHUNK][2];
+    // Every load of the chunk is issued before the first use, unconditionally (steps past the range and rows past M
+    // are clamped, their products discarded): the weights, the activation rows and the scales, so the chunk waits
+    // for one memory latency, not one per step.
+    v4i b[FV_CHUNK][2], aq[FV_CHUNK][MT][2];
+    float swv[FV_CHUNK], sav[FV_CHUNK][MT];
+    constexpr bool kRowScales = F32S && MT == 1;  // the fp32 row scales of C's rows too (registers permitting)
+    float sa32v[FV_CHUNK][4];
 #pragma unroll
-    for (int u = 0; u < FV_CHUNK; ++u) {  // unconditional (clamped) loads: all in flight before the first use
+    for (int u = 0; u < FV_CHUNK; ++u) {
       const int kb = min(kc + u, b1 - 1);
       b[u][0] = *reinterpret_cast<gptr<v4i>>(as_global(wrow + kb * 128));
       b[u][1] = *reinterpret_cast<gptr<v4i>>(as_global(wrow + kb * 128 + 16));
+      swv[u] = F32S ? a.sw32[size_t(nb) * KS + kb] : e8m0_to_f32(a.sw8[size_t(nb) * KS + kb]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int r = min(mt * 16 + nl, M - 1);
+        const uint8_t* ap = a.a + size_t(r) * K + kb * 128 + g * 32;
+        aq[u][mt][0] = *reinterpret_cast<gptr<v4i>>(as_global(ap));
+        aq[u][mt][1] = *reinterpret_cast<gptr<v4i>>(as_global(ap + 16));
+        sav[u][mt] = F32S ? 1.0f : e8m0_to_f32(a.sa8[size_t(r) * KS + kb]);
+      }
+      if constexpr (kRowScales)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sa32v[u][i] = a.sa32[size_t(min(4 * g + i, M - 1)) * KS + kb];
     }
 #pragma unroll
     for (int u = 0; u < FV_CHUNK; ++u) {
       const int kb = kc + u;
       if (kb >= b1) break;
-      const float swv = F32S ? a.sw32[size_t(nb) * KS + kb] : e8m0_to_f32(a.sw8[size_t(nb) * KS + kb]);
       bf16x8 bf[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t)
         bf[t] = fp8x8_to_bf16(uint32_t(b[u][t / 2][2 * (t % 2)]), uint32_t(b[u][t / 2][2 * (t % 2) + 1]),
-                              F32S ? 1.0f : swv);
+                              F32S ? 1.0f : swv[u]);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        if (mt * 16 >= M) break;
-        const int r = mt * 16 + nl;
+        if (mt >= mlive) break;
         bf16x8 af[4];
-        if (r < M) {
-          const uint8_t* ap = a.a + size_t(r) * K + kb * 128 + g * 32;
-          const v4i lo = *reinterpret_cast<gptr<v4i>>(as_global(ap));
-          const v4i hi = *reinterpret_cast<gptr<v4i>>(as_global(ap + 16));
-          const float sc = F32S ? 1.0f : e8m0_to_f32(a.sa8[size_t(r) * KS + kb]);
-          af[0] = fp8x8_to_bf16(lo[0], lo[1], sc);
-          af[1] = fp8x8_to_bf16(lo[2], lo[3], sc);
-          af[2] = fp8x8_to_bf16(hi[0], hi[1], sc);
-          af[3] = fp8x8_to_bf16(hi[2], hi[3], sc);
+        if (mt * 16 + nl < M) {
+          const v4i lo = aq[u][mt][0], hi = aq[u][mt][1];
+          af[0] = fp8x8_to_bf16(lo[0], lo[1], sav[u][mt]);
+          af[1] = fp8x8_to_bf16(lo[2], lo[3], sav[u][mt]);
+          af[2] = fp8x8_to_bf16(hi[0], hi[1], sav[u][mt]);
+          af[3] = fp8x8_to_bf16(hi[2], hi[3], sav[u][mt]);
         } else {
 #pragma unroll
           for (int t = 0; t < 4; ++t) af[t] = bf16x8{};
@@ -320,8 +334,8 @@ __global__ __launch_bounds__(64 * FV_WAVES) void fp8_gemv_kernel(Fp8GemmArgs a, 
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int rr = mt * 16 + 4 * g + i;  // C row of value i
-            const float sav = rr < M ? a.sa32[size_t(rr) * KS + kb] : 0.0f;
-            acc[mt][i] += raw[i] * (sav * swv);
+            const float sa = rr >= M ? 0.0f : kRowScales ? sa32v[u][i] : a.sa32[size_t(rr) * KS + kb];
+            acc[mt][i] += raw[i] * (sa * swv[u]);
           }
         } else {
 #pragma unroll
