@@ -349,7 +349,7 @@ __global__ __launch_bounds__(SMALL_NT) void moe_dispatch_small_kernel(MoeSmallAr
   __shared__ __align__(16) int skey[SMALL_NT];
   __shared__ float swt[SMALL_NT];
   __shared__ int lds[SMALL_NT / 64 + 1];
-  const int T = a.T, K = a.K, E = a.E, n = T * K, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int T = a.T, K = a.K, E = a.E, n = T * K, tid = threadIdx.x, wave = tid >> 6;
   const bool route = a.route_logits || a.ds_logits || a.softmax_logits;
   if (route) {
     const int mode = a.softmax_logits ? 2 : a.route_logits ? 1 : 0;

@@ -405,19 +405,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
       if (lane < 16) dma16(sb, uint32_t(lane) * 16, st + uint32_t(GP_A + GP_B + (sc_q * 2 + sc_j) * 256));
     };
     const int rb_live = __builtin_amdgcn_readfirstlane((M + 31) / 32);
-    v16f_t acc[4][2];
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = v16f_t{};
     issue(0);
     {  // activation scales, after stage 0 is in flight (every thread keeps one row: 256 % 128 == 0)
       const int r = min(tid & 127, M - 1);
       const uint8_t* srow = a.as + size_t(a.x_rows ? a.x_rows[row0 + r] : int(row0 + r)) * KS;
       for (int e = tid; e < 128 * KS; e += 256) as_lds[e] = srow[e >> 7];
     }
-    const auto kloop = [&](auto nrb) {
+    // The K loop and the epilogue, specialised on the tile's live 32-row blocks (RB): each stage is one basic block
+    // the compiler can interleave, and only live accumulators exist (dead ones kept alive across the loop cost
+    // register copies in every stage).
+    const auto tile_body = [&](auto nrb) {
       constexpr int RB = decltype(nrb)::value;
+      v16f_t acc[RB][2];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = v16f_t{};
       for (int s = 0; s < KS; ++s) {
         wait_vm<0>();     // this wave's part of stage s (the only stage in flight)
         __syncthreads();  // every wave's part has landed; the other slot (stage s - 1) is free
@@ -459,99 +462,102 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
           }
         }
       }
-    };
-    if (rb_live == 4) kloop(std::integral_constant<int, 4>{});
-    else if (rb_live == 3) kloop(std::integral_constant<int, 3>{});
-    else if (rb_live == 2) kloop(std::integral_constant<int, 2>{});
-    else kloop(std::integral_constant<int, 1>{});
 
-    // ---- epilogue (the ring is free once every wave is past its last stage)
-    __syncthreads();
-    const auto row_of = [&](int rb, int i) { return rb * 32 + 8 * (i / 4) + 4 * h + (i % 4); };
-    if constexpr (NP == 1) {
-      const int c0 = cq * 64;
-      if (a.out32) {  // fp32 outputs (accuracy checks): two passes of 64 rows through the ring
-        constexpr int LDF = 256 + 4;
-        static_assert(64 * LDF * 4 <= GP_RING, "a 64-row fp32 half tile fits the ring");
-        float* sf = reinterpret_cast<float*>(smem);
+      // ---- epilogue (the ring is free once every wave is past its last stage)
+      __syncthreads();
+      const auto row_of = [&](int rb, int i) { return rb * 32 + 8 * (i / 4) + 4 * h + (i % 4); };
+      if constexpr (NP == 1) {
+        const int c0 = cq * 64;
+        if (a.out32) {  // fp32 outputs (accuracy checks): two passes of 64 rows through the ring
+          constexpr int LDF = 256 + 4;
+          static_assert(64 * LDF * 4 <= GP_RING, "a 64-row fp32 half tile fits the ring");
+          float* sf = reinterpret_cast<float*>(smem);
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          if (half) __syncthreads();  // the first half's stores have read the tile
+          for (int half = 0; half < 2; ++half) {
+            if (half) __syncthreads();  // the first half's stores have read the tile
 #pragma unroll
-          for (int k = 0; k < 2; ++k)
+            for (int k = 0; k < 2; ++k) {
+              constexpr int kNone = -1;
+              const int rb = 2 * half + k < RB ? 2 * half + k : kNone;  // compile-time after unrolling
+              if (rb == kNone) continue;
+#pragma unroll
+              for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) sf[(row_of(k, i)) * LDF + c0 + cb * 32 + l32] = acc[rb][cb][i];
+            }
+            __syncthreads();
+            for (int e = tid; e < min(64, M - 64 * half) * 64; e += 256) {
+              const int r = e / 64, c4 = (e % 64) * 4;
+              *reinterpret_cast<float4*>(a.out32 + (row0 + 64 * half + r) * a.ldo + bx * 256 + c4) =
+                  *reinterpret_cast<const float4*>(sf + r * LDF + c4);
+            }
+          }
+        } else {
+          uint16_t* sc = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
             for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-              for (int i = 0; i < 16; ++i)
-                sf[(row_of(k, i)) * LDF + c0 + cb * 32 + l32] = acc[2 * half + k][cb][i];
+              for (int i = 0; i < 16; ++i) sc[row_of(rb, i) * GP_LDC1 + c0 + cb * 32 + l32] = f32_to_bf16(acc[rb][cb][i]);
           __syncthreads();
-          for (int e = tid; e < min(64, M - 64 * half) * 64; e += 256) {
-            const int r = e / 64, c4 = (e % 64) * 4;
-            *reinterpret_cast<float4*>(a.out32 + (row0 + 64 * half + r) * a.ldo + bx * 256 + c4) =
-                *reinterpret_cast<const float4*>(sf + r * LDF + c4);
+          for (int e = tid; e < M * 32; e += 256) {
+            const int r = e / 32, c8 = (e % 32) * 8;
+            *reinterpret_cast<uint4*>(a.out[0] + (row0 + r) * a.ldo + bx * 256 + c8) =
+                *reinterpret_cast<const uint4*>(sc + r * GP_LDC1 + c8);
           }
         }
       } else {
-        uint16_t* sc = reinterpret_cast<uint16_t*>(smem);
+        // bf16 g (w1) and u (w3) tiles in LDS, then 8 consecutive outputs of one row per thread: h = bf16(SwiGLU(g, u)),
+        // the row's amax over its 128 outputs (16 threads: a DPP row max), fake quantization, 16-byte stores.
+        uint16_t* const tg = reinterpret_cast<uint16_t*>(smem);
+        uint16_t* const tu = tg + 128 * GP_LDC2;
+        uint16_t* const mine = q_own ? tu : tg;
+        const int chh = cq & 1;
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
+        for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
           for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) sc[row_of(rb, i) * GP_LDC1 + c0 + cb * 32 + l32] = f32_to_bf16(acc[rb][cb][i]);
+            for (int i = 0; i < 16; ++i)
+              mine[row_of(rb, i) * GP_LDC2 + chh * 64 + cb * 32 + l32] = f32_to_bf16(acc[rb][cb][i]);
         __syncthreads();
-        for (int e = tid; e < M * 32; e += 256) {
-          const int r = e / 32, c8 = (e % 32) * 8;
-          *reinterpret_cast<uint4*>(a.out[0] + (row0 + r) * a.ldo + bx * 256 + c8) =
-              *reinterpret_cast<const uint4*>(sc + r * GP_LDC1 + c8);
+        for (int e0 = 0; e0 < M * 16; e0 += 256) {  // uniform bound: every 16-lane group is whole
+          const int e = e0 + tid, r = min(e / 16, M - 1), c8 = (e % 16) * 8;
+          const size_t row = row0 + r;
+          const uint4 gv4 = *reinterpret_cast<const uint4*>(tg + r * GP_LDC2 + c8);
+          const uint4 uv4 = *reinterpret_cast<const uint4*>(tu + r * GP_LDC2 + c8);
+          const uint32_t gw4[4] = {gv4.x, gv4.y, gv4.z, gv4.w}, uw4[4] = {uv4.x, uv4.y, uv4.z, uv4.w};
+          const float w = a.gw ? a.gw[row] : 0.0f;
+          float hv[8], am = 0.0f;
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            hv[q] = round_bf16(swiglu_value(bf16_to_f32(uint16_t(gw4[q / 2] >> (16 * (q % 2)))),
+                                            bf16_to_f32(uint16_t(uw4[q / 2] >> (16 * (q % 2)))), w, a.gw != nullptr,
+                                            a.limit));
+            am = fmaxf(am, fabsf(hv[q]));
+          }
+          am = row16_max(am);
+          if (e >= M * 16) continue;
+          const size_t oc = row * a.ldo + size_t(bx) * 128 + c8;
+          if (a.out[0]) *reinterpret_cast<uint4*>(a.out[0] + oc) = gv4;
+          if (a.out[1]) *reinterpret_cast<uint4*>(a.out[1] + oc) = uv4;
+          if (a.gs_tab && !a.gs_tab[a.grow_expert[row]]) continue;
+          const Fp8Block blk = fp8_block_scale(am);
+          uint32_t qb[2];
+          fp8_codes8(hv, blk, qb[0], qb[1]);
+          const size_t o = row * N + size_t(bx) * 128 + c8;
+          if (a.hq) *reinterpret_cast<uint2*>(a.hq + o) = make_uint2(qb[0], qb[1]);
+          if (a.hh)  // the fake-quantized rows (the codes decoded back, exact), only when asked for
+            *reinterpret_cast<uint4*>(a.hh + o) = __builtin_bit_cast(uint4, fp8x8_to_bf16(qb[0], qb[1], blk.sc));
+          if (a.hs && c8 == 0) a.hs[row * (N / 128) + bx] = blk.se;
         }
       }
-    } else {
-      // bf16 g (w1) and u (w3) tiles in LDS, then 8 consecutive outputs of one row per thread: h = bf16(SwiGLU(g, u)),
-      // the row's amax over its 128 outputs (16 threads: a DPP row max), fake quantization, 16-byte stores.
-      uint16_t* const tg = reinterpret_cast<uint16_t*>(smem);
-      uint16_t* const tu = tg + 128 * GP_LDC2;
-      uint16_t* const mine = q_own ? tu : tg;
-      const int chh = cq & 1;
-#pragma unroll
-      for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i)
-            mine[row_of(rb, i) * GP_LDC2 + chh * 64 + cb * 32 + l32] = f32_to_bf16(acc[rb][cb][i]);
-      __syncthreads();
-      for (int e0 = 0; e0 < M * 16; e0 += 256) {  // uniform bound: every 16-lane group is whole
-        const int e = e0 + tid, r = min(e / 16, M - 1), c8 = (e % 16) * 8;
-        const size_t row = row0 + r;
-        const uint4 gv4 = *reinterpret_cast<const uint4*>(tg + r * GP_LDC2 + c8);
-        const uint4 uv4 = *reinterpret_cast<const uint4*>(tu + r * GP_LDC2 + c8);
-        const uint32_t gw4[4] = {gv4.x, gv4.y, gv4.z, gv4.w}, uw4[4] = {uv4.x, uv4.y, uv4.z, uv4.w};
-        const float w = a.gw ? a.gw[row] : 0.0f;
-        float hv[8], am = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          hv[q] = round_bf16(swiglu_value(bf16_to_f32(uint16_t(gw4[q / 2] >> (16 * (q % 2)))),
-                                          bf16_to_f32(uint16_t(uw4[q / 2] >> (16 * (q % 2)))), w, a.gw != nullptr,
-                                          a.limit));
-          am = fmaxf(am, fabsf(hv[q]));
-        }
-        am = row16_max(am);
-        if (e >= M * 16) continue;
-        const size_t oc = row * a.ldo + size_t(bx) * 128 + c8;
-        if (a.out[0]) *reinterpret_cast<uint4*>(a.out[0] + oc) = gv4;
-        if (a.out[1]) *reinterpret_cast<uint4*>(a.out[1] + oc) = uv4;
-        if (a.gs_tab && !a.gs_tab[a.grow_expert[row]]) continue;
-        const Fp8Block blk = fp8_block_scale(am);
-        uint32_t qb[2];
-        fp8_codes8(hv, blk, qb[0], qb[1]);
-        const size_t o = row * N + size_t(bx) * 128 + c8;
-        if (a.hq) *reinterpret_cast<uint2*>(a.hq + o) = make_uint2(qb[0], qb[1]);
-        if (a.hh)  // the fake-quantized rows (the codes decoded back, exact), only when asked for
-          *reinterpret_cast<uint4*>(a.hh + o) = __builtin_bit_cast(uint4, fp8x8_to_bf16(qb[0], qb[1], blk.sc));
-        if (a.hs && c8 == 0) a.hs[row * (N / 128) + bx] = blk.se;
-      }
-    }
+    };
+    if (rb_live == 4) tile_body(std::integral_constant<int, 4>{});
+    else if (rb_live == 3) tile_body(std::integral_constant<int, 3>{});
+    else if (rb_live == 2) tile_body(std::integral_constant<int, 2>{});
+    else tile_body(std::integral_constant<int, 1>{});
   }
 }
 

@@ -140,7 +140,7 @@ unsigned transform_blocks(int P, int K) { return unsigned(std::min<size_t>((size
 // byte, dequantizes them exactly to bf16 with the scaled conversion instructions and issues four bf16 MFMAs against
 // the matching activation inputs. The MFMA accumulates in fp32 with exact products; no cross-lane reductions.
 // GV_PF: weight steps in flight per wave (8 measured slower: the larger ring costs occupancy).
-constexpr int GV_WAVES = 8, GV_NT = 64 * GV_WAVES, GV_PAD = 16, GV_MAXROWS = 16, GV_PF = 4;
+constexpr int GV_WAVES = 8, GV_PAD = 16, GV_MAXROWS = 16, GV_PF = 4;
 
 // AM: activation source -- 0: e4m3 codes + e8m0 scales (aq, as); 1: fake-quantized bf16 rows (xa), codes recovered
 // exactly; 2: raw bf16 token rows x[x_rows[r]] quantized here with the reference's act_quant (mx_xform_in_fp8 fused).
