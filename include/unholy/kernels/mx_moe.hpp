@@ -122,6 +122,17 @@ void mx_grouped_gemm_x(const bf16* x, int ldx, const int32_t* x_rows, int K, con
                        const uint8_t* const* w_tab, const uint8_t* const* s_tab, bf16* out, int ldo, int N,
                        hipStream_t st, const int* ntiles_dev = nullptr, const uint8_t* const* w_tab2 = nullptr,
                        const uint8_t* const* s_tab2 = nullptr, bf16* out2 = nullptr, const MxGlu& glu = {});
+// The prefill GEMM on e4m3 codes with fp32 outputs (no bf16 rounding): for accuracy checks against an fp64 oracle.
+// No reference counterpart.
+void mx_grouped_gemm_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles, int ntiles,
+                              const uint8_t* const* w_tab, const uint8_t* const* s_tab, float* out, int ldo, int N,
+                              hipStream_t st, const int* ntiles_dev = nullptr);
+// The arithmetic of the prefill GEMM on e4m3 codes (no reference counterpart): 0 (default) the block-scaled MFMA
+// (fp8 x fp4 with the e8m0 scales in the instruction), 1 exact dequantization to bf16 + bf16 MFMA (fp32 sums of
+// exact products, the reference's arithmetic in another order). UH_GEMM_EXACT=1 sets the default to 1. Returns the
+// previous setting.
+int mx_gemm_set_exact(int on);
+bool mx_gemm_exact();
 // The GEMV with fp32 outputs (no bf16 rounding): for accuracy checks against an fp64 oracle.
 void mx_grouped_gemv_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles, int ntiles,
                               const uint8_t* const* w_tab, const uint8_t* const* s_tab, float* out, int ldo, int N,

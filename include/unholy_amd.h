@@ -112,6 +112,14 @@ int uh_mx_grouped_gemm_x(const uint16_t* x, int ldx, const int32_t* x_rows, int 
                          const uint8_t* const* s_tab2, uint16_t* out2, const float* glu_w,
                          const int32_t* glu_row_expert, const uint8_t* const* glu_s_tab, uint16_t* glu_hh,
                          uint8_t* glu_hq, uint8_t* glu_hs, float glu_limit);
+/* No reference counterpart: the prefill GEMM (uh_mx_grouped_gemm_q, one projection) with fp32 outputs (before bf16
+ * rounding), for accuracy checks. N % 256 == 0. */
+int uh_mx_grouped_gemm_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const int32_t* tiles, int ntiles,
+                                const uint8_t* const* w_tab, const uint8_t* const* s_tab, float* out, int ldo, int N,
+                                void* stream, const int* ntiles_dev);
+/* No reference counterpart: the prefill GEMM's arithmetic on e4m3 codes: 0 (default) the block-scaled MFMA, 1 exact
+ * bf16 dequantization + bf16 MFMA. Process-wide; returns the previous setting. */
+int uh_mx_gemm_set_exact(int on);
 /* No reference counterpart: uh_mx_grouped_gemv_q with fp32 outputs (before bf16 rounding), for accuracy checks. */
 int uh_mx_grouped_gemv_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const int32_t* tiles, int ntiles,
                                 const uint8_t* const* w_tab, const uint8_t* const* s_tab, float* out, int ldo, int N,

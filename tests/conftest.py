@@ -10,3 +10,12 @@ if str(ROOT) not in sys.path:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) and the built libunholy_amd.so")
+
+
+@pytest.fixture(params=["scaled", "exact"])
+def gemm_arith(request):
+    """The prefill GEMM's arithmetic for one test: the block-scaled MFMA (default) or exact bf16 dequantization."""
+    from unholy_amd import call
+    prev = call("uh_mx_gemm_set_exact", 1 if request.param == "exact" else 0)
+    yield request.param
+    call("uh_mx_gemm_set_exact", prev)

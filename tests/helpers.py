@@ -36,6 +36,14 @@ def max_rel(y, r, floor_frac=2.0 ** -8):
     return float(np.max(np.abs(y - r) / den)) if r.size else 0.0
 
 
+def max_abs_rms(y, r):
+    """max |y - r| / rms(r): the largest error as a fraction of the output scale."""
+    y = np.asarray(y, np.float64)
+    r = np.asarray(r, np.float64)
+    rms = np.sqrt(np.mean(r * r)) if r.size else 0.0
+    return float(np.max(np.abs(y - r)) / rms) if rms else float(np.max(np.abs(y - r), initial=0.0))
+
+
 def rel_l2(y, r):
     y = np.asarray(y, np.float64)
     r = np.asarray(r, np.float64)

@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.helpers import from_bf16, max_rel, mx_weights, randn_bf16, rel_l2
+from tests.helpers import from_bf16, max_abs_rms, max_rel, mx_weights, randn_bf16, rel_l2
 from unholy_amd import call
 from unholy_amd.device import DeviceBuffer, pointer_table, synchronize
 
@@ -137,7 +137,16 @@ def _moe_case(rng, T, E, K, D, I, bias_scale=0.0):
 
 @pytest.mark.parametrize("T,E,K,D,I,bias", [(8, 32, 6, 1024, 512, 0.0), (64, 64, 6, 512, 256, 0.5),
                                             (200, 16, 4, 512, 256, 0.0)])
-def test_moe_forward_vs_oracle(T, E, K, D, I, bias):
+def test_moe_forward_vs_oracle(T, E, K, D, I, bias, gemm_arith):
+    """The whole forward against the oracle. T <= 64 runs the GEMVs (exact dequantization): max-rel <= 1e-2 per
+    element. Larger T runs the prefill GEMM: with exact dequantization the same bar; with the block-scaled MFMA
+    (the default) rel L2 <= 1e-3, the reference's criterion for its fast path (tools/kernel_test/mx_moe.hip:3), and
+    max |err| <= 0.05 rms against gross errors (the exact path itself reaches ~0.015 rms: bf16 rounding of the
+    largest outputs). The block-scaled sums round a few bf16 g / u values one ulp away from the oracle's, and where
+    such a value sits at an e4m3 rounding boundary of h, one code of h moves one step, which shows at single outputs
+    near zero (per-element max-rel up to ~0.9 there)."""
+    if T <= 64 and gemm_arith != "scaled":
+        pytest.skip("T <= 64 does not run the prefill GEMM")
     rng = np.random.default_rng(T * 7 + E)
     limit = 10.0
     experts, bufs, tab, x, logits = _moe_case(rng, T, E, K, D, I, bias)
@@ -153,9 +162,12 @@ def test_moe_forward_vs_oracle(T, E, K, D, I, bias):
     assert np.array_equal(sel.download((T, K), np.int32), sel_ref)
     got = from_bf16(out.download((T, D), np.uint16))
     ref = from_bf16(out_ref)
-    mr = max_rel(got, ref)
-    print(f"moe T={T} E={E}: max_rel {mr:.3e}, rel_l2 {rel_l2(got, ref):.3e}")
-    assert mr <= 1e-2
+    mr, l2, ma = max_rel(got, ref), rel_l2(got, ref), max_abs_rms(got, ref)
+    print(f"moe T={T} E={E} {gemm_arith}: max_rel {mr:.3e}, rel_l2 {l2:.3e}, max|err|/rms {ma:.3e}")
+    if T > 64 and gemm_arith == "scaled":
+        assert l2 <= 1e-3 and ma <= 0.05
+    else:
+        assert mr <= 1e-2
 
 
 @pytest.mark.parametrize("mode", ["glm", "ds"])

@@ -312,6 +312,14 @@ int uh_mx_grouped_gemm_x(const uint16_t* x, int ldx, const int32_t* x_rows, int 
                          s_tab2, out2, glu);
   });
 }
+int uh_mx_grouped_gemm_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const int32_t* tiles, int ntiles,
+                                const uint8_t* const* w_tab, const uint8_t* const* s_tab, float* out, int ldo, int N,
+                                void* st, const int* ntiles_dev) {
+  return guard([&] {
+    k::mx_grouped_gemm_q_f32out(q, qs, K, T3(tiles), ntiles, w_tab, s_tab, out, ldo, N, S(st), ntiles_dev);
+  });
+}
+int uh_mx_gemm_set_exact(int on) { return k::mx_gemm_set_exact(on); }
 int uh_mx_grouped_gemv_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const int32_t* tiles, int ntiles,
                                 const uint8_t* const* w_tab, const uint8_t* const* s_tab, float* out, int ldo, int N,
                                 void* st, const int* ntiles_dev, int max_rows) {

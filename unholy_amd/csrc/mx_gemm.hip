@@ -352,7 +352,7 @@ constexpr int GP_LDC1 = 256 + 8, GP_LDC2 = 128 + 8;
 constexpr int GP_C1 = 128 * GP_LDC1 * 2, GP_C2 = 2 * 128 * GP_LDC2 * 2;
 static_assert(GP_C1 <= GP_RING, "the bf16 C tile reuses the ring");
 
-template <int NP>
+template <int NP, bool SC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mx_gemm_pipe_kernel(MxGemvArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   int bx, by;
@@ -411,61 +411,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
       const uint8_t* srow = a.as + size_t(a.x_rows ? a.x_rows[row0 + r] : int(row0 + r)) * KS;
       for (int e = tid; e < 128 * KS; e += 256) as_lds[e] = srow[e >> 7];
     }
-    // The K loop and the epilogue, specialised on the tile's live 32-row blocks (RB): each stage is one basic block
-    // the compiler can interleave, and only live accumulators exist (dead ones kept alive across the loop cost
-    // register copies in every stage).
-    const auto tile_body = [&](auto nrb) {
-      constexpr int RB = decltype(nrb)::value;
-      v16f_t acc[RB][2];
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = v16f_t{};
-      for (int s = 0; s < KS; ++s) {
-        wait_vm<0>();     // this wave's part of stage s (the only stage in flight)
-        __syncthreads();  // every wave's part has landed; the other slot (stage s - 1) is free
-        if (s + 1 < KS) issue(s + 1);
-        const uint8_t* stb = smem + (s % GP_S) * GP_STAGE;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          v4i bq[2];
-          float bs[2];
-#pragma unroll
-          for (int cb = 0; cb < 2; ++cb) {
-            const int c = (cq & 1) * 2 + cb, u = q_own * 8 + j * 4 + c, n = c * 32 + l32;
-            bq[cb] = *reinterpret_cast<const v4i*>(stb + GP_A + u * 1024 + (h * 32 + l32) * 16);
-            bs[cb] = __uint_as_float(
-                uint32_t(stb[GP_A + GP_B + (q_own * 2 + j) * 256 + (n >> 4) * 32 + (n & 15) * 2 + h]) << 23);
-          }
-          v4i aq[RB][2];
-          float asc[RB];
-#pragma unroll
-          for (int rb = 0; rb < RB; ++rb) {
-            const int r = rb * 32 + l32;
-#pragma unroll
-            for (int x = 0; x < 2; ++x)
-              aq[rb][x] = *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 * j + 2 * h + x) ^ lds_swz(r))) * 16);
-            asc[rb] = __uint_as_float(uint32_t(as_lds[s * 128 + r]) << 23);
-          }
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            bf16x8 bf[2];
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) bf[cb] = fp4x8_to_bf16(uint32_t(bq[cb][t]), bs[cb]);
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb) {
-              const bf16x8 af = fp8x8_to_bf16(uint32_t(aq[rb][t >> 1][(t & 1) * 2]),
-                                              uint32_t(aq[rb][t >> 1][(t & 1) * 2 + 1]), asc[rb]);
-#pragma unroll
-              for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = mfma32_bf16(af, bf[cb], acc[rb][cb]);
-            }
-          }
-        }
-      }
-
-      // ---- epilogue (the ring is free once every wave is past its last stage)
+    // The epilogue, given each(f): f(row, column in the wave's 64, value) for every accumulator element.
+    const auto epilogue = [&](const auto& each) {
+      // ---- the ring is free once every wave is past its last stage
       __syncthreads();
-      const auto row_of = [&](int rb, int i) { return rb * 32 + 8 * (i / 4) + 4 * h + (i % 4); };
       if constexpr (NP == 1) {
         const int c0 = cq * 64;
         if (a.out32) {  // fp32 outputs (accuracy checks): two passes of 64 rows through the ring
@@ -475,16 +424,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
 #pragma unroll
           for (int half = 0; half < 2; ++half) {
             if (half) __syncthreads();  // the first half's stores have read the tile
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-              constexpr int kNone = -1;
-              const int rb = 2 * half + k < RB ? 2 * half + k : kNone;  // compile-time after unrolling
-              if (rb == kNone) continue;
-#pragma unroll
-              for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) sf[(row_of(k, i)) * LDF + c0 + cb * 32 + l32] = acc[rb][cb][i];
-            }
+            each([&](int row, int col, float v) {
+              if (row >= 64 * half && row < 64 * half + 64) sf[(row - 64 * half) * LDF + c0 + col] = v;
+            });
             __syncthreads();
             for (int e = tid; e < min(64, M - 64 * half) * 64; e += 256) {
               const int r = e / 64, c4 = (e % 64) * 4;
@@ -494,12 +436,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
           }
         } else {
           uint16_t* sc = reinterpret_cast<uint16_t*>(smem);
-#pragma unroll
-          for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-              for (int i = 0; i < 16; ++i) sc[row_of(rb, i) * GP_LDC1 + c0 + cb * 32 + l32] = f32_to_bf16(acc[rb][cb][i]);
+          each([&](int row, int col, float v) { sc[row * GP_LDC1 + c0 + col] = f32_to_bf16(v); });
           __syncthreads();
           for (int e = tid; e < M * 32; e += 256) {
             const int r = e / 32, c8 = (e % 32) * 8;
@@ -514,13 +451,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
         uint16_t* const tu = tg + 128 * GP_LDC2;
         uint16_t* const mine = q_own ? tu : tg;
         const int chh = cq & 1;
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-          for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-            for (int i = 0; i < 16; ++i)
-              mine[row_of(rb, i) * GP_LDC2 + chh * 64 + cb * 32 + l32] = f32_to_bf16(acc[rb][cb][i]);
+        each([&](int row, int col, float v) { mine[row * GP_LDC2 + chh * 64 + col] = f32_to_bf16(v); });
         __syncthreads();
         for (int e0 = 0; e0 < M * 16; e0 += 256) {  // uniform bound: every 16-lane group is whole
           const int e = e0 + tid, r = min(e / 16, M - 1), c8 = (e % 16) * 8;
@@ -554,17 +485,133 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
         }
       }
     };
-    if (rb_live == 4) tile_body(std::integral_constant<int, 4>{});
-    else if (rb_live == 3) tile_body(std::integral_constant<int, 3>{});
-    else if (rb_live == 2) tile_body(std::integral_constant<int, 2>{});
-    else tile_body(std::integral_constant<int, 1>{});
+
+    // The K loop, specialised on the tile's live row blocks (RB): each stage is one basic block the compiler can
+    // interleave, and only live accumulators exist (dead ones kept alive across the loop cost register copies in
+    // every stage).
+    const auto tile_body = [&](auto nrb) {
+      constexpr int RB = decltype(nrb)::value;
+      if constexpr (SC) {
+        // Scaled MFMA 16x16x128 (fp8 x fp4, per-32 e8m0 scales in the instruction), 16-row blocks; no conversions.
+        v4f acc[RB][4];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        const int m16 = lane & 15, g = lane >> 4, jb = g >> 1, hb = g & 1;
+        for (int s = 0; s < KS; ++s) {
+          wait_vm<0>();     // this wave's part of stage s (the only stage in flight)
+          __syncthreads();  // every wave's part has landed; the other slot (stage s - 1) is free
+          if (s + 1 < KS) issue(s + 1);
+          const uint8_t* stb = smem + (s % GP_S) * GP_STAGE;
+          v4i bq[4];
+          int bsc[4];
+#pragma unroll
+          for (int cb = 0; cb < 4; ++cb) {  // column cq % 2 * 64 + 16 cb + m16, inputs 32 g .. 32 g + 31
+            const int n = (cq & 1) * 64 + cb * 16 + m16, c = n >> 5;
+            bq[cb] = *reinterpret_cast<const v4i*>(stb + GP_A + (q_own * 8 + jb * 4 + c) * 1024 + (hb * 32 + (n & 31)) * 16);
+            bsc[cb] = stb[GP_A + GP_B + (q_own * 2 + jb) * 256 + (n >> 4) * 32 + (n & 15) * 2 + hb];
+          }
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) {  // row 16 rb + m16: inputs 16 g .. + 15 and 64 + 16 g .. + 15
+            const int r = rb * 16 + m16;
+            const v4i lo = *reinterpret_cast<const v4i*>(stb + (r * 8 + (g ^ lds_swz(r))) * 16);
+            const v4i hi = *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 + g) ^ lds_swz(r))) * 16);
+            const v8i aq = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            const int asc = as_lds[s * 128 + r];
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = mfma_fp8_fp4(aq, bq[cb], asc, bsc[cb], acc[rb][cb]);
+          }
+        }
+        epilogue([&](const auto& f) {
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) f(rb * 16 + 4 * g + i, cb * 16 + m16, acc[rb][cb][i]);
+        });
+      } else {
+        v16f_t acc[RB][2];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = v16f_t{};
+        for (int s = 0; s < KS; ++s) {
+          wait_vm<0>();     // this wave's part of stage s (the only stage in flight)
+          __syncthreads();  // every wave's part has landed; the other slot (stage s - 1) is free
+          if (s + 1 < KS) issue(s + 1);
+          const uint8_t* stb = smem + (s % GP_S) * GP_STAGE;
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            v4i bq[2];
+            float bs[2];
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+              const int c = (cq & 1) * 2 + cb, u = q_own * 8 + j * 4 + c, n = c * 32 + l32;
+              bq[cb] = *reinterpret_cast<const v4i*>(stb + GP_A + u * 1024 + (h * 32 + l32) * 16);
+              bs[cb] = __uint_as_float(
+                  uint32_t(stb[GP_A + GP_B + (q_own * 2 + j) * 256 + (n >> 4) * 32 + (n & 15) * 2 + h]) << 23);
+            }
+            v4i aq[RB][2];
+            float asc[RB];
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+              const int r = rb * 32 + l32;
+#pragma unroll
+              for (int x = 0; x < 2; ++x)
+                aq[rb][x] = *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 * j + 2 * h + x) ^ lds_swz(r))) * 16);
+              asc[rb] = __uint_as_float(uint32_t(as_lds[s * 128 + r]) << 23);
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              bf16x8 bf[2];
+#pragma unroll
+              for (int cb = 0; cb < 2; ++cb) bf[cb] = fp4x8_to_bf16(uint32_t(bq[cb][t]), bs[cb]);
+#pragma unroll
+              for (int rb = 0; rb < RB; ++rb) {
+                const bf16x8 af = fp8x8_to_bf16(uint32_t(aq[rb][t >> 1][(t & 1) * 2]),
+                                                uint32_t(aq[rb][t >> 1][(t & 1) * 2 + 1]), asc[rb]);
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = mfma32_bf16(af, bf[cb], acc[rb][cb]);
+              }
+            }
+          }
+        }
+        epilogue([&](const auto& f) {
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+              for (int i = 0; i < 16; ++i) f(rb * 32 + 8 * (i / 4) + 4 * h + (i % 4), cb * 32 + l32, acc[rb][cb][i]);
+        });
+      }
+    };
+    if constexpr (SC) {
+      const int rb16 = __builtin_amdgcn_readfirstlane((M + 15) / 16);
+      if (rb16 == 8) tile_body(std::integral_constant<int, 8>{});
+      else if (rb16 == 7) tile_body(std::integral_constant<int, 7>{});
+      else if (rb16 == 6) tile_body(std::integral_constant<int, 6>{});
+      else if (rb16 == 5) tile_body(std::integral_constant<int, 5>{});
+      else if (rb16 == 4) tile_body(std::integral_constant<int, 4>{});
+      else if (rb16 == 3) tile_body(std::integral_constant<int, 3>{});
+      else if (rb16 == 2) tile_body(std::integral_constant<int, 2>{});
+      else tile_body(std::integral_constant<int, 1>{});
+    } else {
+      if (rb_live == 4) tile_body(std::integral_constant<int, 4>{});
+      else if (rb_live == 3) tile_body(std::integral_constant<int, 3>{});
+      else if (rb_live == 2) tile_body(std::integral_constant<int, 2>{});
+      else tile_body(std::integral_constant<int, 1>{});
+    }
   }
 }
+
 
 template <int NP>
 void launch_pipe_t(const MxGemvArgs& a, int ntiles, hipStream_t st) {
   const size_t lds = std::max<size_t>(size_t(GP_RING) + size_t(128) * (a.K / 128), NP == 2 ? GP_C2 : GP_C1);
-  auto* kern = &mx_gemm_pipe_kernel<NP>;
+  auto* kern = mx_gemm_exact() ? &mx_gemm_pipe_kernel<NP, false> : &mx_gemm_pipe_kernel<NP, true>;
   UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                int(lds)));
   MxGemvArgs b = a;
@@ -694,6 +741,32 @@ void mx_grouped_gemm_q(const uint8_t* q, const uint8_t* qs, int K, const Exl3Til
   MxGemvArgs a = gemm_args(nullptr, q, qs, K, tiles, w_tab, s_tab, out, ldo, N, ntiles_dev, w_tab2, s_tab2, out2, glu);
   a.x_rows = x_rows;
   launch_mx_gemm(a, ntiles, 0, st);
+}
+
+void mx_grouped_gemm_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles, int ntiles,
+                              const uint8_t* const* w_tab, const uint8_t* const* s_tab, float* out, int ldo, int N,
+                              hipStream_t st, const int* ntiles_dev) {
+  if (N % 256) throw std::runtime_error("mx_grouped_gemm_q_f32out: N % 256");
+  MxGemvArgs a = gemm_args(nullptr, q, qs, K, tiles, w_tab, s_tab, nullptr, ldo, N, ntiles_dev, nullptr, nullptr,
+                           nullptr, MxGlu{});
+  a.out32 = out;
+  launch_mx_gemm(a, ntiles, 0, st);
+}
+
+namespace {
+int g_gemm_exact = -1;
+}
+bool mx_gemm_exact() {
+  static const bool env = [] {
+    const char* v = std::getenv("UH_GEMM_EXACT");
+    return v && v[0] == '1';
+  }();
+  return g_gemm_exact < 0 ? env : g_gemm_exact > 0;
+}
+int mx_gemm_set_exact(int on) {
+  const int prev = mx_gemm_exact() ? 1 : 0;
+  g_gemm_exact = on ? 1 : 0;
+  return prev;
 }
 
 void mx_grouped_gemm_x(const bf16* x, int ldx, const int32_t* x_rows, int K, const Exl3Tile* tiles, int ntiles,
