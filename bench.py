@@ -36,6 +36,7 @@ HBM_PEAK_GBS = 8000.0
 # rocprofv3 --pmc runs, scaled by the same counters on a 1 GiB device copy (profiles/hbm_traffic_pmc.md).
 GEMV_TRAFFIC_BYTES = 398.9e6
 BF16_PEAK_TFLOPS = 2500.0
+FP8_PEAK_TFLOPS = 5000.0  # the block-scaled fp8 x fp4 MFMA runs at the fp8 rate (4.29 PFLOP/s sustained, measured)
 
 
 def to_bf16(x):
@@ -319,12 +320,22 @@ def main():
         wl["moe_verify_T64 (configs[2])"] = {"ms": v["ms"], "tokens_per_s": 64 / (v["ms"] * 1e-3),
                                               "distinct_experts": v["U"],
                                               "GBps_weights": v["U"] * EXPERT_BYTES / (v["ms"] * 1e-3) / 1e9}
-        p = bench_moe(w, 4096, 5, 1, rng, R=2)
+        from unholy_amd import call
         flops = 4096 * TOPK * 3 * 2 * D * I
-        wl["moe_prefill_T4096 (configs[3])"] = {"ms": p["ms"], "tokens_per_s": 4096 / (p["ms"] * 1e-3),
-                                                 "TFLOPs": flops / (p["ms"] * 1e-3) / 1e12,
-                                                 "frac_bf16_mfma_peak": flops / (p["ms"] * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
-                                                 "GBps_weights": E * EXPERT_BYTES / (p["ms"] * 1e-3) / 1e9}
+        p = bench_moe(w, 4096, 5, 1, rng, R=2)
+        prev = call("uh_mx_gemm_set_exact", 1)
+        try:
+            px = bench_moe(w, 4096, 5, 1, rng, R=2)
+        finally:
+            call("uh_mx_gemm_set_exact", prev)
+        wl["moe_prefill_T4096 (configs[3])"] = {
+            "ms": p["ms"], "tokens_per_s": 4096 / (p["ms"] * 1e-3),
+            "TFLOPs": flops / (p["ms"] * 1e-3) / 1e12,
+            "mfma": "v_mfma_scale_f32_16x16x128_f8f6f4 (e4m3 x e2m1, e8m0 block scales)",
+            "frac_mfma_peak": flops / (p["ms"] * 1e-3) / 1e12 / FP8_PEAK_TFLOPS,
+            "GBps_weights": E * EXPERT_BYTES / (p["ms"] * 1e-3) / 1e9,
+            "exact_dequant_bf16_mfma": {"ms": px["ms"], "TFLOPs": flops / (px["ms"] * 1e-3) / 1e12,
+                                        "frac_bf16_mfma_peak": flops / (px["ms"] * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}}
         for M, copies in ((1, 64), (64, 64), (4096, 4)):
             t = bench_fp8_dense(M, 100 if M < 4096 else 10, 10 if M < 4096 else 2, rng, copies)
             wl[f"fp8_dense_M{M} (configs[4])"] = {"ms": t, "tokens_per_s": M / (t * 1e-3),

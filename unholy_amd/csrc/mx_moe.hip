@@ -548,9 +548,11 @@ void launch_mx_gemv(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st) 
   if (glu) UH_GV(2, 1);
   else if (graw) UH_GV(2, 2);
   else if (np2) UH_GV(2, 0);
-  else if (!a.out32 && a.N % 32 == 0 && gemv_split_enabled()) {
+  else if (!a.out32 && a.N % 32 == 0 && size_t(ntiles) * cdiv(size_t(a.N) / 32, GV_WAVES) >= 512 &&
+           gemv_split_enabled()) {
     // One matrix as two column streams per wave: twice the weight bytes behind each workgroup's start-up (the
-    // staging of its rows and the first loads), half the workgroups.
+    // staging of its rows and the first loads), half the workgroups -- when at least 512 remain (two per CU); a
+    // smaller launch is latency-bound and wants every workgroup it can get.
     MxGemvArgs b = a;
     b.split = a.N / 32;
     b.w_tab[1] = a.w_tab[0];
