@@ -147,8 +147,11 @@ constexpr int GV_WAVES = 8, GV_PAD = 16, GV_MAXROWS = 16, GV_PF = 4;
 // GM: epilogue -- 0: plain outputs; 1: SwiGLU + fp8 requantization of each row's 128-output block (W = 8 waves
 // cover the block); 2: SwiGLU to raw bf16 rows h (no requantization: the consumer quantizes them while staging).
 // W: waves per workgroup (16 outputs each).
-template <int NP, int GM, int AM, int W>
+// KSPLIT (small launches, plain outputs): the workgroup is one 16-column tile whose W waves take K / W steps each, so
+// every wave's weight loads are in flight at once; the partial sums are added in LDS in wave order.
+template <int NP, int GM, int AM, int W, bool KSPLIT = false>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void mx_gemv_kernel(MxGemvArgs a) {
+  static_assert(!KSPLIT || GM == 0, "the K split has a plain epilogue");
   constexpr int NT = 64 * W;
   extern __shared__ __align__(16) uint8_t smem[];
   if (a.ntiles_dev && int(blockIdx.y) >= *a.ntiles_dev) return;
@@ -174,8 +177,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
   uint8_t* sA = smem;
   uint8_t* sS = smem + size_t(a.rows_cap) * ldA;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nl = lane & 15, g = lane >> 4;
-  const int nt = blockIdx.x * W + wave;
+  const int nt = KSPLIT ? int(blockIdx.x) : int(blockIdx.x) * W + wave;
   const bool active = nt < (a.split ? a.split : ntn);  // uniform per wave
+  const int sb = KSPLIT ? wave * (KS / W) : 0, se = KSPLIT ? sb + KS / W : KS;  // this wave's K steps
   const int boff = nl * 32 + (g & 1) * 16;
   for (int rg = 0; rg < tile.rows; rg += a.rows_cap) {
     const int M = min(a.rows_cap, tile.rows - rg);
@@ -208,9 +212,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
       }
     };
     if (active) {
-      load_scales(0, sq_cur);
+      load_scales(sb, sq_cur);
 #pragma unroll
-      for (int i = 0; i < GV_PF; ++i) load_step(min(i, KS - 1), i);  // K < 128 * GV_PF: re-read the last step
+      for (int i = 0; i < GV_PF; ++i) load_step(min(sb + i, se - 1), i);  // fewer than GV_PF steps: re-read the last
     }
     __syncthreads();
     if constexpr (AM != 0) {
@@ -296,15 +300,15 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
       }
     };
     if (active) {
-      int s0 = 0;
+      int s0 = sb;
       // Every round but the last loads the next round's weights. The loads are unconditional (a conditional load
       // would leave the compiler unsure how many are outstanding, and it would then wait for all of them each
       // round); with K % 512 == 0 none of them is past the end (otherwise they re-read the last step).
-      for (; s0 + GV_PF < KS; s0 += GV_PF) {
+      for (; s0 + GV_PF < se; s0 += GV_PF) {
 #pragma unroll
         for (int i = 0; i < GV_PF; ++i) {
-          if (s0 + i < KS) step(s0 + i, i);
-          load_step(min(s0 + i + GV_PF, KS - 1), i);
+          if (s0 + i < se) step(s0 + i, i);
+          load_step(min(s0 + i + GV_PF, se - 1), i);
           if (i == 0) load_scales(s0 + GV_PF, sq_nxt);
           // Keep each step's conversions and MFMAs together: interleaving the unrolled steps would only raise
           // register pressure (the loads of later steps are already in flight).
@@ -317,13 +321,28 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
       }
 #pragma unroll
       for (int i = 0; i < GV_PF; ++i) {  // the last round: nothing left to load
-        if (s0 + i < KS) step(s0 + i, i);
+        if (s0 + i < se) step(s0 + i, i);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+    if constexpr (KSPLIT) {  // the W partial sums of the tile, added in wave order, into wave 0
+      __syncthreads();      // every wave is past its reads of the staged rows
+      v4f* red = reinterpret_cast<v4f*>(smem);
+#pragma unroll
+      for (int p = 0; p < NP; ++p) red[(wave * NP + p) * 64 + lane] = acc[p];
+      __syncthreads();
+      if (wave == 0)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          v4f t = red[p * 64 + lane];
+#pragma unroll
+          for (int w = 1; w < W; ++w) t += red[(w * NP + p) * 64 + lane];
+          acc[p] = t;
+        }
+    }
 
     if constexpr (GM == 0) {
-      if (active)
+      if (active && (!KSPLIT || wave == 0))
 #pragma unroll
         for (int p = 0; p < NP; ++p)
 #pragma unroll
@@ -499,15 +518,34 @@ void set_lds_limit(K kernel, size_t bytes) {
                                                   hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes)));
 }
 
+static bool ksplit_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("UH_GEMV_KSPLIT");
+    return !v || std::string(v) != "0";
+  }();
+  return on;
+}
+
 // Workgroup shape: 8 waves (128 outputs) for every launch. A requantizing epilogue needs a whole 128-output block;
 // for the others 8-wave workgroups measured 1% (decode) to 3% (verify) faster than 4-wave ones, whose smaller work
 // items were expected to balance better.
 template <int NP, int GM, int AM, int W>
 void launch_gemv_w(const MxGemvArgs& a, int ntiles, hipStream_t st) {
   const size_t lds = size_t(a.rows_cap) * (a.K + GV_PAD) + size_t(a.rows_cap) * (a.K / 128);
+  const size_t ntn = a.split ? size_t(a.split) : size_t(a.N) / 16;
+  if constexpr (GM == 0 && NP == 1) {
+    // A launch of fewer than 256 workgroups (one per CU) is latency-bound: split each tile's K over its waves.
+    if (size_t(ntiles) * cdiv(ntn, W) < 256 && a.K % (128 * W) == 0 && !a.out32 && ksplit_enabled()) {
+      auto* kern = &mx_gemv_kernel<NP, GM, AM, W, true>;
+      set_lds_limit(kern, std::max<size_t>(lds, size_t(W) * NP * 64 * 16));
+      kern<<<dim3(unsigned(ntn), unsigned(ntiles), 1), 64 * W, std::max<size_t>(lds, size_t(W) * NP * 64 * 16), st>>>(a);
+      UH_CHECK_LAUNCH();
+      return;
+    }
+  }
   auto* kern = &mx_gemv_kernel<NP, GM, AM, W>;
   set_lds_limit(kern, lds);
-  const dim3 grid(cdiv(a.split ? size_t(a.split) : size_t(a.N) / 16, W), unsigned(ntiles), 1);
+  const dim3 grid(cdiv(ntn, W), unsigned(ntiles), 1);
   kern<<<grid, 64 * W, lds, st>>>(a);
   UH_CHECK_LAUNCH();
 }
