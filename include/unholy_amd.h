@@ -67,7 +67,8 @@ int uh_mx_swiglu(const uint16_t* g, const uint16_t* u, const float* w, const int
  * software round-to-nearest-even encode on every fp32 value in [-448, 448]; *bad = mismatching codes. */
 int uh_check_fp8_encode(unsigned long long* bad, unsigned long long* total);
 /* No reference counterpart: exhaustive check of the hardware bf16 rounding (v_cvt_pk_bf16_f32) against the software
- * round-to-nearest-even over all 2^32 fp32 bit patterns; *bad at non-NaN inputs, *nan_bad at NaN inputs. */
+ * round-to-nearest-even over all 2^32 fp32 bit patterns; *bad = mismatches at non-NaN inputs plus NaN inputs whose
+ * result is not a NaN, *nan_bad = NaN inputs whose NaN payload differs. */
 int uh_check_bf16_encode(unsigned long long* bad, unsigned long long* nan_bad);
 /* mx_moe.hpp:61: exhaustive MFMA block-scaled decode check; *bad = mismatches among normal results. */
 int uh_mx_check_dequant(unsigned long long* bad, unsigned long long* total);

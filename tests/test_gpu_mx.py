@@ -43,7 +43,8 @@ def test_check_fp8_encode_exhaustive():
 
 def test_check_bf16_encode_exhaustive():
     """The hardware bf16 rounding the kernels use for fp32 -> bf16 equals the software round-to-nearest-even (the
-    reference's rounding) at every non-NaN fp32 input; NaN inputs stay NaN (payloads may differ)."""
+    reference's rounding) at every non-NaN fp32 input, and every NaN input gives a NaN (payloads may differ; they are
+    counted apart and printed)."""
     bad = ctypes.c_ulonglong(0)
     nan_bad = ctypes.c_ulonglong(0)
     call("uh_check_bf16_encode", ctypes.byref(bad), ctypes.byref(nan_bad))

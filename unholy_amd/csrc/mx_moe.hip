@@ -456,9 +456,12 @@ __global__ __launch_bounds__(256) void bf16_check_encode_kernel(unsigned long lo
     const bf16x2_t v = {__bf16(x), __bf16(y)};
     const uint32_t hw = __builtin_bit_cast(uint32_t, v);
     const bool nan = (uint32_t(u) & 0x7fffffffu) > 0x7f800000u;
-    const unsigned m = ((hw & 0xffffu) != f32_to_bf16_sw(x)) + ((hw >> 16) != f32_to_bf16_sw(y));
-    if (nan) bad_nan += m;
-    else bad += m;
+    if (nan) {  // a NaN must stay a NaN; differing payloads are counted apart
+      bad += ((hw & 0x7fffu) <= 0x7f80u) + (((hw >> 16) & 0x7fffu) <= 0x7f80u);
+      bad_nan += ((hw & 0xffffu) != f32_to_bf16_sw(x)) + ((hw >> 16) != f32_to_bf16_sw(y));
+    } else {
+      bad += ((hw & 0xffffu) != f32_to_bf16_sw(x)) + ((hw >> 16) != f32_to_bf16_sw(y));
+    }
   }
   if (bad) atomicAdd(&cnt[0], bad);
   if (bad_nan) atomicAdd(&cnt[1], bad_nan);
