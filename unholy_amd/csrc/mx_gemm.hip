@@ -399,7 +399,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
       for (int i = 0; i < 4; ++i) {
         const int u = wave * 4 + i, q = u >> 3, j = (u >> 2) & 1, c = u & 3;
         const uint8_t* bb = wq[q] + size_t(2 * s + j) * cslab + size_t((colq0 + q * colq_step) / 16) * 512 + c * 1024;
-        dma16(bb, boff, st + uint32_t(GP_A + u * 1024));
+        dma16_nt(bb, boff, st + uint32_t(GP_A + u * 1024));
       }
       const uint8_t* sb = sq[sc_q] + size_t(2 * s + sc_j) * sslab + size_t((colq0 + sc_q * colq_step) / 16) * 32;
       if (lane < 16) dma16(sb, uint32_t(lane) * 16, st + uint32_t(GP_A + GP_B + (sc_q * 2 + sc_j) * 256));

@@ -38,6 +38,15 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t 
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
                : "memory", "m0");
 }
+// dma16 with the nontemporal policy, for data read once (expert weights streamed from HBM by the prefill GEMM:
+// 1.5-2.5% faster there). Not for data that other workgroups read again from L2 (the dense fp8 GEMM's weights, read
+// by every row tile: 12% slower with it).
+__device__ __forceinline__ void dma16_nt(const void* base, uint32_t voff, uint32_t lds) {
+  const uint64_t sbase = uniform_ptr(base);
+  lds = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase), "s"(lds)
+               : "memory", "m0");
+}
 // The same with 4 bytes per lane (to LDS lds + 4 * lane): a gather of one dword per lane.
 __device__ __forceinline__ void dma4(const void* base, uint32_t voff, uint32_t lds) {
   const uint64_t sbase = uniform_ptr(base);
