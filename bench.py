@@ -178,9 +178,10 @@ def bench_single_gemv(w, steps, warmup, rng):
     return time_graph(fn, steps, warmup, per_graph=64)
 
 
-def bench_fp8_dense(M, steps, warmup, rng, copies):
+def bench_fp8_dense(M, steps, warmup, rng, copies, fused=True):
     """A bf16 [M, 4096] -> e4m3 per 1x128 with fp32 scales (in the step); W e4m3 [4096, 4096]
-    with fp32 128x128 scales (quantized once from N(0, 0.02)); rotating over `copies` weight copies."""
+    with fp32 128x128 scales (quantized once from N(0, 0.02)); rotating over `copies` weight copies. For M <= 16
+    the quantization runs inside the GEMV (uh_gemm_fp8_f32s_x, the same results bit for bit) unless fused=False."""
     from unholy_amd import call
     from unholy_amd.device import DeviceBuffer
     N = K = 4096
@@ -195,6 +196,9 @@ def bench_fp8_dense(M, steps, warmup, rng, copies):
     c = DeviceBuffer(M * N * 2)
 
     def fn(i, stream):
+        if fused and M <= 16:
+            call("uh_gemm_fp8_f32s_x", x, K, wq[i % copies], ws, c, N, M, N, K, stream.handle)
+            return
         call("uh_act_quant_fp8_f32s", x, K, q, sa, M, K, 128, stream.handle)
         call("uh_gemm_fp8_f32s", q, sa, wq[i % copies], ws, c, N, M, N, K, stream.handle)
 
@@ -341,6 +345,9 @@ def main():
             wl[f"fp8_dense_M{M} (configs[4])"] = {"ms": t, "tokens_per_s": M / (t * 1e-3),
                                                   "TFLOPs": 2 * M * D * D / (t * 1e-3) / 1e12,
                                                   "GBps_weights": D * D / (t * 1e-3) / 1e9}
+            if M <= 16:  # the two-call form (act_quant_fp8_f32s, then gemm_fp8_f32s) beside the fused one
+                wl[f"fp8_dense_M{M} (configs[4])"]["ms_two_launches"] = bench_fp8_dense(M, 100, 10, rng, copies,
+                                                                                         fused=False)
         result["workloads"] = wl
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()

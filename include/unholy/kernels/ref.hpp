@@ -26,6 +26,10 @@ void gemm_w8a8(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint
 // weight block; C = sum_kb (raw_kb) * (sa * sw), fp32, bf16 out.
 void gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw, bf16* c, int ldc, int M,
                    int N, int K, hipStream_t st);
+// No reference counterpart: act_quant_fp8_f32s (block 128) of bf16 x [M, ldx] fused into gemm_fp8_f32s, M <= 16;
+// the same results bit for bit in one launch (for decode rows). ldx % 8 == 0, x 16-byte aligned.
+void gemm_fp8_f32s_x(const bf16* x, int ldx, const uint8_t* w, const float* sw, bf16* c, int ldc, int M, int N,
+                     int K, hipStream_t st);
 // fp8 activations x e2m1 weights [N, K/2] (row-major or the tile-major layout). Ref ref.hpp:139-143.
 void gemm_a8w4(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, bf16* c, int ldc, int M,
                int N, int K, hipStream_t st);

@@ -203,6 +203,10 @@ int uh_gemv_w8a8_glu(const uint8_t* a, const uint8_t* sa, const uint8_t* w_gate,
 /* kernel.py fp8_gemm with fp32 scales (scale_fmt=None); gemm_wmma.hip:89-100's fold */
 int uh_gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw, uint16_t* c, int ldc,
                      int M, int N, int K, void* stream);
+/* No reference counterpart: uh_act_quant_fp8_f32s (block 128) of bf16 x [M, ldx] fused into uh_gemm_fp8_f32s for
+ * M <= 16 (decode rows): the same results bit for bit, one launch. */
+int uh_gemm_fp8_f32s_x(const uint16_t* x, int ldx, const uint8_t* w, const float* sw, uint16_t* c, int ldc, int M,
+                       int N, int K, void* stream);
 /* ref.hpp:139-140 and :142-143: the reference-order (bit-exact) a8w4 GEMMs */
 int uh_gemm_a8w4(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, uint16_t* c, int ldc,
                  int M, int N, int K, void* stream);

@@ -47,6 +47,30 @@ def test_fp8_f32_scales(M, N, K):
     assert mr <= 1e-2
 
 
+@pytest.mark.parametrize("M,N,K,pad", [(1, 4096, 4096, 0), (5, 136, 384, 64), (16, 1024, 1024, 8), (3, 200, 256, 0)])
+def test_fp8_f32s_fused_quant_is_bit_identical(M, N, K, pad):
+    """gemm_fp8_f32s_x (act_quant_fp8_f32s fused into the GEMV, M <= 16) against the two calls it replaces: the same
+    bf16 outputs bit for bit, also with a row stride wider than K and a ragged N; and past 16 rows it refuses."""
+    rng = np.random.default_rng(7 * M + N)
+    ldx = K + pad
+    x = randn_bf16(rng, (M, ldx))
+    x[:, 0:128] = 0  # an all-zero block: the 1e-4 amax floor
+    x[0, 130] = np.uint16(0x4480)  # 1024.0: a block whose scale a single value sets
+    wq, ws, _ = _weights_f32s(rng, N, K)
+    dx, dwq, dws = dev(x), dev(wq), dev(ws)
+    q, sa = DeviceBuffer(M * K), DeviceBuffer(M * (K // 128) * 4)
+    call("uh_act_quant_fp8_f32s", dx, ldx, q, sa, M, K, 128, None)
+    c_ref = DeviceBuffer(M * N * 2)
+    call("uh_gemm_fp8_f32s", q, sa, dwq, dws, c_ref, N, M, N, K, None)
+    c = DeviceBuffer(M * N * 2)
+    call("uh_gemm_fp8_f32s_x", dx, ldx, dwq, dws, c, N, M, N, K, None)
+    got, ref = c.download((M, N), np.uint16), c_ref.download((M, N), np.uint16)
+    print(f"fp8 f32s fused M={M} N={N} K={K}: bit-identical fraction {np.mean(got == ref):.6f}")
+    assert np.array_equal(got, ref)
+    with pytest.raises(Exception, match="M <= 16"):
+        call("uh_gemm_fp8_f32s_x", dx, ldx, dwq, dws, c, N, 17, N, K, None)
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (8, 1024, 512), (33, 256, 1024), (200, 512, 512), (17, 200, 640), (1000, 768, 1024)])
 def test_fp8_e8m0_scales(M, N, K):
     """The reference's W8A8 contract (gemm_w8a8 / gemv_w8a8 / gemm_w8a8_wmma): e8m0 scales on both sides."""

@@ -463,6 +463,10 @@ int uh_gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const 
                      int M, int N, int K, void* st) {
   return guard([&] { k::gemm_fp8_f32s(a, sa, w, sw, c, ldc, M, N, K, S(st)); });
 }
+int uh_gemm_fp8_f32s_x(const uint16_t* x, int ldx, const uint8_t* w, const float* sw, uint16_t* c, int ldc, int M,
+                       int N, int K, void* st) {
+  return guard([&] { k::gemm_fp8_f32s_x(x, ldx, w, sw, c, ldc, M, N, K, S(st)); });
+}
 int uh_gemm_a8w4(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, uint16_t* c, int ldc,
                  int M, int N, int K, void* st) {
   return guard([&] { k::gemm_a8w4(a, sa, w, sw, c, ldc, M, N, K, S(st)); });

@@ -254,9 +254,16 @@ __global__ __launch_bounds__(DN_NT) void fp8_skinny_kernel(Fp8GemmArgs a) {
 // summed in wave order through LDS.
 constexpr int FV_WAVES = 8, FV_CHUNK = 4;
 
-template <bool F32S, int MT>
+// XQ: A arrives as bf16 rows (a.xa). The workgroup first quantizes its M rows into LDS as act_quant_fp8_f32s does
+// (s = max(amax, 1e-4) * fp32(1/448), codes e4m3(x / s); 8 values per thread, a block's amax a DPP row max over its
+// 16 threads; all waves, before the K loop, so that a wave with no K blocks still meets the barrier), then reads
+// codes and scales from LDS. Same codes and
+// scales as the separate quantization, so the same results bit for bit, one launch fewer.
+template <bool F32S, int MT, bool XQ = false>
 __global__ __launch_bounds__(64 * FV_WAVES) void fp8_gemv_kernel(Fp8GemmArgs a, Fp8Parts pp) {
+  static_assert(!XQ || (F32S && MT == 1), "the fused quantization: fp32 scales, one row tile");
   __shared__ v4f red[FV_WAVES][MT][64];
+  extern __shared__ __align__(16) uint8_t xq_lds[];  // XQ: codes [M][K], then fp32 scales [M][K / 128]
   int tile = blockIdx.x;
   if (pp.n) {  // column ranges: this workgroup's range (uniform)
     int p = 0;
@@ -278,6 +285,31 @@ __global__ __launch_bounds__(64 * FV_WAVES) void fp8_gemv_kernel(Fp8GemmArgs a, 
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   const int mlive = (M + 15) / 16;  // row tiles with rows (uniform)
+  if constexpr (XQ) {  // every wave: quantize the M rows into LDS before any wave reads them
+    const int nbk = KS * 16, items = M * nbk;  // 8 values per item
+    float* const sl = reinterpret_cast<float*>(xq_lds + size_t(M) * K);
+    for (int base = 0; base < items; base += 64 * FV_WAVES) {  // uniform bound: 16-thread groups stay whole
+      const int it = min(base + tid, items - 1), r = it / nbk, rem = it % nbk, bk = rem >> 4, l = rem & 15;
+      const uint4 raw = *reinterpret_cast<const uint4*>(a.xa + size_t(r) * a.ldx + bk * 128 + 8 * l);
+      const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
+      float v[8], am = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float(rw[i] << 16);
+        v[2 * i + 1] = __uint_as_float(rw[i] & 0xffff0000u);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
+      am = row16_max(am);
+      if (base + tid >= items) continue;
+      const float sc = fmaxf(am, 1e-4f) * (1.0f / 448.0f);
+      uint32_t c0, c1;
+      fp8_codes8(v, sc, c0, c1);
+      *reinterpret_cast<uint2*>(xq_lds + size_t(r) * K + bk * 128 + 8 * l) = make_uint2(c0, c1);
+      if (l == 0) sl[r * KS + bk] = sc;
+    }
+    __syncthreads();
+  }
   for (int kc = b0; kc < b1; kc += FV_CHUNK) {
     // Every load of the chunk is issued before the first use, unconditionally (steps past the range and rows past M
     // are clamped, their products discarded): the weights, the activation rows and the scales, so the chunk waits
@@ -292,17 +324,33 @@ __global__ __launch_bounds__(64 * FV_WAVES) void fp8_gemv_kernel(Fp8GemmArgs a, 
       b[u][0] = *reinterpret_cast<gptr<v4i>>(as_global(wrow + kb * 128));
       b[u][1] = *reinterpret_cast<gptr<v4i>>(as_global(wrow + kb * 128 + 16));
       swv[u] = F32S ? a.sw32[size_t(nb) * KS + kb] : e8m0_to_f32(a.sw8[size_t(nb) * KS + kb]);
+      if constexpr (XQ) {
+        sav[u][0] = 1.0f;
+      } else {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int r = min(mt * 16 + nl, M - 1);
-        const uint8_t* ap = a.a + size_t(r) * K + kb * 128 + g * 32;
-        aq[u][mt][0] = *reinterpret_cast<gptr<v4i>>(as_global(ap));
-        aq[u][mt][1] = *reinterpret_cast<gptr<v4i>>(as_global(ap + 16));
-        sav[u][mt] = F32S ? 1.0f : e8m0_to_f32(a.sa8[size_t(r) * KS + kb]);
+        for (int mt = 0; mt < MT; ++mt) {
+          const int r = min(mt * 16 + nl, M - 1);
+          const uint8_t* ap = a.a + size_t(r) * K + kb * 128 + g * 32;
+          aq[u][mt][0] = *reinterpret_cast<gptr<v4i>>(as_global(ap));
+          aq[u][mt][1] = *reinterpret_cast<gptr<v4i>>(as_global(ap + 16));
+          sav[u][mt] = F32S ? 1.0f : e8m0_to_f32(a.sa8[size_t(r) * KS + kb]);
+        }
+        if constexpr (kRowScales)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sa32v[u][i] = a.sa32[size_t(min(4 * g + i, M - 1)) * KS + kb];
       }
-      if constexpr (kRowScales)
+    }
+    if constexpr (XQ) {  // codes and C rows' scales from the LDS copy
+      const float* const sl = reinterpret_cast<const float*>(xq_lds + size_t(M) * K);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sa32v[u][i] = a.sa32[size_t(min(4 * g + i, M - 1)) * KS + kb];
+      for (int u = 0; u < FV_CHUNK; ++u) {
+        const int kb = min(kc + u, b1 - 1);
+        const uint8_t* ap = xq_lds + size_t(min(nl, M - 1)) * K + kb * 128 + g * 32;
+        aq[u][0][0] = *reinterpret_cast<const v4i*>(ap);
+        aq[u][0][1] = *reinterpret_cast<const v4i*>(ap + 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sa32v[u][i] = sl[min(4 * g + i, M - 1) * KS + kb];
+      }
     }
 #pragma unroll
     for (int u = 0; u < FV_CHUNK; ++u) {
@@ -359,6 +407,15 @@ __global__ __launch_bounds__(64 * FV_WAVES) void fp8_gemv_kernel(Fp8GemmArgs a, 
         if (r < M) a.c[size_t(r) * a.ldc + n0 + nl] = f32_to_bf16(s[i]);
       }
   }
+}
+
+void launch_fp8_gemv_xq(const Fp8GemmArgs& a, hipStream_t st) {
+  const size_t lds = size_t(a.M) * a.K + size_t(a.M) * (a.K / 128) * 4;
+  auto* kern = &fp8_gemv_kernel<true, 1, true>;
+  UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               int(lds)));
+  kern<<<dim3(unsigned(cdiv(size_t(a.N), 16))), 64 * FV_WAVES, lds, st>>>(a, Fp8Parts{});
+  UH_CHECK_LAUNCH();
 }
 
 template <bool F32S>
@@ -476,6 +533,27 @@ void gemv_w8a8(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint
   g.N = N;
   g.K = K;
   launch_fp8_gemm(g, st);
+}
+void gemm_fp8_f32s_x(const bf16* x, int ldx, const uint8_t* w, const float* sw, bf16* c, int ldc, int M, int N,
+                     int K, hipStream_t st) {
+  if (M <= 0) return;
+  if (M > 16) throw std::runtime_error("gemm_fp8_f32s_x: M <= 16");
+  if (K % 128 || K <= 0 || N <= 0) throw std::runtime_error("gemm_fp8_f32s_x: K % 128");
+  if (!x || !w || !sw || !c) throw std::runtime_error("gemm_fp8_f32s_x: null operand");
+  if (ldx < K || ldx % 8 || reinterpret_cast<uintptr_t>(x) % 16) throw std::runtime_error("gemm_fp8_f32s_x: x rows");
+  if (ldc < N) throw std::runtime_error("gemm_fp8_f32s_x: ldc < N");
+  if (size_t(M) * K * (1 + 4.0 / 128) > 128 * 1024) throw std::runtime_error("gemm_fp8_f32s_x: M * K > 126 KiB");
+  Fp8GemmArgs g{};
+  g.xa = x;
+  g.ldx = ldx;
+  g.w = w;
+  g.sw32 = sw;
+  g.c = c;
+  g.ldc = ldc;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  launch_fp8_gemv_xq(g, st);
 }
 void gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw, bf16* c, int ldc, int M,
                    int N, int K, hipStream_t st) {

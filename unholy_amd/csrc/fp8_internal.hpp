@@ -19,6 +19,8 @@ struct Fp8GemmArgs {
   uint16_t* c;
   int ldc, M, N, K;
   int rows_cap;
+  const uint16_t* xa = nullptr;  // raw bf16 activations [M, ldx] quantized in the GEMV (fp32 scales, M <= 16)
+  int ldx = 0;
 };
 
 // Up to three column ranges on one input (gemv_w8a8_parts): range i has its own weights, e8m0 scales, output, ldc
