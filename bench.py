@@ -2,7 +2,7 @@
 """Benchmark of the MXFP4 routed-expert FFN on one MI355X (gfx950).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
-    python bench.py --only {decode,single,verify,prefill,fp8,copy}   # one workload (for profilers), one JSON line
+    python bench.py --only {decode,single,verify,prefill,fp8,grouped,copy}   # one workload (for profilers), one JSON line
 
 A step is one routed-expert FFN over one batch of synthetic tokens: softmax top-6 routing of [T, 256] logits,
 dispatch, fp8 input transform, w1/w3 grouped GEMV with the SwiGLU epilogue, w2 grouped GEMV, combine to bf16
@@ -36,6 +36,7 @@ HBM_PEAK_GBS = 8000.0
 # rocprofv3 --pmc runs, scaled by the same counters on a 1 GiB device copy (profiles/hbm_traffic_pmc.md).
 GEMV_TRAFFIC_BYTES = 398.9e6
 BF16_PEAK_TFLOPS = 2500.0
+GW_G, GW_R, GW_K = 8, 1024, 4096  # the DSV4 wo_a shape (o_groups, o_lora_rank, heads x head_dim / o_groups)
 FP8_PEAK_TFLOPS = 5000.0  # the block-scaled fp8 x fp4 MFMA runs at the fp8 rate (4.29 PFLOP/s sustained, measured)
 
 
@@ -205,6 +206,39 @@ def bench_fp8_dense(M, steps, warmup, rng, copies, fused=True):
     return time_graph(fn, steps, warmup, per_graph=copies)
 
 
+def bench_grouped_fp8w(M, steps, warmup, rng, copies):
+    """The reference's wo_a projection (forward_ref.hip:1012-1022), grouped "mgk,grk->mgr" at the DSV4 shape: a bf16
+    [M, 8, 4096], w e4m3 [8 x 1024, 4096] (32 MiB) with 128 x 128 e8m0 scales, c bf16 [M, 8, 1024]; through
+    uh_gemm_grouped_fp8w_wmma (the GEMV for M <= 32, the tiled MFMA GEMM above), rotating over `copies` weight copies
+    so that they are read from HBM."""
+    from unholy_amd import call
+    from unholy_amd.device import DeviceBuffer
+    G, R, K = GW_G, GW_R, GW_K
+    wq = [DeviceBuffer(G * R * K) for _ in range(copies)]
+    for i, c in enumerate(wq):
+        call("uh_fill_random_bytes", c, G * R * K, 100 + i, 0, 126, None)  # finite e4m3 codes
+    sw = DeviceBuffer.from_array(rng.integers(118, 126, (G * R // 128, K // 128), dtype=np.uint8))
+    a = DeviceBuffer.from_array(to_bf16(rng.standard_normal((M, G, K), dtype=np.float32)))
+    c = DeviceBuffer(M * G * R * 2)
+
+    def fn(i, stream):
+        call("uh_gemm_grouped_fp8w_wmma", a, wq[i % copies], sw, c, M, G, R, K, stream.handle)
+
+    return time_graph(fn, steps, warmup, per_graph=copies)
+
+
+def grouped_entry(M, ms):
+    G, R, K = GW_G, GW_R, GW_K
+    wbytes = G * R * K + (G * R // 128) * (K // 128)
+    e = {"ms": ms, "tokens_per_s": M / (ms * 1e-3), "TFLOPs": 2 * M * G * R * K / (ms * 1e-3) / 1e12,
+         "GBps_weights": wbytes / (ms * 1e-3) / 1e9}
+    if M <= 32:
+        e["frac_hbm_peak"] = e["GBps_weights"] / HBM_PEAK_GBS
+    else:
+        e["frac_bf16_mfma_peak"] = e["TFLOPs"] / BF16_PEAK_TFLOPS
+    return e
+
+
 def cpu_baseline(seconds=10.0, max_reps=5):
     """The CPU oracle (reference arithmetic, oracle/uh_oracle.cpp) on one decode step of the headline workload:
     T = 8 tokens, softmax top-6 over 256 experts; host weights are generated for the experts the step touches only
@@ -246,6 +280,9 @@ def run_only(name, args, rng):
             call("uh_memcpy_d2d", dst, src, n, None)
         synchronize()
         return {"workload": "copy", "bytes_per_copy": n, "copies": 4}
+    if name == "grouped":
+        return {f"grouped_fp8w_M{M}": bench_grouped_fp8w(M, 100 if M < 4096 else 10, 10 if M < 4096 else 2, rng, c)
+                for M, c in ((1, 16), (64, 16), (4096, 2))}
     if name == "fp8":
         return {f"fp8_dense_M{M}": bench_fp8_dense(M, 100 if M < 4096 else 10, 10 if M < 4096 else 2, rng, c)
                 for M, c in ((1, 64), (64, 64), (4096, 4))}
@@ -269,7 +306,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "single", "verify", "prefill", "fp8", "copy"])
+    ap.add_argument("--only", choices=["decode", "single", "verify", "prefill", "fp8", "grouped", "copy"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the MoE expert path runs on a single MI355X in this build "
@@ -348,6 +385,9 @@ def main():
             if M <= 16:  # the two-call form (act_quant_fp8_f32s, then gemm_fp8_f32s) beside the fused one
                 wl[f"fp8_dense_M{M} (configs[4])"]["ms_two_launches"] = bench_fp8_dense(M, 100, 10, rng, copies,
                                                                                          fused=False)
+        for M, copies in ((1, 16), (64, 16), (4096, 2)):
+            t = bench_grouped_fp8w(M, 100 if M < 4096 else 10, 10 if M < 4096 else 2, rng, copies)
+            wl[f"grouped_fp8w_wo_a_M{M}"] = grouped_entry(M, t)
         result["workloads"] = wl
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()

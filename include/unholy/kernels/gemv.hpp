@@ -23,6 +23,11 @@ struct GemvQuant {
   uint8_t* qs = nullptr;
   uint32_t* counters = nullptr;
 };
+// Ref gemv.hpp:36-37: the grouped fp8-weight GEMV ("mgk,grk->mgr", as gemm_grouped_fp8w_wmma), M <= 32,
+// K % 128 == 0; gq.q set: act_quant_fp8 (block 128) of the outputs c [M, G R] into gq.q / gq.qs ((G R) % 128 == 0;
+// a second launch here, gq.counters never touched).
+void gemv_grouped_fp8w(const bf16* a, const uint8_t* w, const uint8_t* sw, bf16* c, int M, int G, int R, int K,
+                       hipStream_t st, const GemvQuant& gq = {});
 // Ref gemv.hpp:40-49: a column range on the shared input: weights (e4m3 [N, K]), e8m0 scales [ceil(N/128), K/128],
 // bf16 output [M, ldc], width N.
 struct GemvPart {

@@ -30,6 +30,10 @@ void gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const fl
 // the same results bit for bit in one launch (for decode rows). ldx % 8 == 0, x 16-byte aligned.
 void gemm_fp8_f32s_x(const bf16* x, int ldx, const uint8_t* w, const float* sw, bf16* c, int ldc, int M, int N,
                      int K, hipStream_t st);
+// Grouped "mgk,grk->mgr" with fp8 weights dequantized by 128x128 e8m0 block scales, in the reference's order (one
+// fp32 fmaf chain over k per output). Ref ref.hpp:42-45. K % 128 == 0.
+void gemm_grouped_fp8w(const bf16* a, const uint8_t* w, const uint8_t* sw, bf16* c, int M, int G, int R, int K,
+                       hipStream_t st);
 // fp8 activations x e2m1 weights [N, K/2] (row-major or the tile-major layout). Ref ref.hpp:139-143.
 void gemm_a8w4(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, bf16* c, int ldc, int M,
                int N, int K, hipStream_t st);

@@ -203,6 +203,16 @@ int uh_gemv_w8a8_glu(const uint8_t* a, const uint8_t* sa, const uint8_t* w_gate,
 /* kernel.py fp8_gemm with fp32 scales (scale_fmt=None); gemm_wmma.hip:89-100's fold */
 int uh_gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw, uint16_t* c, int ldc,
                      int M, int N, int K, void* stream);
+/* ref.hpp:42-45 (reference order), gemm_wmma.hpp:24-26 (fast path), gemv.hpp:36-37 (GEMV, M <= 32): grouped
+ * "mgk,grk->mgr" with fp8 weights x 128x128 e8m0 scales. a bf16 [M, G, K], w e4m3 [G R, K],
+ * sw [ceil(G R / 128), K / 128], c bf16 [M, G, R]; K % 128 == 0. uh_gemv_grouped_fp8w with q set also writes
+ * act_quant_fp8 (block 128) of c into q [M, G R] / qs [M, G R / 128] ((G R) % 128 == 0; counters may be NULL). */
+int uh_gemm_grouped_fp8w(const uint16_t* a, const uint8_t* w, const uint8_t* sw, uint16_t* c, int M, int G, int R,
+                         int K, void* stream);
+int uh_gemm_grouped_fp8w_wmma(const uint16_t* a, const uint8_t* w, const uint8_t* sw, uint16_t* c, int M, int G,
+                              int R, int K, void* stream);
+int uh_gemv_grouped_fp8w(const uint16_t* a, const uint8_t* w, const uint8_t* sw, uint16_t* c, int M, int G, int R,
+                         int K, uint8_t* q, uint8_t* qs, uint32_t* counters, void* stream);
 /* No reference counterpart: uh_act_quant_fp8_f32s (block 128) of bf16 x [M, ldx] fused into uh_gemm_fp8_f32s for
  * M <= 16 (decode rows): the same results bit for bit, one launch. */
 int uh_gemm_fp8_f32s_x(const uint16_t* x, int ldx, const uint8_t* w, const float* sw, uint16_t* c, int ldc, int M,

@@ -40,6 +40,8 @@ _SIGS = {
     "or_gemm_a8w4_f64": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I]),
     "or_gemm_w8a8": (None, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]),
     "or_gemm_w8a8_f64": (None, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]),
+    "or_gemm_grouped_fp8w": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I]),
+    "or_gemm_grouped_fp8w_f64": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I]),
     "or_swiglu": (None, [_P, _P, _P, _P, _I, _I, _F]),
     "or_route_ds": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P, _I]),
     "or_route_glm": (None, [_P, _P, _P, _P, _I, _I, _I, _F]),
@@ -231,6 +233,29 @@ def gemm_w8a8_f64(a, sa, w, sw, threads=8):
         lib().or_gemm_w8a8_f64(_p(a), None, _p(sa), _p(w), None, _p(sw), _p(c), N, M, N, K, threads)
     else:
         lib().or_gemm_w8a8_f64(_p(a), _p(sa), None, _p(w), _p(sw), None, _p(c), N, M, N, K, threads)
+    return c
+
+
+def gemm_grouped_fp8w(a, w, sw, G, R, threads=8):
+    """a bf16 (uint16) [M, G, K]; w e4m3 [G R, K]; sw e8m0 [ceil(G R / 128), K / 128]. Returns (bf16, fp32) [M, G, R]."""
+    a = _c(a, np.uint16)
+    w = _c(w, np.uint8)
+    sw = _c(sw, np.uint8)
+    M, K = a.shape[0], w.shape[1]
+    assert a.shape == (M, G, K) and w.shape[0] == G * R
+    c16 = np.empty((M, G, R), np.uint16)
+    c32 = np.empty((M, G, R), np.float32)
+    lib().or_gemm_grouped_fp8w(_p(a), _p(w), _p(sw), _p(c16), _p(c32), M, G, R, K, threads)
+    return c16, c32
+
+
+def gemm_grouped_fp8w_f64(a, w, sw, G, R, threads=8):
+    a = _c(a, np.uint16)
+    w = _c(w, np.uint8)
+    sw = _c(sw, np.uint8)
+    M, K = a.shape[0], w.shape[1]
+    c = np.empty((M, G, R), np.float64)
+    lib().or_gemm_grouped_fp8w_f64(_p(a), _p(w), _p(sw), _p(c), M, G, R, K, threads)
     return c
 
 

@@ -12,6 +12,8 @@
 //   gemm_a8w4(_tiled)   src/kernels/ref_gemm.hip:15-67 (K-block partial sums), :77-99, :138-155, :180-188
 //   gemm_w8a8           src/kernels/ref_gemm.hip:130-137, :175-178; fp32-scale form: gemm_wmma.hip:89-100
 //                       (raw per-128 chain folded with acc += raw * (sa * sw))
+//   gemm_grouped_fp8w   src/kernels/ref_gemm.hip:111-125, :198-202 with gemm_ref_kernel :18-67 at G = K (one
+//                       K-block: a single fp32 fmaf chain over k in order, scale 1): "mgk,grk->mgr"
 //   swiglu              src/kernels/ref_moe.hip:62-74
 //   route (DSV4)        src/kernels/ref_moe.hip:14-60
 //   route (GLM sigmoid) src/kernels/moe_dispatch.hip:308-356
@@ -297,6 +299,41 @@ void or_gemm_w8a8_f64(const uint8_t* a, const uint8_t* sa, const float* sa32, co
         acc += part * sc;
       }
       c[size_t(m) * ldc + n] = acc;
+    }
+  });
+}
+
+// gemm_grouped_fp8w: c[m][g][r] = bf16(fmaf chain over k of bf16 a[m][g][k] * (e4m3 w[g R + r][k] * e8m0
+// sw[(g R + r) / 128][k / 128])), the weight product exact in fp32 (ref_gemm.hip:116-125; gemm_ref_kernel at G = K).
+void or_gemm_grouped_fp8w(const uint16_t* a, const uint8_t* w, const uint8_t* sw, uint16_t* c16, float* c32, int M,
+                          int G, int R, int K, int nthreads) {
+  const int kbs = K / 128;
+  parallel_for(G * R, nthreads, [&](int n) {
+    const int g = n / R;
+    std::vector<float> wv(static_cast<size_t>(K));
+    for (int k = 0; k < K; ++k)
+      wv[size_t(k)] = e4m3_to_f32(w[size_t(n) * K + k]) * e8m0_to_f32(sw[size_t(n / 128) * kbs + k / 128]);
+    for (int m = 0; m < M; ++m) {
+      const uint16_t* am = a + (size_t(m) * G + g) * K;
+      float acc = 0.0f;
+      for (int k = 0; k < K; ++k) acc = std::fma(bf16_to_f32(am[k]), wv[size_t(k)], acc);
+      if (c16) c16[size_t(m) * G * R + n] = f32_to_bf16(acc);
+      if (c32) c32[size_t(m) * G * R + n] = acc;
+    }
+  });
+}
+void or_gemm_grouped_fp8w_f64(const uint16_t* a, const uint8_t* w, const uint8_t* sw, double* c, int M, int G, int R,
+                              int K, int nthreads) {
+  const int kbs = K / 128;
+  parallel_for(G * R, nthreads, [&](int n) {
+    const int g = n / R;
+    for (int m = 0; m < M; ++m) {
+      const uint16_t* am = a + (size_t(m) * G + g) * K;
+      double acc = 0.0;
+      for (int k = 0; k < K; ++k)
+        acc += double(bf16_to_f32(am[k])) * double(e4m3_to_f32(w[size_t(n) * K + k])) *
+               double(e8m0_to_f32(sw[size_t(n / 128) * kbs + k / 128]));
+      c[size_t(m) * G * R + n] = acc;
     }
   });
 }

@@ -229,6 +229,26 @@ def test_gemm_w8a8_brute_force(f32):
     assert np.allclose(oracle.gemm_w8a8_f64(q, sa, wq, sw), exact, rtol=1e-12, atol=1e-12 * np.abs(exact).max())
 
 
+def test_gemm_grouped_fp8w_brute_force():
+    """The grouped fp8-weight GEMM against numpy in fp64 from the formats' closed forms: group g of row m meets
+    weight rows g R .. g R + R - 1, each scaled by its 128 x 128 block's e8m0 (a block straddling two groups when
+    R % 128 != 0); the reference-order fp32 chain within fp32 rounding of the exact sums, its bf16 the RNE of it."""
+    rng = np.random.default_rng(11)
+    for M, G, R, K in ((3, 3, 200, 256), (2, 1, 128, 384), (1, 4, 64, 128)):
+        a = randn_bf16(rng, (M, G, K))
+        w = rng.integers(0, 256, (G * R, K), dtype=np.uint8)
+        w[(w & 0x7F) == 0x7F] = 0
+        sw = rng.integers(118, 130, ((G * R + 127) // 128, K // 128), dtype=np.uint8)
+        wv = np.vectorize(e4m3_closed)(w) * np.repeat(np.repeat(2.0 ** (sw.astype(int) - 127), 128, axis=0),
+                                                      128, axis=1)[:G * R]
+        exact = np.einsum("mgk,grk->mgr", from_bf16(a).astype(np.float64), wv.reshape(G, R, K))
+        c16, c32 = oracle.gemm_grouped_fp8w(a, w, sw, G, R)
+        assert np.max(np.abs(c32 - exact)) <= 2e-6 * np.max(np.abs(exact))
+        assert np.array_equal(c16, to_bf16(c32))
+        c64 = oracle.gemm_grouped_fp8w_f64(a, w, sw, G, R)
+        assert np.allclose(c64, exact, rtol=1e-12, atol=1e-12 * np.abs(exact).max())
+
+
 # ---- MoE pieces ------------------------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("limit", [10.0, 0.0])
 def test_swiglu_closed_form(limit):

@@ -463,6 +463,18 @@ int uh_gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const 
                      int M, int N, int K, void* st) {
   return guard([&] { k::gemm_fp8_f32s(a, sa, w, sw, c, ldc, M, N, K, S(st)); });
 }
+int uh_gemm_grouped_fp8w(const uint16_t* a, const uint8_t* w, const uint8_t* sw, uint16_t* c, int M, int G, int R,
+                         int K, void* st) {
+  return guard([&] { k::gemm_grouped_fp8w(a, w, sw, c, M, G, R, K, S(st)); });
+}
+int uh_gemm_grouped_fp8w_wmma(const uint16_t* a, const uint8_t* w, const uint8_t* sw, uint16_t* c, int M, int G,
+                              int R, int K, void* st) {
+  return guard([&] { k::gemm_grouped_fp8w_wmma(a, w, sw, c, M, G, R, K, S(st)); });
+}
+int uh_gemv_grouped_fp8w(const uint16_t* a, const uint8_t* w, const uint8_t* sw, uint16_t* c, int M, int G, int R,
+                         int K, uint8_t* q, uint8_t* qs, uint32_t* counters, void* st) {
+  return guard([&] { k::gemv_grouped_fp8w(a, w, sw, c, M, G, R, K, S(st), k::GemvQuant{q, qs, counters}); });
+}
 int uh_gemm_fp8_f32s_x(const uint16_t* x, int ldx, const uint8_t* w, const float* sw, uint16_t* c, int ldc, int M,
                        int N, int K, void* st) {
   return guard([&] { k::gemm_fp8_f32s_x(x, ldx, w, sw, c, ldc, M, N, K, S(st)); });

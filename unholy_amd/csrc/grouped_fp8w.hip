@@ -1,0 +1,319 @@
+// Grouped GEMM with fp8 weights, "mgk,grk->mgr": c[m][g][r] = bf16(sum_k a[m][g][k] * (e4m3 w[g R + r][k] *
+// e8m0 sw[(g R + r) / 128][k / 128])). a bf16 [M, G, K], w e4m3 [G R, K], sw [ceil(G R / 128), K / 128],
+// c bf16 [M, G, R]. The reference's wo_a projection (src/model/forward_ref.hip:1012-1022, dense_grouped_fp8w
+// :577-582): the weights dequantize exactly to bf16 (an e4m3 value times a power of two), so every product is exact
+// and only the fp32 summation order separates the kernels.
+//
+// Three entry points, as the reference has them:
+//   gemm_grouped_fp8w       the reference order (ref_gemm.hip:116-125, :198-202 at G = K: one fp32 fmaf chain over k
+//                           in order), a thread per output: bit-exact against the CPU oracle, not a fast path;
+//   gemm_grouped_fp8w_wmma  the fast path: the GEMV below for M <= 160, else the tiled MFMA GEMM;
+//   gemv_grouped_fp8w       the GEMV (M <= 32), optionally followed by act_quant_fp8 of its outputs (GemvQuant).
+//
+// GEMV (bound: HBM, 32 MB of weights at the DSV4 shape G = 8, R = 1024, K = 4096): a workgroup per 16-column tile,
+// its 8 waves splitting K in 128-input blocks, every load of a chunk issued before its first use; bf16 MFMA
+// 16x16x32 on the activations as they are and the weights dequantized with the block scale folded in; the 8
+// partial tiles added in LDS in wave order.
+// GEMM (bound: MFMA at M = 4096): 128-row tiles of one group, 4 waves, 64-input stages in an LDS ring filled by direct
+// global -> LDS loads (two workgroups per CU); bf16 MFMA 32x32x16. A wave's columns lie in one 128-row weight block
+// and a stage in one 128-input block, so the weight scale is one value per stage, folded into the dequantization.
+#include <stdexcept>
+#include <string>
+
+#include "common.hpp"
+#include "numerics.hpp"
+#include "pipe.hpp"
+#include "unholy/kernels/gemm_wmma.hpp"
+#include "unholy/kernels/gemv.hpp"
+#include "unholy/kernels/ref.hpp"
+
+namespace unholy::kernels {
+
+using namespace uh;
+using namespace pipe;
+
+namespace {
+
+// ---- reference order ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void grouped_fp8w_ref_kernel(const bf16* a, const uint8_t* w, const uint8_t* sw,
+                                                               bf16* c, int M, int G, int R, int K) {
+  const int n = blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
+  if (n >= G * R) return;
+  const int g = n / R, kbs = K / 128;
+  const bf16* am = a + (size_t(m) * G + g) * K;
+  const uint8_t* wn = w + size_t(n) * K;
+  float acc = 0.0f;
+  for (int k = 0; k < K; ++k)
+    acc = fmaf(bf16_to_f32(am[k]), e4m3_to_f32(wn[k]) * e8m0_to_f32(sw[size_t(n / 128) * kbs + k / 128]), acc);
+  c[size_t(m) * G * R + n] = f32_to_bf16(acc);
+}
+
+// ---- GEMV ------------------------------------------------------------------------------------------------------------
+constexpr int GV_W = 8, GV_CHUNK = 4;
+
+// Workgroup (blockIdx.x, blockIdx.y) = 16 columns x row chunk blockIdx.y of 16 MT rows: several chunks when M is
+// above 16 MT (each chunk re-reads the tile's weights, from the Infinity Cache when the chunks run close together).
+template <int MT>
+__global__ __launch_bounds__(64 * GV_W) void grouped_fp8w_gemv_kernel(const bf16* a, const uint8_t* w,
+                                                                      const uint8_t* sw, bf16* c, int M, int G, int R,
+                                                                      int K) {
+  __shared__ v4f red[GV_W][MT][64];
+  const int KS = K / 128, N = G * R;
+  a += size_t(blockIdx.y) * 16 * MT * G * K;
+  c += size_t(blockIdx.y) * 16 * MT * N;
+  M = min(16 * MT, M - int(blockIdx.y) * 16 * MT);
+  const int tid = threadIdx.x, lane = tid & 63, nl = lane & 15, q4 = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n0 = blockIdx.x * 16, n = n0 + nl, grp = n0 / R;  // R % 16 == 0: the tile lies in one group
+  const int per = (KS + GV_W - 1) / GV_W, b0 = min(KS, wave * per), b1 = min(KS, b0 + per);
+  const uint8_t* wrow = w + size_t(n) * K + q4 * 32;
+  const uint8_t* swrow = sw + size_t(n0 / 128) * KS;  // a 16-column tile lies in one 128-row block
+  v4f acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int kc = b0; kc < b1; kc += GV_CHUNK) {
+    // Lane (nl, q4) holds inputs 32 q4 .. 32 q4 + 31 of each 128-input block: 32 codes of column n and 32 bf16 of
+    // row nl (rows past M clamped, their products discarded).
+    v4i b[GV_CHUNK][2], x[GV_CHUNK][MT][4];
+    float swv[GV_CHUNK];
+#pragma unroll
+    for (int u = 0; u < GV_CHUNK; ++u) {
+      const int kb = min(kc + u, b1 - 1);
+      b[u][0] = *reinterpret_cast<gptr<v4i>>(as_global(wrow + kb * 128));
+      b[u][1] = *reinterpret_cast<gptr<v4i>>(as_global(wrow + kb * 128 + 16));
+      swv[u] = e8m0_to_f32(swrow[kb]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const bf16* ap = a + (size_t(min(mt * 16 + nl, M - 1)) * G + grp) * K + kb * 128 + q4 * 32;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[u][mt][i] = *reinterpret_cast<gptr<v4i>>(as_global(ap + 8 * i));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < GV_CHUNK; ++u) {
+      if (kc + u >= b1) break;
+      bf16x8 bf[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        bf[t] = fp8x8_to_bf16(uint32_t(b[u][t / 2][2 * (t % 2)]), uint32_t(b[u][t / 2][2 * (t % 2) + 1]), swv[u]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if (mt * 16 >= M) break;
+        const bool live = mt * 16 + nl < M;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const bf16x8 af = live ? __builtin_bit_cast(bf16x8, x[u][mt][t]) : bf16x8{};
+          acc[mt] = mfma_bf16(af, bf[t], acc[mt]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) red[wave][mt][lane] = acc[mt];
+  __syncthreads();
+  // Wave w < MT stores row tile w: the sum of the 8 partials in wave order.
+  if (wave < MT && wave * 16 < M) {
+    v4f s = red[0][wave][lane];
+#pragma unroll
+    for (int v = 1; v < GV_W; ++v) s += red[v][wave][lane];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = wave * 16 + 4 * q4 + i;
+      if (r < M) c[size_t(r) * N + n] = f32_to_bf16(s[i]);
+    }
+  }
+}
+
+// ---- tiled GEMM ------------------------------------------------------------------------------------------------------
+// Tile 128 rows x TN columns of one group, 4 waves of 64 rows x TN / 2 columns (TN / 64 MFMA blocks of 32 x 32 across
+// each wave's columns), 64-input stages. TN 256 (R % 256 == 0): 2 slots of 32 KB, 32 MFMAs per wave per stage; TN 128:
+// 3 slots of 24 KB, 16 MFMAs per stage. Either way under 80 KB of LDS, two workgroups per CU.
+template <int TN>
+struct GroupedTile {
+  static constexpr int A = 128 * 128, B = TN * 64, STAGE = A + B, S = TN == 256 ? 2 : 3, RING = S * STAGE;
+  static constexpr int CB = TN / 64, OPS = 4 + TN / 64;  // MFMA column blocks per wave; direct loads per wave per stage
+  static constexpr int LDC = TN + 8;
+  static constexpr size_t lds() { return RING > 128 * LDC * 2 ? size_t(RING) : size_t(128) * LDC * 2; }
+};
+
+// XOR swizzle of a 64-byte row (4 pieces of 16 bytes): an operand read's pass covers 16 consecutive rows starting at
+// a multiple of 16 at one piece, and (n % 4) * 4 + (p ^ ((n >> 2) & 3)) modulo 16 differs across them, so the pass
+// touches each of the 64 banks once.
+__device__ __forceinline__ int swz64(int n) { return (n >> 2) & 3; }
+
+template <int TN>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void grouped_fp8w_tiled_kernel(
+    const bf16* a, const uint8_t* w, const uint8_t* sw, bf16* c, int M, int G, int R, int K) {
+  using T = GroupedTile<TN>;
+  extern __shared__ __align__(16) uint8_t smem[];
+  int bx, by;
+  tile_block(gridDim.x, bx, by);
+  const int row0 = by * 128;
+  if (row0 >= M) return;  // padding of the grid's row-tile count
+  const int KS = K / 64, N = G * R, Mt = min(128, M - row0), col0 = bx * TN, grp = col0 / R;
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rh = wave & 1, ch = wave >> 1;
+  const uint32_t lds0 = lds_addr(smem);
+  // Per-lane load offsets (bytes; constant over the stages). A: 128-byte row pieces (64 bf16 of a stage) of row r
+  // of the group, rows past the tile repeating its last; B: 64-byte row pieces of weight row col0 + n.
+  uint32_t aoff[4], boff[T::CB];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int slot = (wave * 4 + i) * 64 + lane, r = slot >> 3, p = (slot & 7) ^ lds_swz(r);
+    aoff[i] = uint32_t(min(r, Mt - 1) * G + grp) * uint32_t(2 * K) + uint32_t(p * 16);
+  }
+#pragma unroll
+  for (int i = 0; i < T::CB; ++i) {
+    const int slot = (wave * T::CB + i) * 64 + lane, n = slot >> 2, p = (slot & 3) ^ swz64(n);
+    boff[i] = uint32_t(n) * uint32_t(K) + uint32_t(p * 16);
+  }
+  const uint8_t* abase = reinterpret_cast<const uint8_t*>(a + size_t(row0) * G * K);
+  const uint8_t* wbase = w + size_t(col0) * K;
+  // The wave's TN / 2 columns lie in one 128-row weight block: one scale per stage.
+  const uint8_t* swrow = sw + size_t((col0 + ch * (TN / 2)) / 128) * (K / 128);
+  const auto issue = [&](int s) {
+    const uint32_t st = lds0 + uint32_t((s % T::S) * T::STAGE);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma16(abase + s * 128, aoff[i], st + uint32_t(wave * 4 + i) * 1024);
+#pragma unroll
+    for (int i = 0; i < T::CB; ++i) dma16(wbase + s * 64, boff[i], st + uint32_t(T::A + (wave * T::CB + i) * 1024));
+  };
+  for (int j = 0; j < T::S - 1 && j < KS; ++j) issue(j);
+
+  const int rb_live = __builtin_amdgcn_readfirstlane(min(2, max(0, (Mt - rh * 64 + 31) / 32)));
+  v16f_t acc[2][T::CB];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < T::CB; ++cb) acc[rb][cb] = v16f_t{};
+
+  for (int s = 0; s < KS; ++s) {
+    // This wave's part of stage s has landed when at most its loads of the later stages issued (S - 2 at most) are
+    // pending.
+    if (T::S == 3 && s + 1 < KS) wait_vm<T::OPS>();
+    else wait_vm<0>();
+    __syncthreads();  // every wave's part has landed; slot (s - 1) % S is free
+    if (s + T::S - 1 < KS) issue(s + T::S - 1);
+    const uint8_t* stb = smem + (s % T::S) * T::STAGE;
+    const float swv = e8m0_to_f32(swrow[s >> 1]);
+    // MFMA step t (16 inputs): lane half h supplies inputs 32 h + 8 t .. + 7 of the stage, on both sides.
+    v4i bq[T::CB][2];
+#pragma unroll
+    for (int cb = 0; cb < T::CB; ++cb) {
+      const int n = ch * (TN / 2) + cb * 32 + l32;
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+        bq[cb][x] = *reinterpret_cast<const v4i*>(stb + T::A + (n * 4 + ((2 * h + x) ^ swz64(n))) * 16);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      bf16x8 bf[T::CB];
+#pragma unroll
+      for (int cb = 0; cb < T::CB; ++cb)
+        bf[cb] = fp8x8_to_bf16(uint32_t(bq[cb][t >> 1][(t & 1) * 2]), uint32_t(bq[cb][t >> 1][(t & 1) * 2 + 1]), swv);
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        if (rb >= rb_live) break;
+        const int r = rh * 64 + rb * 32 + l32;
+        const bf16x8 af =
+            __builtin_bit_cast(bf16x8, *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 * h + t) ^ lds_swz(r))) * 16));
+#pragma unroll
+        for (int cb = 0; cb < T::CB; ++cb) acc[rb][cb] = mfma32_bf16(af, bf[cb], acc[rb][cb]);
+      }
+    }
+  }
+
+  // ---- epilogue through LDS: 128 x TN bf16, then 16-byte row stores
+  __syncthreads();
+  uint16_t* sc = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < T::CB; ++cb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        sc[(rh * 64 + rb * 32 + 8 * (i / 4) + 4 * h + (i % 4)) * T::LDC + ch * (TN / 2) + cb * 32 + l32] =
+            f32_to_bf16(acc[rb][cb][i]);
+  __syncthreads();
+  for (int e = tid; e < Mt * (TN / 8); e += 256) {
+    const int r = e / (TN / 8), c8 = (e % (TN / 8)) * 8;
+    *reinterpret_cast<uint4*>(c + size_t(row0 + r) * N + col0 + c8) = *reinterpret_cast<const uint4*>(sc + r * T::LDC + c8);
+  }
+}
+
+void check_args(const char* name, const bf16* a, const uint8_t* w, const uint8_t* sw, const bf16* c, int M, int G,
+                int R, int K) {
+  if (M < 0 || G <= 0 || R <= 0 || K <= 0 || K % 128) throw std::runtime_error(std::string(name) + ": K % 128");
+  if (!a || !w || !sw || !c) throw std::runtime_error(std::string(name) + ": null operand");
+}
+
+void launch_ref(const bf16* a, const uint8_t* w, const uint8_t* sw, bf16* c, int M, int G, int R, int K,
+                hipStream_t st) {
+  grouped_fp8w_ref_kernel<<<dim3(unsigned(cdiv(size_t(G) * R, 256)), unsigned(M)), 256, 0, st>>>(a, w, sw, c, M, G,
+                                                                                                 R, K);
+  UH_CHECK_LAUNCH();
+}
+
+// The GEMV for up to 160 rows (32-row chunks side by side), the tiled GEMM above: at the DSV4 shape M = 64 ran
+// 69 us tiled (64 workgroups) and 46 us as two chunks; the tiled kernel's workgroup count grows with M.
+constexpr int GV_MAX_ROWS = 160;
+bool gemv_fits(int M, int R) { return M <= GV_MAX_ROWS && R % 16 == 0; }
+void launch_gemv(const bf16* a, const uint8_t* w, const uint8_t* sw, bf16* c, int M, int G, int R, int K,
+                 hipStream_t st) {
+  const unsigned tiles = unsigned(size_t(G) * R / 16);
+  if (M <= 16) grouped_fp8w_gemv_kernel<1><<<dim3(tiles), 64 * GV_W, 0, st>>>(a, w, sw, c, M, G, R, K);
+  else grouped_fp8w_gemv_kernel<2><<<dim3(tiles, unsigned(cdiv(M, 32))), 64 * GV_W, 0, st>>>(a, w, sw, c, M, G, R, K);
+  UH_CHECK_LAUNCH();
+}
+
+// 32-bit DMA offsets: a tile's rows span 128 G K bf16 from its base.
+bool tiled_fits(int G, int R, int K) { return R % 128 == 0 && size_t(128) * G * K * 2 < (size_t(1) << 32); }
+template <int TN>
+void launch_tiled_t(const bf16* a, const uint8_t* w, const uint8_t* sw, bf16* c, int M, int G, int R, int K,
+                    hipStream_t st) {
+  const size_t lds = GroupedTile<TN>::lds();
+  auto* kern = &grouped_fp8w_tiled_kernel<TN>;
+  UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               int(lds)));
+  kern<<<tile_grid(G * R / TN, (M + 127) / 128), 256, lds, st>>>(a, w, sw, c, M, G, R, K);
+  UH_CHECK_LAUNCH();
+}
+void launch_tiled(const bf16* a, const uint8_t* w, const uint8_t* sw, bf16* c, int M, int G, int R, int K,
+                  hipStream_t st) {
+  if (R % 256 == 0) launch_tiled_t<256>(a, w, sw, c, M, G, R, K, st);
+  else launch_tiled_t<128>(a, w, sw, c, M, G, R, K, st);
+}
+
+}  // namespace
+
+void gemm_grouped_fp8w(const bf16* a, const uint8_t* w, const uint8_t* sw, bf16* c, int M, int G, int R, int K,
+                       hipStream_t st) {
+  check_args("gemm_grouped_fp8w", a, w, sw, c, M, G, R, K);
+  if (M == 0) return;
+  launch_ref(a, w, sw, c, M, G, R, K, st);
+}
+
+void gemm_grouped_fp8w_wmma(const bf16* a, const uint8_t* w, const uint8_t* sw, bf16* c, int M, int G, int R, int K,
+                            hipStream_t st) {
+  check_args("gemm_grouped_fp8w_wmma", a, w, sw, c, M, G, R, K);
+  if (M == 0) return;
+  if (gemv_fits(M, R)) launch_gemv(a, w, sw, c, M, G, R, K, st);
+  else if (tiled_fits(G, R, K)) launch_tiled(a, w, sw, c, M, G, R, K, st);
+  else launch_ref(a, w, sw, c, M, G, R, K, st);  // shapes the fast kernels do not tile (R % 128 != 0)
+}
+
+void gemv_grouped_fp8w(const bf16* a, const uint8_t* w, const uint8_t* sw, bf16* c, int M, int G, int R, int K,
+                       hipStream_t st, const GemvQuant& gq) {
+  check_args("gemv_grouped_fp8w", a, w, sw, c, M, G, R, K);
+  if (M > 32) throw std::runtime_error("gemv_grouped_fp8w: M > 32");  // the reference's bound (gemv.hip:653)
+  if (gq.q && (!gq.qs || (size_t(G) * R) % 128)) throw std::runtime_error("gemv_grouped_fp8w: quantization shape");
+  if (M == 0) return;
+  if (gemv_fits(M, R)) launch_gemv(a, w, sw, c, M, G, R, K, st);
+  else launch_ref(a, w, sw, c, M, G, R, K, st);
+  // act_quant_fp8 (block 128) of the bf16 outputs, the values the reference's last blocks quantize (a second launch
+  // here instead of its per-segment counters, which stay zero).
+  if (gq.q) act_quant_fp8(c, G * R, gq.q, gq.qs, M, G * R, 128, st);
+}
+
+}  // namespace unholy::kernels
