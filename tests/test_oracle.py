@@ -13,6 +13,7 @@ GRID_E2M1 = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
 
 
 def e4m3_closed(c):
+    c = int(c)  # numpy uint8 arithmetic would wrap e - 7
     s = -1.0 if c & 0x80 else 1.0
     e, m = (c >> 3) & 15, c & 7
     return s * (m * 2.0 ** -9 if e == 0 else (1 + m / 8) * 2.0 ** (e - 7))
