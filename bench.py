@@ -2,7 +2,7 @@
 """Benchmark of the MXFP4 routed-expert FFN on one MI355X (gfx950).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
-    python bench.py --only {decode,single,verify,prefill,fp8,grouped,copy}   # one workload (for profilers), one JSON line
+    python bench.py --only {decode,single,verify,prefill,fp8,grouped,producers,copy}   # one workload (for profilers), one JSON line
 
 A step is one routed-expert FFN over one batch of synthetic tokens: softmax top-6 routing of [T, 256] logits,
 dispatch, fp8 input transform, w1/w3 grouped GEMV with the SwiGLU epilogue, w2 grouped GEMV, combine to bf16
@@ -227,6 +227,32 @@ def bench_grouped_fp8w(M, steps, warmup, rng, copies):
     return time_graph(fn, steps, warmup, per_graph=copies)
 
 
+def bench_producers(rows, steps, warmup, rng):
+    """The fused activation producers at D = 4096: rmsnorm_quant_slices (rmsnorm + act_quant_fp8 of its output) of
+    `rows` rows, and quant_remote_tokens of `rows` gathered rows (every token remote). Returns ms per call of each."""
+    import ctypes
+    from unholy_amd import call
+    from unholy_amd.device import DeviceBuffer
+    x = DeviceBuffer.from_array(to_bf16(rng.standard_normal((rows, D), dtype=np.float32)))
+    w = DeviceBuffer.from_array(to_bf16(rng.standard_normal(D, dtype=np.float32)))
+    y, q, qs = DeviceBuffer(rows * D * 2), DeviceBuffer(rows * D), DeviceBuffer(rows * D // 128)
+    u2t = DeviceBuffer.from_array(rng.permutation(rows).astype(np.int32))
+    plan = DeviceBuffer.from_array(np.array([6 * rows, 0, 0, 0, rows], np.int32))
+    done = ctypes.c_int(0)
+    t_norm = time_graph(lambda i, st: call("uh_rmsnorm_quant_slices", x, D, w, y, D, q, qs, rows, D, 1e-6,
+                                           ctypes.byref(done), st.handle), steps, warmup)
+    t_rq = time_graph(lambda i, st: call("uh_quant_remote_tokens", x, D, u2t, plan, q, qs, rows, st.handle),
+                      steps, warmup)
+    return t_norm, t_rq
+
+
+def producers_entry(rows, t_norm, t_rq):
+    b_norm = rows * D * (2 + 2 + 1) + rows * D // 128 + D * 2  # x in, y out, codes, scales, weights
+    b_rq = rows * D * (2 + 1) + rows * D // 128
+    return {"rmsnorm_quant_slices": {"ms": t_norm, "GBps": b_norm / (t_norm * 1e-3) / 1e9},
+            "quant_remote_tokens": {"ms": t_rq, "GBps": b_rq / (t_rq * 1e-3) / 1e9}}
+
+
 def grouped_entry(M, ms):
     G, R, K = GW_G, GW_R, GW_K
     wbytes = G * R * K + (G * R // 128) * (K // 128)
@@ -280,6 +306,8 @@ def run_only(name, args, rng):
             call("uh_memcpy_d2d", dst, src, n, None)
         synchronize()
         return {"workload": "copy", "bytes_per_copy": n, "copies": 4}
+    if name == "producers":
+        return {f"producers_rows{r}": producers_entry(r, *bench_producers(r, 64, 16, rng)) for r in (8, 4096)}
     if name == "grouped":
         return {f"grouped_fp8w_M{M}": bench_grouped_fp8w(M, 100 if M < 4096 else 10, 10 if M < 4096 else 2, rng, c)
                 for M, c in ((1, 16), (64, 16), (4096, 2))}
@@ -306,7 +334,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "single", "verify", "prefill", "fp8", "grouped", "copy"])
+    ap.add_argument("--only", choices=["decode", "single", "verify", "prefill", "fp8", "grouped", "producers",
+                                       "copy"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the MoE expert path runs on a single MI355X in this build "
@@ -388,6 +417,8 @@ def main():
         for M, copies in ((1, 16), (64, 16), (4096, 2)):
             t = bench_grouped_fp8w(M, 100 if M < 4096 else 10, 10 if M < 4096 else 2, rng, copies)
             wl[f"grouped_fp8w_wo_a_M{M}"] = grouped_entry(M, t)
+        for r in (8, 4096):
+            wl[f"producers_rows{r}"] = producers_entry(r, *bench_producers(r, 64, 16, rng))
         result["workloads"] = wl
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()

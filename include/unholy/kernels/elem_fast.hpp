@@ -1,0 +1,21 @@
+// The fused rmsnorm -> fp8 producer. Drop-in for rmsnorm_quant_slices and row_slices of the reference's
+// src/kernels/elem_fast.hpp:23-26, 40-41.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace unholy::kernels {
+
+using bf16 = uint16_t;
+
+// Ref elem_fast.hpp:23-26: rmsnorm of rows x [rows, dim] (bf16 weights w [dim], eps) into y [rows, ldy], then, with
+// q, act_quant_fp8 (block 128) of y into q [rows, dim] / qs [rows, dim / 128], in one launch. false (nothing
+// launched) where the reference's is: in place, or slices not whole multiples of 256 values.
+bool rmsnorm_quant_slices(const bf16* x, int ldx, const bf16* w, bf16* y, int ldy, uint8_t* q, uint8_t* qs, int rows,
+                          int dim, float eps, hipStream_t st);
+// Ref elem_fast.hpp:40-41: slices per row so that a launch of `rows` rows has ~64 workgroups, each >= 256 values.
+int row_slices(int rows, int dim);
+
+}  // namespace unholy::kernels

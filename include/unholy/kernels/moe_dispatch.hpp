@@ -84,4 +84,10 @@ struct MoeSmallArgs {
 };
 void moe_dispatch_small(const MoeSmallArgs& a, hipStream_t st);
 
+// Ref moe_dispatch.hpp:71-76: act_quant_fp8 (block 128) of the rows x[u2t[u]] [dim] for u < plan->n_remote_tokens
+// (a device-side count) into q_dst [U, dim] / s_dst [U, dim / 128]: the compact fp8 form of the tokens whose experts
+// run on another device. Grid sized for max_tokens; dim % 128 == 0, x 16-byte aligned.
+void quant_remote_tokens(const uint16_t* x, int dim, const int32_t* u2t, const MoePlan* plan, uint8_t* q_dst,
+                         uint8_t* s_dst, int max_tokens, hipStream_t st);
+
 }  // namespace unholy::kernels

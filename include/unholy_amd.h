@@ -203,6 +203,15 @@ int uh_gemv_w8a8_glu(const uint8_t* a, const uint8_t* sa, const uint8_t* w_gate,
 /* kernel.py fp8_gemm with fp32 scales (scale_fmt=None); gemm_wmma.hip:89-100's fold */
 int uh_gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw, uint16_t* c, int ldc,
                      int M, int N, int K, void* stream);
+/* elem_fast.hpp:23-26: rmsnorm of x [rows, dim] with w [dim] into y, then (q set) act_quant_fp8 (block 128) of y into
+ * q [rows, dim] / qs [rows, dim / 128], one launch. *launched = 0 where the reference's returns false (in place, or
+ * slices not whole multiples of 256 values): nothing was done. */
+int uh_rmsnorm_quant_slices(const uint16_t* x, int ldx, const uint16_t* w, uint16_t* y, int ldy, uint8_t* q,
+                            uint8_t* qs, int rows, int dim, float eps, int* launched, void* stream);
+/* moe_dispatch.hpp:71-76: act_quant_fp8 (block 128) of rows x[u2t[u]] for u < plan[4] (n_remote_tokens, on the
+ * device) into q [U, dim] / s [U, dim / 128]; grid for max_tokens. */
+int uh_quant_remote_tokens(const uint16_t* x, int dim, const int32_t* u2t, const int32_t* plan, uint8_t* q, uint8_t* s,
+                           int max_tokens, void* stream);
 /* ref.hpp:42-45 (reference order), gemm_wmma.hpp:24-26 (fast path), gemv.hpp:36-37 (GEMV, M <= 32): grouped
  * "mgk,grk->mgr" with fp8 weights x 128x128 e8m0 scales. a bf16 [M, G, K], w e4m3 [G R, K],
  * sw [ceil(G R / 128), K / 128], c bf16 [M, G, R]; K % 128 == 0. uh_gemv_grouped_fp8w with q set also writes

@@ -42,6 +42,7 @@ _SIGS = {
     "or_gemm_w8a8_f64": (None, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]),
     "or_gemm_grouped_fp8w": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I]),
     "or_gemm_grouped_fp8w_f64": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I]),
+    "or_rmsnorm_quant": (None, [_P, _I, _P, _P, _I, _P, _P, _I, _I, _F]),
     "or_swiglu": (None, [_P, _P, _P, _P, _I, _I, _F]),
     "or_route_ds": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P, _I]),
     "or_route_glm": (None, [_P, _P, _P, _P, _I, _I, _I, _F]),
@@ -257,6 +258,22 @@ def gemm_grouped_fp8w_f64(a, w, sw, G, R, threads=8):
     c = np.empty((M, G, R), np.float64)
     lib().or_gemm_grouped_fp8w_f64(_p(a), _p(w), _p(sw), _p(c), M, G, R, K, threads)
     return c
+
+
+def rmsnorm_quant(x, w, eps, quant=True):
+    """rmsnorm of bf16 rows x [rows, dim] with bf16 weights w [dim] in the reference's order; with quant also
+    act_quant_fp8 (block 128) of the output. Returns y (bf16) or (y, q, qs)."""
+    x = _c(x, np.uint16)
+    w = _c(w, np.uint16)
+    rows, dim = x.shape
+    y = np.empty((rows, dim), np.uint16)
+    if not quant:
+        lib().or_rmsnorm_quant(_p(x), dim, _p(w), _p(y), dim, None, None, rows, dim, eps)
+        return y
+    q = np.empty((rows, dim), np.uint8)
+    qs = np.empty((rows, dim // 128), np.uint8)
+    lib().or_rmsnorm_quant(_p(x), dim, _p(w), _p(y), dim, _p(q), _p(qs), rows, dim, eps)
+    return y, q, qs
 
 
 # ---- MoE pieces -------------------------------------------------------------------------------------------------------

@@ -14,6 +14,12 @@
 //                       (raw per-128 chain folded with acc += raw * (sa * sw))
 //   gemm_grouped_fp8w   src/kernels/ref_gemm.hip:111-125, :198-202 with gemm_ref_kernel :18-67 at G = K (one
 //                       K-block: a single fp32 fmaf chain over k in order, scale 1): "mgk,grk->mgr"
+//   rmsnorm (+ quant)   src/kernels/ref_elem.hip:62-77 (rmsnorm_kernel, 256 threads), dev.hip.hpp:154-180
+//                       (block_sum: a wave32 xor butterfly per warp, then the same butterfly over the warp sums);
+//                       elem_fast.hip:52-88 (rmsnorm_quant_slices: act_quant_fp8 per 128 of the bf16 output).
+//                       The sum of squares as the device compiles `ss += v * v` (contracted: fma). One deviation:
+//                       1 / sqrt in IEEE single (sqrt, then divide, each correctly rounded) where the reference's
+//                       rsqrtf is the hardware approximation, which no CPU restatement reproduces
 //   swiglu              src/kernels/ref_moe.hip:62-74
 //   route (DSV4)        src/kernels/ref_moe.hip:14-60
 //   route (GLM sigmoid) src/kernels/moe_dispatch.hip:308-356
@@ -336,6 +342,48 @@ void or_gemm_grouped_fp8w_f64(const uint16_t* a, const uint8_t* w, const uint8_t
       c[size_t(m) * G * R + n] = acc;
     }
   });
+}
+
+// rmsnorm of rows [rows, dim] in the reference's order, then (q set) act_quant_fp8 (block 128) of the bf16 output.
+void or_rmsnorm_quant(const uint16_t* x, int ldx, const uint16_t* w, uint16_t* y, int ldy, uint8_t* q, uint8_t* qs,
+                      int rows, int dim, float eps) {
+  constexpr int NT = 256;
+  for (int r = 0; r < rows; ++r) {
+    const uint16_t* xr = x + size_t(r) * ldx;
+    float part[NT];
+    for (int t = 0; t < NT; ++t) {
+      float ss = 0.0f;
+      for (int i = t; i < dim; i += NT) {
+        const float v = bf16_to_f32(xr[i]);
+        ss = std::fma(v, v, ss);
+      }
+      part[t] = ss;
+    }
+    // block_sum: within each 32-thread warp v += v[lane ^ o] for o = 16, 8, 4, 2, 1 (every lane ends with the same
+    // value), then warp 0 repeats it over the 8 warp sums (lanes 8-31 hold zero: the first two steps add zero).
+    const auto butterfly = [](float* v) {
+      for (int o = 16; o >= 1; o >>= 1) {
+        float nv[32];
+        for (int l = 0; l < 32; ++l) nv[l] = v[l] + v[l ^ o];
+        std::memcpy(v, nv, sizeof(nv));
+      }
+    };
+    float red[32] = {};
+    for (int wv = 0; wv < NT / 32; ++wv) {
+      float v[32];
+      std::memcpy(v, part + wv * 32, sizeof(v));
+      butterfly(v);
+      red[wv] = v[0];
+    }
+    butterfly(red);
+    const float rinv = 1.0f / std::sqrt(red[0] / float(dim) + eps);
+    uint16_t* yr = y + size_t(r) * ldy;
+    for (int i = 0; i < dim; ++i) {
+      const float t = bf16_to_f32(xr[i]) * rinv;
+      yr[i] = f32_to_bf16(bf16_to_f32(w[i]) * t);
+    }
+  }
+  if (q) or_act_quant_fp8(y, ldy, q, qs, rows, dim, 128);
 }
 
 // ---- SwiGLU (ref_moe.hip:62-74) -----------------------------------------------------------------------------------

@@ -250,6 +250,23 @@ def test_gemm_grouped_fp8w_brute_force():
         assert np.allclose(c64, exact, rtol=1e-12, atol=1e-12 * np.abs(exact).max())
 
 
+def test_rmsnorm_quant_closed_form():
+    """rmsnorm against fp64 w x / sqrt(mean(x^2) + eps): within the two roundings the reference applies (x * r to fp32,
+    w * t to bf16); the output's quantization is act_quant_fp8 of it."""
+    rng = np.random.default_rng(13)
+    for rows, dim, eps in ((3, 4096, 1e-6), (2, 512, 1e-2), (1, 7168, 1e-6)):
+        x = randn_bf16(rng, (rows, dim), scale=4.0)
+        w = randn_bf16(rng, (dim,))
+        y, q, qs = oracle.rmsnorm_quant(x, w, eps)
+        xf, wf = from_bf16(x).astype(np.float64), from_bf16(w).astype(np.float64)
+        exact = wf * xf / np.sqrt((xf ** 2).mean(axis=1, keepdims=True) + eps)
+        err = np.abs(from_bf16(y) - exact)
+        assert np.all(err <= 2.0 ** -8 * np.abs(exact) + 1e-30)
+        q_ref, qs_ref = oracle.act_quant_fp8(y)
+        assert np.array_equal(q, q_ref) and np.array_equal(qs, qs_ref)
+        assert np.array_equal(oracle.rmsnorm_quant(x, w, eps, quant=False), y)
+
+
 # ---- MoE pieces ------------------------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("limit", [10.0, 0.0])
 def test_swiglu_closed_form(limit):

@@ -6,6 +6,7 @@
 
 #include "common.hpp"
 #include "numerics.hpp"
+#include "unholy/kernels/elem_fast.hpp"
 #include "unholy/kernels/gemm_wmma.hpp"
 #include "unholy/kernels/gemv.hpp"
 #include "unholy/kernels/moe_dispatch.hpp"
@@ -462,6 +463,19 @@ int uh_gemv_w8a8_glu(const uint8_t* a, const uint8_t* sa, const uint8_t* w_gate,
 int uh_gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw, uint16_t* c, int ldc,
                      int M, int N, int K, void* st) {
   return guard([&] { k::gemm_fp8_f32s(a, sa, w, sw, c, ldc, M, N, K, S(st)); });
+}
+int uh_rmsnorm_quant_slices(const uint16_t* x, int ldx, const uint16_t* w, uint16_t* y, int ldy, uint8_t* q,
+                            uint8_t* qs, int rows, int dim, float eps, int* launched, void* st) {
+  return guard([&] {
+    const bool done = k::rmsnorm_quant_slices(x, ldx, w, y, ldy, q, qs, rows, dim, eps, S(st));
+    if (launched) *launched = done ? 1 : 0;
+  });
+}
+int uh_quant_remote_tokens(const uint16_t* x, int dim, const int32_t* u2t, const int32_t* plan, uint8_t* q, uint8_t* s,
+                           int max_tokens, void* st) {
+  return guard([&] {
+    k::quant_remote_tokens(x, dim, u2t, reinterpret_cast<const k::MoePlan*>(plan), q, s, max_tokens, S(st));
+  });
 }
 int uh_gemm_grouped_fp8w(const uint16_t* a, const uint8_t* w, const uint8_t* sw, uint16_t* c, int M, int G, int R,
                          int K, void* st) {
