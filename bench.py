@@ -2,7 +2,7 @@
 """Benchmark of the MXFP4 routed-expert FFN on one MI355X (gfx950).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
-    python bench.py --only {decode,single,verify,prefill,fp8,grouped,producers,copy}   # one workload (for profilers), one JSON line
+    python bench.py --only {decode,single,verify,prefill,fp8,grouped,producers,pack,copy}   # one workload (for profilers), one JSON line
 
 A step is one routed-expert FFN over one batch of synthetic tokens: softmax top-6 routing of [T, 256] logits,
 dispatch, fp8 input transform, w1/w3 grouped GEMV with the SwiGLU epilogue, w2 grouped GEMV, combine to bf16
@@ -253,6 +253,40 @@ def producers_entry(rows, t_norm, t_rq):
             "quant_remote_tokens": {"ms": t_rq, "GBps": b_rq / (t_rq * 1e-3) / 1e9}}
 
 
+def bench_pack(n_experts=16, reps=3):
+    """The expert pack's loader: a pack of n_experts experts of the headline shape (13.4 MB each) written to a
+    temporary file (its pages stay in the host's page cache), then its slots loaded into device memory through the
+    pinned double-buffered staging, with and without the per-slot xxh64 check. Returns GB/s of slot bytes (best of
+    reps), host page cache to HBM."""
+    import ctypes
+    import tempfile
+    from unholy_amd import call
+    from unholy_amd.device import DeviceBuffer, synchronize
+    rng = np.random.default_rng(77)
+    parts = []
+    for _ in range(n_experts):
+        for rows, cols in ((I, D), (I, D), (D, I)):
+            parts.append(rng.integers(0, 256, rows * cols // 2, dtype=np.uint8))
+            parts.append(rng.integers(119, 126, rows * cols // 32, dtype=np.uint8))
+    ptrs = (ctypes.c_void_p * len(parts))(*[a.ctypes.data for a in parts])
+    with tempfile.TemporaryDirectory() as tmp:
+        path = (tmp + "/experts.pack").encode()
+        call("uh_pack_write", path, 1, 0, n_experts, I, D, D, I, ptrs, 0, 0)
+        del parts
+        dst = DeviceBuffer(n_experts * EXPERT_BYTES)
+        out = {"experts": n_experts, "bytes": n_experts * EXPERT_BYTES}
+        for verify in (0, 1):
+            best = None
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                call("uh_pack_load", path, 0, n_experts, dst, EXPERT_BYTES, verify, 0, None)
+                synchronize()
+                dt = time.perf_counter() - t0
+                best = dt if best is None else min(best, dt)
+            out["GBps_verified" if verify else "GBps"] = n_experts * EXPERT_BYTES / best / 1e9
+        return out
+
+
 def grouped_entry(M, ms):
     G, R, K = GW_G, GW_R, GW_K
     wbytes = G * R * K + (G * R // 128) * (K // 128)
@@ -306,6 +340,8 @@ def run_only(name, args, rng):
             call("uh_memcpy_d2d", dst, src, n, None)
         synchronize()
         return {"workload": "copy", "bytes_per_copy": n, "copies": 4}
+    if name == "pack":
+        return {"expert_pack_load": bench_pack()}
     if name == "producers":
         return {f"producers_rows{r}": producers_entry(r, *bench_producers(r, 64, 16, rng)) for r in (8, 4096)}
     if name == "grouped":
@@ -335,7 +371,7 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["decode", "single", "verify", "prefill", "fp8", "grouped", "producers",
-                                       "copy"])
+                                       "pack", "copy"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the MoE expert path runs on a single MI355X in this build "
@@ -419,6 +455,7 @@ def main():
             wl[f"grouped_fp8w_wo_a_M{M}"] = grouped_entry(M, t)
         for r in (8, 4096):
             wl[f"producers_rows{r}"] = producers_entry(r, *bench_producers(r, 64, 16, rng))
+        wl["expert_pack_load"] = bench_pack()
         result["workloads"] = wl
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()

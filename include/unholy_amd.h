@@ -203,6 +203,24 @@ int uh_gemv_w8a8_glu(const uint8_t* a, const uint8_t* sa, const uint8_t* w_gate,
 /* kernel.py fp8_gemm with fp32 scales (scale_fmt=None); gemm_wmma.hip:89-100's fold */
 int uh_gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw, uint16_t* c, int ldc,
                      int M, int N, int K, void* stream);
+/* ---- the expert pack (src/model/expert_pack.hpp:1-92; the file format byte for byte) ---- */
+/* XXH64 of len bytes (a value, not a status). */
+uint64_t uh_pack_xxh64(const void* data, size_t len, uint64_t seed);
+/* The writer (tools/expert_pack's job, from host arrays): (n_layers + n_mtp) * n_experts slots; parts: host table of
+ * 6 pointers per slot {w1 codes [w13_out, w13_in/2], w1 scales [w13_out, w13_in/32], w3 ..., w2 codes
+ * [w2_out, w2_in/2], w2 scales}, row-major, or six NULLs for an absent slot. */
+int uh_pack_write(const char* path, int n_layers, int n_mtp, int n_experts, int w13_out, int w13_in, int w2_out,
+                  int w2_in, const uint8_t* const* parts, uint64_t config_hash, uint64_t source_hash);
+/* expert_pack.hpp:88-89 (read_header): the validated header's 264 bytes into header (host). */
+int uh_pack_read_header(const char* path, uint8_t* header);
+/* The loader: slots [first, first + count) into device memory dst + i * stride (stride >= slot_bytes, % 256 == 0),
+ * through pinned double-buffered staging; verify: each slot's xxh64 against the checksum table; direct: O_DIRECT.
+ * Synchronous on stream at return. */
+int uh_pack_load(const char* path, size_t first, size_t count, void* dst, size_t stride, int verify, int direct,
+                 void* stream);
+/* The forward's expert table (6 x E device pointers, {w1 codes, w1 scales, w3 ..., w2 scales} x E, as
+ * uh_mx_moe_forward takes it) of E slots loaded at slots + e * stride, into the host array tab [6 * E]. */
+int uh_pack_expert_table(const uint8_t* header, const void* slots, size_t stride, int E, uint64_t* tab);
 /* elem_fast.hpp:23-26: rmsnorm of x [rows, dim] with w [dim] into y, then (q set) act_quant_fp8 (block 128) of y into
  * q [rows, dim] / qs [rows, dim / 128], one launch. *launched = 0 where the reference's returns false (in place, or
  * slices not whole multiples of 256 values): nothing was done. */

@@ -89,6 +89,9 @@ def ref_lib() -> ctypes.CDLL | None:
         l.ref_e2m1_to_float.argtypes = [ctypes.c_uint8]
         l.ref_repack_matrix.argtypes = [_P, _P, _P, _P, _I, _I]
         l.ref_unrepack_matrix.argtypes = [_P, _P, _P, _P, _I, _I]
+        l.ref_xxh64.restype, l.ref_xxh64.argtypes = ctypes.c_uint64, [_P, ctypes.c_size_t, ctypes.c_uint64]
+        l.ref_read_header.restype, l.ref_read_header.argtypes = _I, [ctypes.c_char_p, _P]
+        l.ref_header_size.restype, l.ref_header_size.argtypes = _I, []
         _ref = l
     return _ref
 

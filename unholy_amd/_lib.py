@@ -76,7 +76,7 @@ def parse_header(path: pathlib.Path = HEADER) -> dict[str, tuple]:
 _lib = None
 _protos = None
 # Entry points whose int result is a value, not a status.
-_NOT_STATUS = {"uh_version", "uh_mx_gemm_set_exact"}
+_NOT_STATUS = {"uh_version", "uh_mx_gemm_set_exact", "uh_pack_xxh64"}
 
 
 def lib() -> ctypes.CDLL:

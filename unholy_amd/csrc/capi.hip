@@ -1,12 +1,16 @@
 // The C ABI (include/unholy_amd.h): exception-to-status wrappers over the C++ entry points, device memory and
 // stream helpers for hosts without a HIP binding (the Python package binds this library with ctypes), the
 // synthetic-data generator and the one-call routed-expert FFN.
+#include <fcntl.h>
+#include <unistd.h>
+
 #include <cstring>
 #include <string>
 
 #include "common.hpp"
 #include "numerics.hpp"
 #include "unholy/kernels/elem_fast.hpp"
+#include "unholy/model/expert_pack.hpp"
 #include "unholy/kernels/gemm_wmma.hpp"
 #include "unholy/kernels/gemv.hpp"
 #include "unholy/kernels/moe_dispatch.hpp"
@@ -463,6 +467,56 @@ int uh_gemv_w8a8_glu(const uint8_t* a, const uint8_t* sa, const uint8_t* w_gate,
 int uh_gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw, uint16_t* c, int ldc,
                      int M, int N, int K, void* st) {
   return guard([&] { k::gemm_fp8_f32s(a, sa, w, sw, c, ldc, M, N, K, S(st)); });
+}
+uint64_t uh_pack_xxh64(const void* data, size_t len, uint64_t seed) { return unholy::model::pack::xxh64(data, len, seed); }
+int uh_pack_write(const char* path, int n_layers, int n_mtp, int n_experts, int w13_out, int w13_in, int w2_out,
+                  int w2_in, const uint8_t* const* parts, uint64_t config_hash, uint64_t source_hash) {
+  namespace pk = unholy::model::pack;
+  return guard([&] {
+    pk::write_pack(path, pk::geometry_for(n_layers, n_mtp, n_experts, w13_out, w13_in, w2_out, w2_in), parts,
+                   config_hash, source_hash);
+  });
+}
+int uh_pack_read_header(const char* path, uint8_t* header) {
+  namespace pk = unholy::model::pack;
+  return guard([&] {
+    const int fd = ::open(path, O_RDONLY);
+    if (fd < 0) throw std::runtime_error(std::string("expert pack: cannot open ") + path);
+    try {
+      const pk::Header h = pk::read_header(fd);
+      std::memcpy(header, &h, sizeof h);
+    } catch (...) {
+      ::close(fd);
+      throw;
+    }
+    ::close(fd);
+  });
+}
+int uh_pack_load(const char* path, size_t first, size_t count, void* dst, size_t stride, int verify, int direct,
+                 void* st) {
+  namespace pk = unholy::model::pack;
+  return guard([&] {
+    const int fd = ::open(path, O_RDONLY | (direct ? O_DIRECT : 0));
+    if (fd < 0) throw std::runtime_error(std::string("expert pack: cannot open ") + path);
+    try {
+      pk::load_slots(fd, pk::read_header(fd), first, count, dst, stride, verify != 0, st);
+    } catch (...) {
+      ::close(fd);
+      throw;
+    }
+    ::close(fd);
+  });
+}
+int uh_pack_expert_table(const uint8_t* header, const void* slots, size_t stride, int E, uint64_t* tab) {
+  namespace pk = unholy::model::pack;
+  return guard([&] {
+    pk::Header h;
+    std::memcpy(&h, header, sizeof h);
+    if (!slots || !tab || E <= 0 || stride < h.slot_bytes) throw std::runtime_error("expert pack: table arguments");
+    for (int e = 0; e < E; ++e)
+      for (int f = 0; f < pk::kParts; ++f)
+        tab[size_t(f) * E + e] = uint64_t(reinterpret_cast<uintptr_t>(slots) + e * stride + h.part_offset[f]);
+  });
 }
 int uh_rmsnorm_quant_slices(const uint16_t* x, int ldx, const uint16_t* w, uint16_t* y, int ldy, uint8_t* q,
                             uint8_t* qs, int rows, int dim, float eps, int* launched, void* st) {
