@@ -8,12 +8,19 @@
 #include <fcntl.h>
 #include <unistd.h>
 
+#include <algorithm>
+#include <atomic>
 #include <cerrno>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <exception>
+#include <mutex>
 #include <stdexcept>
 #include <string>
+#include <thread>
+#include <unordered_map>
+#include <utility>
 #include <vector>
 
 #include "common.hpp"
@@ -22,6 +29,45 @@
 namespace unholy::model::pack {
 
 namespace {
+
+constexpr size_t kLoadThreads = 8;  // reader threads of load_slots
+
+// Pinned staging buffers of load_slots, kept for the life of the process and reused by later calls (allocating pinned
+// memory costs milliseconds per buffer, more than loading a few slots). Portable, so any device can copy from them.
+// A buffer is taken by one reader thread at a time and returned only after its last copy has completed.
+class StagingPool {
+ public:
+  void* take(size_t bytes) {
+    {
+      const std::lock_guard<std::mutex> lock(mu_);
+      for (size_t i = 0; i < free_.size(); ++i)
+        if (free_[i].second >= bytes) {
+          void* p = free_[i].first;
+          free_.erase(free_.begin() + std::ptrdiff_t(i));
+          return p;
+        }
+    }
+    void* p = nullptr;
+    UH_CHECK(hipHostMalloc(&p, bytes, hipHostMallocPortable));
+    const std::lock_guard<std::mutex> lock(mu_);
+    size_[p] = bytes;
+    return p;
+  }
+  void give(void* p) {
+    const std::lock_guard<std::mutex> lock(mu_);
+    free_.emplace_back(p, size_[p]);
+  }
+
+ private:
+  std::mutex mu_;
+  std::vector<std::pair<void*, size_t>> free_;
+  std::unordered_map<void*, size_t> size_;
+};
+
+StagingPool& staging_pool() {
+  static StagingPool* pool = new StagingPool;  // never destroyed: pinned memory is released at process exit
+  return *pool;
+}
 
 // XXH64 constants and steps as published with xxHash.
 constexpr uint64_t kP1 = 0x9E3779B185EBCA87ull, kP2 = 0xC2B2AE3D27D4EB4Full, kP3 = 0x165667B19E3779F9ull,
@@ -270,43 +316,59 @@ void load_slots(int fd, const Header& h, size_t first, size_t count, void* dst, 
     }
     free_aligned(buf);
   }
-  // Two pinned staging buffers (4 KiB aligned for O_DIRECT; slots start on 4 KiB boundaries and are whole 4 KiB
-  // multiples, so each read is exactly its slot).
-  void* stage[2] = {nullptr, nullptr};
-  hipEvent_t done[2] = {nullptr, nullptr};
-  const auto release = [&] {
-    for (int b = 0; b < 2; ++b) {
+  // Reader threads, as the reference's stream test issues whole-slot reads from several threads: each thread claims
+  // slots from a shared counter and owns two pinned staging buffers (4 KiB aligned for O_DIRECT; slots start on
+  // 4 KiB boundaries and are whole 4 KiB multiples, so each read is exactly its slot). A thread's file read and
+  // checksum of one slot overlap the host-to-device copy of its previous one and the other threads' work.
+  int device = 0;
+  UH_CHECK(hipGetDevice(&device));
+  const int nthreads = int(std::min<size_t>(count, kLoadThreads));
+  std::atomic<size_t> next{0};
+  std::atomic<bool> failed{false};
+  std::mutex err_mu;
+  std::exception_ptr err;
+  const auto reader = [&] {
+    void* stage[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    try {
+      UH_CHECK(hipSetDevice(device));
+      for (int b = 0; b < 2; ++b) {
+        stage[b] = staging_pool().take(h.slot_bytes + kAlign);
+        UH_CHECK(hipEventCreateWithFlags(&done[b], hipEventDisableTiming));
+      }
+      for (int n = 0; !failed.load(std::memory_order_relaxed); ++n) {
+        const size_t i = next.fetch_add(1);
+        if (i >= count) break;
+        const int b = n & 1;
+        UH_CHECK(hipEventSynchronize(done[b]));  // the copy that last used this buffer is over
+        uint8_t* a = reinterpret_cast<uint8_t*>(align_up(reinterpret_cast<uintptr_t>(stage[b])));
+        read_aligned(fd, h.slots_offset + (first + i) * h.slot_bytes, h.slot_bytes, a);
+        if (verify) {
+          const ChecksumEntry& e = table[first + i];
+          if (!e.present) throw std::runtime_error("expert pack: slot " + std::to_string(first + i) + " is absent");
+          if (xxh64(a, h.slot_bytes) != e.hash)
+            throw std::runtime_error("expert pack: slot " + std::to_string(first + i) + " checksum mismatch");
+        }
+        UH_CHECK(hipMemcpyAsync(static_cast<uint8_t*>(dst) + i * stride, a, h.slot_bytes, hipMemcpyHostToDevice,
+                                st));
+        UH_CHECK(hipEventRecord(done[b], st));
+      }
+    } catch (...) {
+      failed = true;
+      const std::lock_guard<std::mutex> lock(err_mu);
+      if (!err) err = std::current_exception();
+    }
+    for (int b = 0; b < 2; ++b) {  // a buffer is freed only once its copy is over
       if (done[b]) (void)hipEventSynchronize(done[b]), (void)hipEventDestroy(done[b]);
-      if (stage[b]) (void)hipHostFree(stage[b]);
+      if (stage[b]) staging_pool().give(stage[b]);
     }
   };
-  try {
-    for (int b = 0; b < 2; ++b) {
-      UH_CHECK(hipHostMalloc(&stage[b], h.slot_bytes + kAlign, hipHostMallocDefault));
-      UH_CHECK(hipEventCreateWithFlags(&done[b], hipEventDisableTiming));
-    }
-    for (size_t i = 0; i < count; ++i) {
-      const int b = int(i & 1);
-      UH_CHECK(hipEventSynchronize(done[b]));  // the copy that last used this buffer is over
-      uint8_t* buf = static_cast<uint8_t*>(stage[b]);
-      uint8_t* a = reinterpret_cast<uint8_t*>(align_up(reinterpret_cast<uintptr_t>(buf)));
-      const uint64_t off = h.slots_offset + (first + i) * h.slot_bytes;
-      read_aligned(fd, off, h.slot_bytes, a);
-      if (verify) {
-        const ChecksumEntry& e = table[first + i];
-        if (!e.present) throw std::runtime_error("expert pack: slot " + std::to_string(first + i) + " is absent");
-        if (xxh64(a, h.slot_bytes) != e.hash)
-          throw std::runtime_error("expert pack: slot " + std::to_string(first + i) + " checksum mismatch");
-      }
-      UH_CHECK(hipMemcpyAsync(static_cast<uint8_t*>(dst) + i * stride, a, h.slot_bytes, hipMemcpyHostToDevice, st));
-      UH_CHECK(hipEventRecord(done[b], st));
-    }
-    UH_CHECK(hipStreamSynchronize(st));
-  } catch (...) {
-    release();
-    throw;
-  }
-  release();
+  std::vector<std::thread> pool;
+  for (int t = 1; t < nthreads; ++t) pool.emplace_back(reader);
+  reader();
+  for (auto& th : pool) th.join();
+  if (err) std::rethrow_exception(err);
+  UH_CHECK(hipStreamSynchronize(st));
 }
 
 }  // namespace unholy::model::pack
