@@ -10,6 +10,15 @@ namespace unholy::kernels {
 
 using bf16 = uint16_t;
 
+// Ref elem_fast.hpp:14-20: the mHC post-mix done by the producer of a row, in place on the streams x [T][hc][dim]
+// (x null: not asked for); post [T][hc], comb [T][hc][hc] fp32; hc <= 4.
+struct HcPostArgs {
+  bf16* x = nullptr;
+  const float* post = nullptr;
+  const float* comb = nullptr;
+  int hc = 0;
+};
+
 // Ref elem_fast.hpp:23-26: rmsnorm of rows x [rows, dim] (bf16 weights w [dim], eps) into y [rows, ldy], then, with
 // q, act_quant_fp8 (block 128) of y into q [rows, dim] / qs [rows, dim / 128], in one launch. false (nothing
 // launched) where the reference's is: in place, or slices not whole multiples of 256 values.

@@ -11,6 +11,8 @@
 
 #include <cstdint>
 
+#include "unholy/kernels/elem_fast.hpp"
+
 #include "unholy/kernels/exl3_moe.hpp"
 
 namespace unholy::kernels {
@@ -40,9 +42,10 @@ void moe_scatter_e(const int32_t* sel, const float* wt, int T, int K, int E, con
                    float* ewt, int32_t* row_expert, int32_t* pidx, hipStream_t st);
 
 // count + plan + scatter (optionally routing first) for steps of up to kMoeSmallMaxTokens tokens in one
-// single-block launch. Ref :79-124. The remote-side fields (remote, qin, tok2u, u2t, p2u_dst, u2p_dst, plan_dst,
-// tiles_dst, w_dst, e_dst, x_dst, q_dst, req_flag) belong to the cross-device transport: this single-GPU
-// library rejects them set (all experts must be resident).
+// single-block launch. Ref :79-124. resident (null: all resident) puts the other experts' rows after remote0 and their
+// tiles in rtl. With remote: stage_remote's outputs (plan_dst, tiles_dst, w_dst, e_dst); with qin also remote_tokens'
+// (tok2u, u2t, p2u_dst, u2p_dst), and then x_dst (copy_remote_tokens) and q_dst / qs_dst (quant_remote_tokens) when
+// given; req_flag: value stored with system-scope release after every write above.
 constexpr int kMoeSmallMaxTokens = 32;
 struct MoeSmallArgs {
   const int32_t* sel;
@@ -83,6 +86,42 @@ struct MoeSmallArgs {
   const float* softmax_logits = nullptr;
 };
 void moe_dispatch_small(const MoeSmallArgs& a, hipStream_t st);
+
+// ---- remote experts (the compact transport of experts held elsewhere) -------------------------------------------------
+// Kernels with device-side extents (the plan); grids sized for max_rows / max_tokens. Each ends with a system-scope
+// fence so a peer reading pinned host memory over the link sees its writes.
+// Ref moe_dispatch.hpp:34-40: rows [remote0, P) of src -> the same rows of dst; the plan, remote tiles and the remote
+// rows' routing weights and experts -> the remote side's staging.
+void copy_remote_rows(const uint16_t* src, uint16_t* dst, const MoePlan* plan, int dim, int max_rows, hipStream_t st);
+void stage_remote(const MoePlan* plan, const Exl3Tile* rtiles, const float* ewt, const int32_t* row_expert,
+                  MoePlan* plan_dst, Exl3Tile* tiles_dst, float* w_dst, int32_t* e_dst, int max_rows, hipStream_t st);
+// Ref moe_dispatch.hpp:125-126: the remote rows' weights and experts only.
+void copy_remote_meta(const float* ewt, const int32_t* row_expert, float* w_dst, int32_t* e_dst, const MoePlan* plan,
+                      int max_rows, hipStream_t st);
+// Ref moe_dispatch.hpp:41-46: the tokens with at least one remote pair, in token order: tok2u [T] (-1: none),
+// u2t [U], plan->n_remote_tokens = U, p2u_dst[p] = tok2u[eidx[p]] for p in [remote0, P), and with u2p_dst,
+// u2p_dst[u * K + j] = token u's j-th pair row if remote, else -1. One workgroup.
+void remote_tokens(const int32_t* pidx, const int32_t* eidx, int T, int K, MoePlan* plan, int32_t* tok2u,
+                   int32_t* u2t, int32_t* p2u_dst, int32_t* u2p_dst, hipStream_t st);
+// Ref moe_dispatch.hpp:47-52: dst[u] = bf16(sum over token u's remote pair rows of pair_out, fp32 adds in pick
+// (ascending expert) order) for u < n_remote_tokens. dim % 8, 16-byte aligned rows.
+void remote_combine(const uint16_t* pair_out, const int32_t* u2p, const MoePlan* plan, uint16_t* dst, int K, int dim,
+                    int max_tokens, hipStream_t st);
+// Ref moe_dispatch.hpp:53-57: dst[u] = x[u2t[u]] for u < n_remote_tokens.
+void copy_remote_tokens(const uint16_t* x, int dim, const int32_t* u2t, const MoePlan* plan, uint16_t* dst,
+                        int max_tokens, hipStream_t st);
+// Ref moe_dispatch.hpp:58-60: src rows (remote_combine's dst) -> rows [remote0, remote0 + U) of dst.
+void copy_remote_partial(const uint16_t* src, uint16_t* dst, const MoePlan* plan, int dim, int max_tokens,
+                         hipStream_t st);
+// Ref moe_dispatch.hpp:61-64: out[t] = bf16(token t's local pair rows (pidx order) + its remote partial row
+// (pair_out row remote0 + tok2u[t]) + shared[t]), fp32 adds from 0 (shared null: no term).
+void moe_combine_partial(const uint16_t* pair_out, const int32_t* pidx, const MoePlan* plan, const int32_t* tok2u,
+                         const uint16_t* shared, uint16_t* out, int T, int K, int dim, hipStream_t st);
+// Ref moe_dispatch.hpp:65-70: the same with the remote partial read from row tok2u[t] of `remote`; with hp.x, the
+// mHC post-mix of each combined value into the token's streams.
+void moe_combine_partial_link(const uint16_t* pair_out, const int32_t* pidx, const MoePlan* plan, const int32_t* tok2u,
+                              const uint16_t* remote, const uint16_t* shared, uint16_t* out, int T, int K, int dim,
+                              hipStream_t st, const HcPostArgs& hp = {});
 
 // Ref moe_dispatch.hpp:71-76: act_quant_fp8 (block 128) of the rows x[u2t[u]] [dim] for u < plan->n_remote_tokens
 // (a device-side count) into q_dst [U, dim] / s_dst [U, dim / 128]: the compact fp8 form of the tokens whose experts

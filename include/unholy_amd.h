@@ -156,7 +156,8 @@ int uh_moe_plan(int32_t* count, const uint8_t* resident, int E, int P, int32_t* 
 /* moe_dispatch.hpp:32-33 (deterministic: rows of an expert in ascending token order) */
 int uh_moe_scatter(const int32_t* sel, const float* wt, int T, int K, const int32_t* off, int32_t* fill,
                    int32_t* eidx, float* ewt, int32_t* row_expert, int32_t* pidx, void* stream);
-/* moe_dispatch.hpp:124 (MoeSmallArgs without the remote-side fields; ds_* or route_* logits: routing in-launch) */
+/* moe_dispatch.hpp:124 (MoeSmallArgs without the resident mask and remote-side fields; ds_* or route_* logits:
+ * routing in-launch) */
 int uh_moe_dispatch_small(const int32_t* sel, const float* wt, int T, int K, int E, int P, int max_tiles,
                           int tile_rows, int32_t* plan, int32_t* tiles, int32_t* eidx, float* ewt,
                           int32_t* row_expert, int32_t* pidx, uint32_t* hist, const float* route_logits,
@@ -230,6 +231,46 @@ int uh_rmsnorm_quant_slices(const uint16_t* x, int ldx, const uint16_t* w, uint1
  * device) into q [U, dim] / s [U, dim / 128]; grid for max_tokens. */
 int uh_quant_remote_tokens(const uint16_t* x, int dim, const int32_t* u2t, const int32_t* plan, uint8_t* q, uint8_t* s,
                            int max_tokens, void* stream);
+/* moe_dispatch.hpp:34-40, 125-126: the remote rows [plan[1], plan[0]) of src to the same rows of dst (bf16, dim % 8);
+ * the plan, remote tiles and remote rows' weights / experts to the remote side's staging; weights / experts only. */
+int uh_copy_remote_rows(const uint16_t* src, uint16_t* dst, const int32_t* plan, int dim, int max_rows, void* stream);
+int uh_stage_remote(const int32_t* plan, const int32_t* rtiles, const float* ewt, const int32_t* row_expert,
+                    int32_t* plan_dst, int32_t* tiles_dst, float* w_dst, int32_t* e_dst, int max_rows, void* stream);
+int uh_copy_remote_meta(const float* ewt, const int32_t* row_expert, float* w_dst, int32_t* e_dst, const int32_t* plan,
+                        int max_rows, void* stream);
+/* moe_dispatch.hpp:41-46: compact remote tokens: tok2u [T], u2t [U], plan[4] = U, p2u [P] (remote rows), u2p [U, K]
+ * (may be NULL). One workgroup. */
+int uh_remote_tokens(const int32_t* pidx, const int32_t* eidx, int T, int K, int32_t* plan, int32_t* tok2u,
+                     int32_t* u2t, int32_t* p2u, int32_t* u2p, void* stream);
+/* moe_dispatch.hpp:47-52: dst [U, dim] = bf16 sums of each compact token's remote pair rows. */
+int uh_remote_combine(const uint16_t* pair_out, const int32_t* u2p, const int32_t* plan, uint16_t* dst, int K, int dim,
+                      int max_tokens, void* stream);
+/* moe_dispatch.hpp:53-60: dst[u] = x[u2t[u]]; src [U, dim] -> rows plan[1] + u of dst. */
+int uh_copy_remote_tokens(const uint16_t* x, int dim, const int32_t* u2t, const int32_t* plan, uint16_t* dst,
+                          int max_tokens, void* stream);
+int uh_copy_remote_partial(const uint16_t* src, uint16_t* dst, const int32_t* plan, int dim, int max_tokens,
+                           void* stream);
+/* moe_dispatch.hpp:61-70: out [T, dim] = bf16(local pair rows + remote partial + shared (may be NULL)); the _link form
+ * reads the partial from row tok2u[t] of remote and, with hc_x set, post-mixes each output value into the streams
+ * hc_x [T, hc, dim] (post [T, hc], comb [T, hc, hc], hc <= 4) in place. */
+int uh_moe_combine_partial(const uint16_t* pair_out, const int32_t* pidx, const int32_t* plan, const int32_t* tok2u,
+                           const uint16_t* shared, uint16_t* out, int T, int K, int dim, void* stream);
+int uh_moe_combine_partial_link(const uint16_t* pair_out, const int32_t* pidx, const int32_t* plan,
+                                const int32_t* tok2u, const uint16_t* remote, const uint16_t* shared, uint16_t* out,
+                                int T, int K, int dim, uint16_t* hc_x, const float* post, const float* comb, int hc,
+                                void* stream);
+/* moe_dispatch.hpp:79-124: moe_dispatch_small with the resident mask and the remote-side fields (routing from
+ * ds_logits when not NULL, else sel / wt are inputs). remote: stage plan_dst / tiles_dst / w_dst / e_dst; qin: also
+ * tok2u, u2t, p2u, u2p (may be NULL), then x_dst (may be NULL) and q_dst / qs_dst (may be NULL) from x [T, dim];
+ * req_flag (may be NULL) = req_value, stored last with system-scope release. */
+int uh_moe_dispatch_small_remote(const int32_t* sel, const float* wt, int T, int K, int E, int P, int max_tiles,
+                                 int tile_rows, int32_t* plan, int32_t* tiles, int32_t* remote_tiles, int32_t* eidx,
+                                 float* ewt, int32_t* row_expert, int32_t* pidx, const uint8_t* resident,
+                                 const float* ds_logits, const float* ds_bias, float route_scale, int remote, int qin,
+                                 int32_t* tok2u, int32_t* u2t, int32_t* p2u, int32_t* u2p, int32_t* plan_dst,
+                                 int32_t* tiles_dst, float* w_dst, int32_t* e_dst, const uint16_t* x, int dim,
+                                 uint16_t* x_dst, uint8_t* q_dst, uint8_t* qs_dst, uint32_t* req_flag,
+                                 uint32_t req_value, void* stream);
 /* ref.hpp:42-45 (reference order), gemm_wmma.hpp:24-26 (fast path), gemv.hpp:36-37 (GEMV, M <= 32): grouped
  * "mgk,grk->mgr" with fp8 weights x 128x128 e8m0 scales. a bf16 [M, G, K], w e4m3 [G R, K],
  * sw [ceil(G R / 128), K / 128], c bf16 [M, G, R]; K % 128 == 0. uh_gemv_grouped_fp8w with q set also writes

@@ -49,6 +49,9 @@ _SIGS = {
     "or_route_softmax": (None, [_P, _P, _P, _I, _I, _I]),
     "or_dispatch": (_I, [_P, _P, _I, _I, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P]),
     "or_moe_combine": (None, [_P, _P, _P, _P, _I, _I, _I]),
+    "or_remote_tokens": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _P, _P]),
+    "or_remote_combine": (None, [_P, _P, _I, _I, _I, _P]),
+    "or_moe_combine_partial": (None, [_P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _I]),
     "or_moe_forward": (None, [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _F, _P, _P, _I, _P, _I]),
 }
 
@@ -353,6 +356,50 @@ def moe_combine(pair_out, pidx, shared=None):
     sh = None if shared is None else _c(shared, np.uint16)
     lib().or_moe_combine(_p(pair_out), _p(pidx), _p(sh), _p(out), T, K, dim)
     return out
+
+
+def remote_tokens(pidx, eidx, remote0):
+    """Compact remote tokens (moe_dispatch.hip:149-203): dict of U, tok2u [T], u2t [U], p2u [P] (rows < remote0
+    left -1), u2p [U, K]."""
+    pidx = _c(pidx, np.int32)
+    eidx = _c(eidx, np.int32)
+    T, K = pidx.shape
+    P = eidx.size
+    tok2u = np.empty(T, np.int32)
+    u2t = np.empty(max(T, 1), np.int32)
+    p2u = np.full(max(P, 1), -1, np.int32)
+    u2p = np.empty((max(T, 1), K), np.int32)
+    U = lib().or_remote_tokens(_p(pidx), _p(eidx), T, K, int(remote0), P, _p(tok2u), _p(u2t), _p(p2u), _p(u2p))
+    return dict(U=U, tok2u=tok2u, u2t=u2t[:U], p2u=p2u[:P], u2p=u2p[:U])
+
+
+def remote_combine(pair_out, u2p):
+    pair_out = _c(pair_out, np.uint16)
+    u2p = _c(u2p, np.int32)
+    U, K = u2p.shape
+    dim = pair_out.shape[1]
+    dst = np.empty((U, dim), np.uint16)
+    lib().or_remote_combine(_p(pair_out), _p(u2p), U, K, dim, _p(dst))
+    return dst
+
+
+def moe_combine_partial(pair_out, pidx, remote0, tok2u, remote, shared=None, hc_x=None, post=None, comb=None):
+    """moe_combine_partial(_link) (moe_dispatch.hip:243-278): returns out, and the post-mixed streams when hc_x
+    [T, hc, dim] is given (a copy; the input is not changed)."""
+    pair_out = _c(pair_out, np.uint16)
+    pidx = _c(pidx, np.int32)
+    T, K = pidx.shape
+    dim = pair_out.shape[1]
+    out = np.empty((T, dim), np.uint16)
+    rem = _c(remote, np.uint16) if remote is not None and remote.size else np.zeros((1, dim), np.uint16)
+    sh = None if shared is None else _c(shared, np.uint16)
+    hx = None if hc_x is None else np.array(hc_x, np.uint16, copy=True, order="C")
+    po = None if post is None else _c(post, np.float32)
+    co = None if comb is None else _c(comb, np.float32)
+    hc = 0 if hx is None else hx.shape[1]
+    lib().or_moe_combine_partial(_p(pair_out), _p(pidx), int(remote0), _p(_c(tok2u, np.int32)), _p(rem), _p(sh),
+                                 _p(out), T, K, dim, _p(hx), _p(po), _p(co), hc)
+    return out if hx is None else (out, hx)
 
 
 def moe_forward(x, sel, wt, experts, D, I, limit, tiled=True, threads=8, subset=None):

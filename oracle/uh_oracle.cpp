@@ -566,6 +566,75 @@ void or_moe_combine(const uint16_t* pair_out, const int32_t* pidx, const uint16_
     }
 }
 
+// ---- remote experts: compact tokens and partial combines (moe_dispatch.hip:149-278) ---------------------------------
+// remote_tokens (moe_dispatch.hip:149-203): token t has a remote pair when one of its pair rows is >= remote0; those
+// tokens, in token order, get compact indices u. tok2u [T] (-1: none), u2t [U], p2u[p] = tok2u[eidx[p]] for
+// p in [remote0, P), u2p [U, K] (optional) = token u's j-th pair row if remote, else -1. Returns U.
+int or_remote_tokens(const int32_t* pidx, const int32_t* eidx, int T, int K, int remote0, int P, int32_t* tok2u,
+                     int32_t* u2t, int32_t* p2u, int32_t* u2p) {
+  int U = 0;
+  for (int t = 0; t < T; ++t) {
+    bool f = false;
+    for (int j = 0; j < K; ++j) f = f || pidx[size_t(t) * K + j] >= remote0;
+    tok2u[t] = f ? U : -1;
+    if (!f) continue;
+    u2t[U] = t;
+    if (u2p)
+      for (int j = 0; j < K; ++j) {
+        const int p = pidx[size_t(t) * K + j];
+        u2p[size_t(U) * K + j] = p >= remote0 ? p : -1;
+      }
+    ++U;
+  }
+  for (int p = remote0; p < P; ++p) p2u[p] = tok2u[eidx[p]];
+  return U;
+}
+
+// remote_combine (moe_dispatch.hip:206-229): dst[u] = bf16(sum over j of pair_out[u2p[u][j]] for u2p >= 0), fp32
+// adds from 0 in j order.
+void or_remote_combine(const uint16_t* pair_out, const int32_t* u2p, int U, int K, int dim, uint16_t* dst) {
+  for (int u = 0; u < U; ++u)
+    for (int d = 0; d < dim; ++d) {
+      float acc = 0.0f;
+      for (int j = 0; j < K; ++j) {
+        const int p = u2p[size_t(u) * K + j];
+        if (p >= 0) acc += bf16_to_f32(pair_out[size_t(p) * dim + d]);
+      }
+      dst[size_t(u) * dim + d] = f32_to_bf16(acc);
+    }
+}
+
+// moe_combine_partial / _link (moe_dispatch.hip:243-278): out[t] = bf16(local pair rows (p < remote0, j order) +
+// remote row tok2u[t] (if any) + shared[t]), fp32 adds from 0. remote: the remote rows (pair_out + remote0 * dim for
+// moe_combine_partial, remote_combine's dst for the link form). shared null: no term. hc_x non-null: the mHC post-mix
+// (dev.hip.hpp:185-201) of the combined value o into the streams hc_x [T][hc][dim] in place:
+// x[t][j][d] = bf16(fma(post[t][j], o, s_j)), s_j = fma chain over i of comb[t][i][j] * x[t][i][d] (old values).
+void or_moe_combine_partial(const uint16_t* pair_out, const int32_t* pidx, int remote0, const int32_t* tok2u,
+                            const uint16_t* remote, const uint16_t* shared, uint16_t* out, int T, int K, int dim,
+                            uint16_t* hc_x, const float* post, const float* comb, int hc) {
+  for (int t = 0; t < T; ++t)
+    for (int d = 0; d < dim; ++d) {
+      float acc = 0.0f;
+      for (int j = 0; j < K; ++j) {
+        const int p = pidx[size_t(t) * K + j];
+        if (p < remote0) acc += bf16_to_f32(pair_out[size_t(p) * dim + d]);
+      }
+      const int u = tok2u[t];
+      if (u >= 0) acc += bf16_to_f32(remote[size_t(u) * dim + d]);
+      if (shared) acc += bf16_to_f32(shared[size_t(t) * dim + d]);
+      const uint16_t o = f32_to_bf16(acc);
+      out[size_t(t) * dim + d] = o;
+      if (!hc_x) continue;
+      float r[4];
+      for (int i = 0; i < hc; ++i) r[i] = bf16_to_f32(hc_x[(size_t(t) * hc + i) * dim + d]);
+      for (int j = 0; j < hc; ++j) {
+        float s = 0.0f;
+        for (int i = 0; i < hc; ++i) s = std::fma(comb[(size_t(t) * hc + i) * hc + j], r[i], s);
+        hc_x[(size_t(t) * hc + j) * dim + d] = f32_to_bf16(std::fma(post[size_t(t) * hc + j], bf16_to_f32(o), s));
+      }
+    }
+}
+
 // ---- the routed-expert FFN (forward_ref.hip:268-304 per expert, then moe_combine) ------------------------------------
 // x bf16 [T, D]; sel / wt [T, K]; per-expert tables of code and scale pointers for w1, w3 ([I, D]) and w2
 // ([D, I]), raw or tile-major (tiled). Experts with a null w1 code pointer are skipped (their pair rows are

@@ -531,6 +531,117 @@ int uh_quant_remote_tokens(const uint16_t* x, int dim, const int32_t* u2t, const
     k::quant_remote_tokens(x, dim, u2t, reinterpret_cast<const k::MoePlan*>(plan), q, s, max_tokens, S(st));
   });
 }
+int uh_copy_remote_rows(const uint16_t* src, uint16_t* dst, const int32_t* plan, int dim, int max_rows, void* st) {
+  return guard([&] { k::copy_remote_rows(src, dst, reinterpret_cast<const k::MoePlan*>(plan), dim, max_rows, S(st)); });
+}
+int uh_stage_remote(const int32_t* plan, const int32_t* rtiles, const float* ewt, const int32_t* row_expert,
+                    int32_t* plan_dst, int32_t* tiles_dst, float* w_dst, int32_t* e_dst, int max_rows, void* st) {
+  return guard([&] {
+    k::stage_remote(reinterpret_cast<const k::MoePlan*>(plan), reinterpret_cast<const k::Exl3Tile*>(rtiles), ewt,
+                    row_expert, reinterpret_cast<k::MoePlan*>(plan_dst), reinterpret_cast<k::Exl3Tile*>(tiles_dst),
+                    w_dst, e_dst, max_rows, S(st));
+  });
+}
+int uh_copy_remote_meta(const float* ewt, const int32_t* row_expert, float* w_dst, int32_t* e_dst, const int32_t* plan,
+                        int max_rows, void* st) {
+  return guard([&] {
+    k::copy_remote_meta(ewt, row_expert, w_dst, e_dst, reinterpret_cast<const k::MoePlan*>(plan), max_rows, S(st));
+  });
+}
+int uh_remote_tokens(const int32_t* pidx, const int32_t* eidx, int T, int K, int32_t* plan, int32_t* tok2u,
+                     int32_t* u2t, int32_t* p2u, int32_t* u2p, void* st) {
+  return guard([&] {
+    k::remote_tokens(pidx, eidx, T, K, reinterpret_cast<k::MoePlan*>(plan), tok2u, u2t, p2u, u2p, S(st));
+  });
+}
+int uh_remote_combine(const uint16_t* pair_out, const int32_t* u2p, const int32_t* plan, uint16_t* dst, int K, int dim,
+                      int max_tokens, void* st) {
+  return guard([&] {
+    k::remote_combine(pair_out, u2p, reinterpret_cast<const k::MoePlan*>(plan), dst, K, dim, max_tokens, S(st));
+  });
+}
+int uh_copy_remote_tokens(const uint16_t* x, int dim, const int32_t* u2t, const int32_t* plan, uint16_t* dst,
+                          int max_tokens, void* st) {
+  return guard([&] {
+    k::copy_remote_tokens(x, dim, u2t, reinterpret_cast<const k::MoePlan*>(plan), dst, max_tokens, S(st));
+  });
+}
+int uh_copy_remote_partial(const uint16_t* src, uint16_t* dst, const int32_t* plan, int dim, int max_tokens,
+                           void* st) {
+  return guard([&] {
+    k::copy_remote_partial(src, dst, reinterpret_cast<const k::MoePlan*>(plan), dim, max_tokens, S(st));
+  });
+}
+int uh_moe_combine_partial(const uint16_t* pair_out, const int32_t* pidx, const int32_t* plan, const int32_t* tok2u,
+                           const uint16_t* shared, uint16_t* out, int T, int K, int dim, void* st) {
+  return guard([&] {
+    k::moe_combine_partial(pair_out, pidx, reinterpret_cast<const k::MoePlan*>(plan), tok2u, shared, out, T, K, dim,
+                           S(st));
+  });
+}
+int uh_moe_combine_partial_link(const uint16_t* pair_out, const int32_t* pidx, const int32_t* plan,
+                                const int32_t* tok2u, const uint16_t* remote, const uint16_t* shared, uint16_t* out,
+                                int T, int K, int dim, uint16_t* hc_x, const float* post, const float* comb, int hc,
+                                void* st) {
+  return guard([&] {
+    k::HcPostArgs hp;
+    hp.x = hc_x;
+    hp.post = post;
+    hp.comb = comb;
+    hp.hc = hc;
+    k::moe_combine_partial_link(pair_out, pidx, reinterpret_cast<const k::MoePlan*>(plan), tok2u, remote, shared, out,
+                                T, K, dim, S(st), hp);
+  });
+}
+int uh_moe_dispatch_small_remote(const int32_t* sel, const float* wt, int T, int K, int E, int P, int max_tiles,
+                                 int tile_rows, int32_t* plan, int32_t* tiles, int32_t* remote_tiles, int32_t* eidx,
+                                 float* ewt, int32_t* row_expert, int32_t* pidx, const uint8_t* resident,
+                                 const float* ds_logits, const float* ds_bias, float route_scale, int remote, int qin,
+                                 int32_t* tok2u, int32_t* u2t, int32_t* p2u, int32_t* u2p, int32_t* plan_dst,
+                                 int32_t* tiles_dst, float* w_dst, int32_t* e_dst, const uint16_t* x, int dim,
+                                 uint16_t* x_dst, uint8_t* q_dst, uint8_t* qs_dst, uint32_t* req_flag,
+                                 uint32_t req_value, void* st) {
+  return guard([&] {
+    k::MoeSmallArgs a{};
+    a.sel = sel;
+    a.wt = wt;
+    a.T = T;
+    a.K = K;
+    a.resident = resident;
+    a.E = E;
+    a.P = P;
+    a.max_tiles = max_tiles;
+    a.tile_rows = tile_rows;
+    a.plan = reinterpret_cast<k::MoePlan*>(plan);
+    a.lt = reinterpret_cast<k::Exl3Tile*>(tiles);
+    a.rtl = reinterpret_cast<k::Exl3Tile*>(remote_tiles);
+    a.eidx = eidx;
+    a.ewt = ewt;
+    a.row_expert = row_expert;
+    a.pidx = pidx;
+    a.ds_logits = ds_logits;
+    a.ds_bias = ds_bias;
+    a.route_scale = route_scale;
+    a.remote = remote != 0;
+    a.qin = qin != 0;
+    a.tok2u = tok2u;
+    a.u2t = u2t;
+    a.p2u_dst = p2u;
+    a.u2p_dst = u2p;
+    a.plan_dst = reinterpret_cast<k::MoePlan*>(plan_dst);
+    a.tiles_dst = reinterpret_cast<k::Exl3Tile*>(tiles_dst);
+    a.w_dst = w_dst;
+    a.e_dst = e_dst;
+    a.x = x;
+    a.dim = dim;
+    a.x_dst = x_dst;
+    a.q_dst = q_dst;
+    a.qs_dst = qs_dst;
+    a.req_flag = req_flag;
+    a.req_value = req_value;
+    k::moe_dispatch_small(a, S(st));
+  });
+}
 int uh_gemm_grouped_fp8w(const uint16_t* a, const uint8_t* w, const uint8_t* sw, uint16_t* c, int M, int G, int R,
                          int K, void* st) {
   return guard([&] { k::gemm_grouped_fp8w(a, w, sw, c, M, G, R, K, S(st)); });

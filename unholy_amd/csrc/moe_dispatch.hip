@@ -382,11 +382,14 @@ __global__ __launch_bounds__(SMALL_NT) void moe_dispatch_small_kernel(MoeSmallAr
     j = i % K;
     if (a.hist) atomicAdd(&a.hist[e], 1u);
   }
+  // Non-resident experts sort after every resident one: key class ek = e + E (resident first, then the others, each
+  // in ascending id: the reference's plan order). Rows below remote0 = keys below E * T * K.
+  const int ek = (a.resident && live && !a.resident[e]) ? e + E : e;
   __syncthreads();
-  if (live) skey[i] = (e * T + t) * K + j;
+  if (live) skey[i] = (ek * T + t) * K + j;
   __syncthreads();
-  const int mykey = (e * T + t) * K + j, lo = e * T * K, hi = (e + 1) * T * K;
-  int rank = 0, off = 0, cnt = 0;
+  const int mykey = (ek * T + t) * K + j, lo = ek * T * K, hi = (ek + 1) * T * K, lim = E * T * K;
+  int rank = 0, off = 0, cnt = 0, nloc = 0;
   if (live) {
     int q = 0;
     for (; q + 4 <= n; q += 4) {  // the same address in every lane: broadcast reads, four keys at a time
@@ -397,6 +400,7 @@ __global__ __launch_bounds__(SMALL_NT) void moe_dispatch_small_kernel(MoeSmallAr
         rank += kk[u] < mykey;
         off += kk[u] < lo;
         cnt += kk[u] >= lo && kk[u] < hi;
+        nloc += kk[u] < lim;
       }
     }
     for (; q < n; ++q) {
@@ -404,21 +408,31 @@ __global__ __launch_bounds__(SMALL_NT) void moe_dispatch_small_kernel(MoeSmallAr
       rank += kq < mykey;
       off += kq < lo;
       cnt += kq >= lo && kq < hi;
+      nloc += kq < lim;
     }
   }
-  int below = 0;  // token t's picks ordered before this one (expert, then selection order)
+  const int remote0 = live ? nloc : 0;  // the same in every live thread; thread 0 is live (n >= 1)
+  // Token t's picks ordered before this one by expert id, then selection order (the reference's sorted picks):
+  // the expert id comes back from the key, whose class puts non-resident experts at e + E.
+  int below = 0;
   if (live)
     for (int q = 0; q < K; ++q) {
-      const int kq = skey[t * K + q];
-      below += kq < mykey;
+      const int cq = skey[t * K + q] / (T * K), eq = cq >= E ? cq - E : cq;
+      below += eq < e || (eq == e && q < j);
     }
   const int p = rank;
-  __shared__ int srow_e[SMALL_NT], srow_left[SMALL_NT];
+  __shared__ int srow_e[SMALL_NT], srow_left[SMALL_NT], spidx[SMALL_NT];
+  __shared__ int stok[kMoeSmallMaxTokens], su2t[kMoeSmallMaxTokens], sU;
   if (live) {
     a.eidx[p] = t;
     a.ewt[p] = w;
     a.row_expert[p] = e;
     a.pidx[size_t(t) * K + below] = p;
+    spidx[t * K + below] = p;
+    if (a.remote && p >= remote0) {  // stage_remote: the remote rows' weights and experts
+      a.w_dst[p] = w;
+      a.e_dst[p] = e;
+    }
     srow_e[p] = e;
     // rows of the expert's run from here, or 0 when this row does not start a tile
     srow_left[p] = (p - off) % a.tile_rows == 0 ? cnt - (p - off) : 0;
@@ -426,15 +440,80 @@ __global__ __launch_bounds__(SMALL_NT) void moe_dispatch_small_kernel(MoeSmallAr
   __syncthreads();
   // Now thread r stands for pair row r: tiles are numbered in row order.
   const int r = tid, left = r < n ? srow_left[r] : 0;
+  // Local and remote tile starts counted in one scan: the low half-word counts local ones, the high one remote ones
+  // (at most 256 rows each). Local rows precede remote rows, so both numberings are in row order.
   int ntiles;
-  const int tile = block_exclusive_scan<SMALL_NT>(left > 0 ? 1 : 0, &ntiles, lds);
-  if (left > 0 && tile < a.max_tiles) a.lt[tile] = Exl3Tile{srow_e[r], r, min(a.tile_rows, left)};
+  const int tile = block_exclusive_scan<SMALL_NT>(left > 0 ? (r < remote0 ? 1 : 1 << 16) : 0, &ntiles, lds);
+  if (left > 0) {
+    const Exl3Tile tl{srow_e[r], r, min(a.tile_rows, left)};
+    if (r < remote0) {
+      if ((tile & 0xffff) < a.max_tiles) a.lt[tile & 0xffff] = tl;
+    } else if ((tile >> 16) < a.max_tiles) {
+      a.rtl[tile >> 16] = tl;
+      if (a.remote) a.tiles_dst[tile >> 16] = tl;  // stage_remote: the remote tiles
+    }
+  }
+  __shared__ int srem0;
+  if (tid == 0) srem0 = remote0;
+  // remote_tokens (moe_dispatch.hip:149-203) for T <= 32: token t has a remote pair when one of its rows is
+  // >= remote0; those tokens, in order, get compact indices.
+  if (a.remote && a.qin && tid < T) {
+    bool f = false;
+    for (int q = 0; q < K; ++q) f = f || skey[tid * K + q] >= lim;
+    stok[tid] = f ? 1 : 0;
+  }
+  __syncthreads();
+  const int R0 = srem0;
+  if (a.remote && a.qin) {
+    if (tid < T) {
+      int ex = 0;
+      for (int q = 0; q < tid; ++q) ex += stok[q];
+      const bool f = stok[tid] != 0;
+      a.tok2u[tid] = f ? ex : -1;
+      if (f) {
+        a.u2t[ex] = tid;
+        su2t[ex] = tid;
+        if (a.u2p_dst)
+          for (int q = 0; q < K; ++q) {
+            const int pq = spidx[tid * K + q];
+            a.u2p_dst[size_t(ex) * K + q] = pq >= R0 ? pq : -1;
+          }
+      }
+      if (tid == T - 1) sU = ex + (f ? 1 : 0);
+    }
+    if (live && p >= R0) {  // stok still holds the flags  // p2u[p] = the compact index of row p's token
+      int ex = 0;
+      for (int q = 0; q < t; ++q) ex += stok[q];
+      a.p2u_dst[p] = ex;
+    }
+  } else if (tid == 0) {
+    sU = 0;
+  }
+  __syncthreads();
+  const int U = sU;
+  const MoePlan pl{a.P, R0, min(ntiles & 0xffff, a.max_tiles), min(ntiles >> 16, a.max_tiles), U};
   if (tid == 0) {
-    a.plan->P = a.P;
-    a.plan->remote0 = n;
-    a.plan->n_local_tiles = min(ntiles, a.max_tiles);
-    a.plan->n_remote_tiles = 0;
-    a.plan->n_remote_tokens = 0;
+    *a.plan = pl;
+    if (a.remote) *a.plan_dst = pl;  // stage_remote: the plan
+  }
+  if (!a.remote) return;
+  if (a.x_dst) {  // copy_remote_tokens: the remote tokens' rows of x, 16 bytes per thread
+    const int cols = a.dim / 8;
+    for (int i2 = tid; i2 < U * cols; i2 += SMALL_NT) {
+      const int u = i2 / cols, c = i2 % cols;
+      reinterpret_cast<uint4*>(a.x_dst + size_t(u) * a.dim)[c] =
+          reinterpret_cast<const uint4*>(a.x + size_t(su2t[u]) * a.dim)[c];
+    }
+  }
+  if (a.q_dst) {  // quant_remote_tokens: the same rows as e4m3 codes + e8m0 exponents
+    const size_t items = size_t(U) * (a.dim / 8);
+    for (size_t base = 0; base < items; base += SMALL_NT)
+      quant_token_item(a.x, a.dim, su2t, a.q_dst, a.qs_dst, base + tid, items);
+  }
+  __threadfence_system();
+  if (a.req_flag) {  // the remote side's request flag, after every write above
+    __syncthreads();
+    if (tid == 0) __hip_atomic_store(a.req_flag, a.req_value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
   }
 }
 
@@ -495,6 +574,206 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const bf16* __restrict
   *reinterpret_cast<uint4*>(out + size_t(t) * dim + d) = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// ---- remote experts: staging, compact tokens, partial combines (moe_dispatch.hip:111-278) ---------------------------
+// Device-side extents (plan) with grids sized for the maximum: grid-stride loops over 16-byte units.
+__global__ __launch_bounds__(256) void copy_rows16_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst,
+                                                          const MoePlan* __restrict__ plan, int units_per_row,
+                                                          int mode) {
+  // mode 0: rows [remote0, P) to the same rows; 1: n_remote_tokens rows from src to rows remote0.. of dst
+  const MoePlan pl = *plan;
+  const size_t r0 = size_t(pl.remote0) * units_per_row;
+  const size_t n = size_t(mode == 0 ? pl.P - pl.remote0 : pl.n_remote_tokens) * units_per_row;
+  const uint4* s = mode == 0 ? src + r0 : src;
+  uint4* o = dst + r0;
+  for (size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
+    o[i] = s[i];
+  __threadfence_system();
+}
+
+__global__ __launch_bounds__(256) void stage_remote_kernel(const MoePlan* __restrict__ plan,
+                                                           const Exl3Tile* __restrict__ rtiles,
+                                                           const float* __restrict__ ewt,
+                                                           const int32_t* __restrict__ row_expert,
+                                                           MoePlan* __restrict__ plan_dst,
+                                                           Exl3Tile* __restrict__ tiles_dst, float* __restrict__ w_dst,
+                                                           int32_t* __restrict__ e_dst, bool with_plan) {
+  const MoePlan pl = *plan;
+  const int tid = blockIdx.x * blockDim.x + threadIdx.x, nt = gridDim.x * blockDim.x;
+  if (with_plan) {
+    if (tid == 0) *plan_dst = pl;
+    for (int i = tid; i < pl.n_remote_tiles; i += nt) tiles_dst[i] = rtiles[i];
+  }
+  for (int i = pl.remote0 + tid; i < pl.P; i += nt) {
+    w_dst[i] = ewt[i];
+    e_dst[i] = row_expert[i];
+  }
+  __threadfence_system();
+}
+
+// One workgroup: an exclusive scan of "has a remote pair" over the tokens, 1024 at a time, then p2u over the remote
+// rows (tok2u is read back after the barrier that ends the scan; this workgroup wrote it).
+constexpr int RT_NT = 1024;
+__global__ __launch_bounds__(RT_NT) void remote_tokens_kernel(const int32_t* __restrict__ pidx,
+                                                              const int32_t* __restrict__ eidx, int T, int K,
+                                                              MoePlan* __restrict__ plan, int32_t* __restrict__ tok2u,
+                                                              int32_t* __restrict__ u2t, int32_t* __restrict__ p2u,
+                                                              int32_t* __restrict__ u2p) {
+  __shared__ int lds[RT_NT / 64 + 1];
+  const int r0 = plan->remote0, P = plan->P, tid = threadIdx.x;
+  int carry = 0;
+  for (int base = 0; base < T; base += RT_NT) {
+    const int t = base + tid;
+    bool f = false;
+    if (t < T)
+      for (int j = 0; j < K; ++j) f = f || pidx[size_t(t) * K + j] >= r0;
+    int tot;
+    const int u = carry + block_exclusive_scan<RT_NT>(f ? 1 : 0, &tot, lds);
+    if (t < T) {
+      tok2u[t] = f ? u : -1;
+      if (f) {
+        u2t[u] = t;
+        if (u2p)
+          for (int j = 0; j < K; ++j) {
+            const int p = pidx[size_t(t) * K + j];
+            u2p[size_t(u) * K + j] = p >= r0 ? p : -1;
+          }
+      }
+    }
+    carry += tot;
+  }
+  __syncthreads();
+  if (tid == 0) plan->n_remote_tokens = carry;
+  for (int p = r0 + tid; p < P; p += RT_NT) p2u[p] = tok2u[eidx[p]];
+  __threadfence_system();
+}
+
+__device__ __forceinline__ void add_bf16x8(float (&acc)[8], const bf16* p) {
+  const uint4 v = *reinterpret_cast<const uint4*>(p);
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    acc[2 * q] += __uint_as_float(w[q] << 16);
+    acc[2 * q + 1] += __uint_as_float(w[q] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ uint4 pack_bf16x8(const float (&acc)[8]) {
+  uint32_t o[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) o[q] = uint32_t(f32_to_bf16(acc[2 * q])) | uint32_t(f32_to_bf16(acc[2 * q + 1])) << 16;
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// dst[u] = bf16(sum of token u's remote pair rows, fp32 adds from 0 in pick order): items (u, 8 columns).
+__global__ __launch_bounds__(256) void remote_combine_kernel(const bf16* __restrict__ pair_out,
+                                                             const int32_t* __restrict__ u2p,
+                                                             const MoePlan* __restrict__ plan, bf16* __restrict__ dst,
+                                                             int K, int dim) {
+  const int cols = dim / 8;
+  const size_t n = size_t(plan->n_remote_tokens) * cols;
+  for (size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
+    const int u = int(i / cols), c = int(i % cols);
+    float acc[8] = {};
+    for (int j = 0; j < K; ++j) {
+      const int p = u2p[size_t(u) * K + j];
+      if (p >= 0) add_bf16x8(acc, pair_out + size_t(p) * dim + 8 * c);
+    }
+    *reinterpret_cast<uint4*>(dst + size_t(u) * dim + 8 * c) = pack_bf16x8(acc);
+  }
+  __threadfence_system();
+}
+
+// out[t] = bf16(local pair rows (p < remote0, pick order) + the token's remote row + shared[t]), fp32 adds from 0;
+// remote null: the remote rows are pair_out's rows from remote0 on. With hp.x: the mHC post-mix of each output value
+// into the token's hc streams in place, x[t][j][d] = bf16(fma(post[t][j], o, sum_i comb[t][i][j] * x[t][i][d])),
+// the sum an fma chain over i (dev.hip.hpp:185-201). V = 8: 16-byte loads and stores; V = 1: one column.
+template <int V>
+__global__ __launch_bounds__(256) void combine_partial_kernel(const bf16* __restrict__ pair_out,
+                                                              const int32_t* __restrict__ pidx,
+                                                              const MoePlan* __restrict__ plan,
+                                                              const int32_t* __restrict__ tok2u,
+                                                              const bf16* __restrict__ remote,
+                                                              const bf16* __restrict__ shared, bf16* __restrict__ out,
+                                                              int K, int dim, HcPostArgs hp) {
+  const int t = blockIdx.y, d = (blockIdx.x * 256 + threadIdx.x) * V;
+  if (d >= dim) return;
+  const int r0 = plan->remote0, u = tok2u[t];
+  const bf16* rem = remote ? remote : pair_out + size_t(r0) * dim;
+  float acc[8] = {};
+  const auto add = [&](const bf16* p) {
+    if constexpr (V == 8) {
+      add_bf16x8(acc, p);
+    } else {
+      acc[0] += bf16_to_f32(*p);
+    }
+  };
+  for (int j = 0; j < K; ++j) {
+    const int p = pidx[size_t(t) * K + j];
+    if (p < r0) add(pair_out + size_t(p) * dim + d);
+  }
+  if (u >= 0) add(rem + size_t(u) * dim + d);
+  if (shared) add(shared + size_t(t) * dim + d);
+  float o[8];
+  if constexpr (V == 8) {
+    const uint4 ov = pack_bf16x8(acc);
+    *reinterpret_cast<uint4*>(out + size_t(t) * dim + d) = ov;
+    const uint32_t w[4] = {ov.x, ov.y, ov.z, ov.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      o[2 * q] = __uint_as_float(w[q] << 16);
+      o[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+    }
+  } else {
+    const bf16 ob = f32_to_bf16(acc[0]);
+    out[size_t(t) * dim + d] = ob;
+    o[0] = bf16_to_f32(ob);
+  }
+  if (!hp.x) return;
+  const int hc = hp.hc;
+  float r[4][8];
+  for (int i = 0; i < hc; ++i) {
+    const bf16* xp = hp.x + (size_t(t) * hc + i) * dim + d;
+    if constexpr (V == 8) {
+      const uint4 v = *reinterpret_cast<const uint4*>(xp);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        r[i][2 * q] = __uint_as_float(w[q] << 16);
+        r[i][2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+      }
+    } else {
+      r[i][0] = bf16_to_f32(*xp);
+    }
+  }
+  for (int j = 0; j < hc; ++j) {
+    const float pj = hp.post[size_t(t) * hc + j];
+    float y[8];
+#pragma unroll
+    for (int c = 0; c < V; ++c) {
+      float s = 0.0f;
+      for (int i = 0; i < hc; ++i) s = fmaf(hp.comb[(size_t(t) * hc + i) * hc + j], r[i][c], s);
+      y[c] = fmaf(pj, o[c], s);
+    }
+    bf16* xp = hp.x + (size_t(t) * hc + j) * dim + d;
+    if constexpr (V == 8) {
+      *reinterpret_cast<uint4*>(xp) = pack_bf16x8(y);
+    } else {
+      *xp = f32_to_bf16(y[0]);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void gather_tokens16_kernel(const bf16* __restrict__ x, int dim,
+                                                              const int32_t* __restrict__ u2t,
+                                                              const MoePlan* __restrict__ plan, bf16* __restrict__ dst) {
+  const int cols = dim / 8;
+  const size_t n = size_t(plan->n_remote_tokens) * cols;
+  for (size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
+    const size_t u = i / cols, c = i % cols;
+    reinterpret_cast<uint4*>(dst + u * dim)[c] = reinterpret_cast<const uint4*>(x + size_t(u2t[u]) * dim)[c];
+  }
+  __threadfence_system();
+}
+
 }  // namespace
 
 // ---- entry points ---------------------------------------------------------------------------------------------------
@@ -546,13 +825,114 @@ void moe_dispatch_small(const MoeSmallArgs& a, hipStream_t st) {
   if (a.E <= 0 || a.E > 1024) throw std::runtime_error("moe_dispatch_small: E in [1, 1024]");
   if (a.P != a.T * a.K) throw std::runtime_error("moe_dispatch_small: P != T * K");
   if (a.tile_rows <= 0) throw std::runtime_error("moe_dispatch_small: tile_rows");
-  if (a.remote || a.qin || a.x_dst || a.q_dst || a.req_flag || a.plan_dst)
-    throw std::runtime_error("moe_dispatch_small: remote experts are not supported on one GPU");
-  if (a.resident) throw std::runtime_error("moe_dispatch_small: resident mask not supported (all experts local)");
+  if (a.resident && !a.rtl) throw std::runtime_error("moe_dispatch_small: a resident mask needs remote tiles");
+  if (a.remote) {
+    if (!a.resident) throw std::runtime_error("moe_dispatch_small: remote without a resident mask");
+    if (!a.plan_dst || !a.tiles_dst || !a.w_dst || !a.e_dst) throw std::runtime_error("moe_dispatch_small: staging");
+    if (a.qin && (!a.tok2u || !a.u2t || !a.p2u_dst)) throw std::runtime_error("moe_dispatch_small: remote tokens");
+    if ((a.x_dst || a.q_dst) && !a.qin) throw std::runtime_error("moe_dispatch_small: x_dst / q_dst need qin");
+    if ((a.x_dst || a.q_dst) && (!a.x || a.dim <= 0 || reinterpret_cast<uintptr_t>(a.x) % 16))
+      throw std::runtime_error("moe_dispatch_small: x (16-byte aligned) and dim");
+    if (a.x_dst && (a.dim % 8 || reinterpret_cast<uintptr_t>(a.x_dst) % 16))
+      throw std::runtime_error("moe_dispatch_small: x_dst 16-byte aligned, dim % 8");
+    if (a.q_dst && (a.dim % 128 || !a.qs_dst)) throw std::runtime_error("moe_dispatch_small: q_dst needs dim % 128");
+  } else if (a.qin || a.x_dst || a.q_dst || a.req_flag || a.plan_dst) {
+    throw std::runtime_error("moe_dispatch_small: remote-side outputs without remote");
+  }
   if (!a.sel || !a.wt || !a.plan || !a.lt || !a.eidx || !a.ewt || !a.row_expert || !a.pidx)
     throw std::runtime_error("moe_dispatch_small: null output");
   moe_dispatch_small_kernel<<<1, SMALL_NT, 0, st>>>(a);
   UH_CHECK_LAUNCH();
+}
+
+namespace {
+unsigned stride_grid(size_t units) { return unsigned(std::max<size_t>(1, std::min<size_t>(cdiv(units, 256), 1024))); }
+bool a16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+}  // namespace
+
+void stage_remote(const MoePlan* plan, const Exl3Tile* rtiles, const float* ewt, const int32_t* row_expert,
+                  MoePlan* plan_dst, Exl3Tile* tiles_dst, float* w_dst, int32_t* e_dst, int max_rows, hipStream_t st) {
+  if (!plan || !rtiles || !ewt || !row_expert || !plan_dst || !tiles_dst || !w_dst || !e_dst)
+    throw std::runtime_error("stage_remote: null operand");
+  stage_remote_kernel<<<stride_grid(std::max(max_rows, 1)), 256, 0, st>>>(plan, rtiles, ewt, row_expert, plan_dst,
+                                                                          tiles_dst, w_dst, e_dst, true);
+  UH_CHECK_LAUNCH();
+}
+void copy_remote_meta(const float* ewt, const int32_t* row_expert, float* w_dst, int32_t* e_dst, const MoePlan* plan,
+                      int max_rows, hipStream_t st) {
+  if (!plan || !ewt || !row_expert || !w_dst || !e_dst) throw std::runtime_error("copy_remote_meta: null operand");
+  stage_remote_kernel<<<stride_grid(std::max(max_rows, 1)), 256, 0, st>>>(plan, nullptr, ewt, row_expert, nullptr,
+                                                                          nullptr, w_dst, e_dst, false);
+  UH_CHECK_LAUNCH();
+}
+void copy_remote_rows(const uint16_t* src, uint16_t* dst, const MoePlan* plan, int dim, int max_rows, hipStream_t st) {
+  if (dim <= 0 || dim % 8 || !a16(src) || !a16(dst) || !plan)
+    throw std::runtime_error("copy_remote_rows: dim % 8, 16-byte aligned rows");
+  copy_rows16_kernel<<<stride_grid(size_t(std::max(max_rows, 1)) * (dim / 8)), 256, 0, st>>>(
+      reinterpret_cast<const uint4*>(src), reinterpret_cast<uint4*>(dst), plan, dim / 8, 0);
+  UH_CHECK_LAUNCH();
+}
+void copy_remote_partial(const uint16_t* src, uint16_t* dst, const MoePlan* plan, int dim, int max_tokens,
+                         hipStream_t st) {
+  if (dim <= 0 || dim % 8 || !a16(src) || !a16(dst) || !plan)
+    throw std::runtime_error("copy_remote_partial: dim % 8, 16-byte aligned rows");
+  copy_rows16_kernel<<<stride_grid(size_t(std::max(max_tokens, 1)) * (dim / 8)), 256, 0, st>>>(
+      reinterpret_cast<const uint4*>(src), reinterpret_cast<uint4*>(dst), plan, dim / 8, 1);
+  UH_CHECK_LAUNCH();
+}
+void copy_remote_tokens(const uint16_t* x, int dim, const int32_t* u2t, const MoePlan* plan, uint16_t* dst,
+                        int max_tokens, hipStream_t st) {
+  if (max_tokens <= 0) return;
+  if (dim <= 0 || dim % 8 || !a16(x) || !a16(dst) || !u2t || !plan)
+    throw std::runtime_error("copy_remote_tokens: dim % 8, 16-byte aligned rows");
+  gather_tokens16_kernel<<<stride_grid(size_t(max_tokens) * (dim / 8)), 256, 0, st>>>(x, dim, u2t, plan, dst);
+  UH_CHECK_LAUNCH();
+}
+void remote_tokens(const int32_t* pidx, const int32_t* eidx, int T, int K, MoePlan* plan, int32_t* tok2u,
+                   int32_t* u2t, int32_t* p2u_dst, int32_t* u2p_dst, hipStream_t st) {
+  if (T < 0 || K <= 0) throw std::runtime_error("remote_tokens: T >= 0, K >= 1");
+  if (!pidx || !eidx || !plan || !tok2u || !u2t || !p2u_dst) throw std::runtime_error("remote_tokens: null operand");
+  remote_tokens_kernel<<<1, RT_NT, 0, st>>>(pidx, eidx, T, K, plan, tok2u, u2t, p2u_dst, u2p_dst);
+  UH_CHECK_LAUNCH();
+}
+void remote_combine(const uint16_t* pair_out, const int32_t* u2p, const MoePlan* plan, uint16_t* dst, int K, int dim,
+                    int max_tokens, hipStream_t st) {
+  if (max_tokens <= 0) return;
+  if (dim <= 0 || dim % 8 || !a16(pair_out) || !a16(dst)) throw std::runtime_error("remote_combine: dim % 8");
+  if (!u2p || !plan || K <= 0) throw std::runtime_error("remote_combine: null operand");
+  remote_combine_kernel<<<stride_grid(size_t(max_tokens) * (dim / 8)), 256, 0, st>>>(pair_out, u2p, plan, dst, K,
+                                                                                      dim);
+  UH_CHECK_LAUNCH();
+}
+namespace {
+void launch_combine_partial(const uint16_t* pair_out, const int32_t* pidx, const MoePlan* plan, const int32_t* tok2u,
+                            const uint16_t* remote, const uint16_t* shared, uint16_t* out, int T, int K, int dim,
+                            const HcPostArgs& hp, hipStream_t st) {
+  if (T <= 0) return;
+  if (dim <= 0 || K <= 0 || !pair_out || !pidx || !plan || !tok2u || !out)
+    throw std::runtime_error("moe_combine_partial: null operand or shape");
+  if (hp.x && (!hp.post || !hp.comb || hp.hc < 1 || hp.hc > 4))
+    throw std::runtime_error("moe_combine_partial: mHC post-mix needs post, comb and 1 <= hc <= 4");
+  const bool v8 = dim % 8 == 0 && a16(pair_out) && a16(out) && (!remote || a16(remote)) && (!shared || a16(shared)) &&
+                  (!hp.x || a16(hp.x));
+  if (v8)
+    combine_partial_kernel<8><<<dim3(unsigned(cdiv(size_t(dim / 8), 256)), unsigned(T)), 256, 0, st>>>(
+        pair_out, pidx, plan, tok2u, remote, shared, out, K, dim, hp);
+  else
+    combine_partial_kernel<1><<<dim3(unsigned(cdiv(size_t(dim), 256)), unsigned(T)), 256, 0, st>>>(
+        pair_out, pidx, plan, tok2u, remote, shared, out, K, dim, hp);
+  UH_CHECK_LAUNCH();
+}
+}  // namespace
+void moe_combine_partial(const uint16_t* pair_out, const int32_t* pidx, const MoePlan* plan, const int32_t* tok2u,
+                         const uint16_t* shared, uint16_t* out, int T, int K, int dim, hipStream_t st) {
+  launch_combine_partial(pair_out, pidx, plan, tok2u, nullptr, shared, out, T, K, dim, HcPostArgs{}, st);
+}
+void moe_combine_partial_link(const uint16_t* pair_out, const int32_t* pidx, const MoePlan* plan, const int32_t* tok2u,
+                              const uint16_t* remote, const uint16_t* shared, uint16_t* out, int T, int K, int dim,
+                              hipStream_t st, const HcPostArgs& hp) {
+  if (!remote) throw std::runtime_error("moe_combine_partial_link: null remote rows");
+  launch_combine_partial(pair_out, pidx, plan, tok2u, remote, shared, out, T, K, dim, hp, st);
 }
 
 void route(const float* logits, const float* bias, const int32_t* tid2eid, const int32_t* ids, int32_t* sel,

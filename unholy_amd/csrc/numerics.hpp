@@ -160,6 +160,34 @@ __device__ __forceinline__ void fp8_codes8(const float (&v)[8], float sc, uint32
   hi = e4m3x4(clamp448(v[4] / sc), clamp448(v[5] / sc), clamp448(v[6] / sc), clamp448(v[7] / sc));
 }
 
+// act_quant_fp8 (block 128) of compact token rows: item `it` of items = U * dim / 8 is 8 values of row x[u2t[u]]
+// (16-byte load), 16 consecutive items one 128-block (amax a DPP row max). Every lane of a 16-lane group must call
+// it, items past the end included (they clamp to the last item for the max and store nothing).
+__device__ __forceinline__ void quant_token_item(const uint16_t* __restrict__ x, int dim,
+                                                 const int32_t* __restrict__ u2t, uint8_t* __restrict__ q,
+                                                 uint8_t* __restrict__ s, size_t it, size_t items) {
+  const size_t ic = it < items ? it : items - 1;
+  const int per_row = dim / 8;
+  const int u = int(ic / per_row), rem = int(ic % per_row), b = rem >> 4, l = rem & 15;
+  const uint4 raw = *reinterpret_cast<const uint4*>(x + size_t(u2t[u]) * dim + b * 128 + 8 * l);
+  const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
+  float v[8], am = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(rw[i] << 16);
+    v[2 * i + 1] = __uint_as_float(rw[i] & 0xffff0000u);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
+  am = row16_max(am);
+  if (it >= items) return;
+  const Fp8Block blk = fp8_block_scale(am);
+  uint32_t c0, c1;
+  fp8_codes8(v, blk, c0, c1);
+  *reinterpret_cast<uint2*>(q + size_t(u) * dim + b * 128 + 8 * l) = make_uint2(c0, c1);
+  if (l == 0) s[size_t(u) * (dim / 128) + b] = blk.se;
+}
+
 // SwiGLU with the clamp and optional routing weight (ref_moe.hip:66-72): x = silu(min(g, l)) * clamp(u, +-l),
 // then w * x; limit <= 0 turns the clamp off.
 __device__ __forceinline__ float swiglu_value(float g, float u, float w, bool has_w, float limit) {

@@ -121,29 +121,9 @@ __global__ __launch_bounds__(256) void quant_remote_tokens_kernel(const bf16* __
                                                                   const int32_t* __restrict__ u2t,
                                                                   const MoePlan* __restrict__ plan,
                                                                   uint8_t* __restrict__ q, uint8_t* __restrict__ s) {
-  const int per_row = dim / 8;
-  const size_t items = size_t(plan->n_remote_tokens) * per_row;
-  for (size_t base = size_t(blockIdx.x) * 256; base < items; base += size_t(gridDim.x) * 256) {
-    const size_t it = min(base + threadIdx.x, items - 1);
-    const int u = int(it / per_row), rem = int(it % per_row), b = rem >> 4, l = rem & 15;
-    const uint4 raw = *reinterpret_cast<const uint4*>(x + size_t(u2t[u]) * dim + b * 128 + 8 * l);
-    const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
-    float v[8], am = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[2 * i] = __uint_as_float(rw[i] << 16);
-      v[2 * i + 1] = __uint_as_float(rw[i] & 0xffff0000u);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
-    am = row16_max(am);
-    if (base + threadIdx.x >= items) continue;
-    const Fp8Block blk = fp8_block_scale(am);
-    uint32_t c0, c1;
-    fp8_codes8(v, blk, c0, c1);
-    *reinterpret_cast<uint2*>(q + size_t(u) * dim + b * 128 + 8 * l) = make_uint2(c0, c1);
-    if (l == 0) s[size_t(u) * (dim / 128) + b] = blk.se;
-  }
+  const size_t items = size_t(plan->n_remote_tokens) * (dim / 8);
+  for (size_t base = size_t(blockIdx.x) * 256; base < items; base += size_t(gridDim.x) * 256)
+    quant_token_item(x, dim, u2t, q, s, base + threadIdx.x, items);
 }
 
 }  // namespace
