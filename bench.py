@@ -2,7 +2,7 @@
 """Benchmark of the MXFP4 routed-expert FFN on one MI355X (gfx950).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
-    python bench.py --only {decode,single,verify,prefill,fp8,grouped,producers,pack,copy}   # one workload (for profilers), one JSON line
+    python bench.py --only {decode,single,verify,prefill,fp8,grouped,producers,pack,remote,copy}   # one workload (for profilers), one JSON line
 
 A step is one routed-expert FFN over one batch of synthetic tokens: softmax top-6 routing of [T, 256] logits,
 dispatch, fp8 input transform, w1/w3 grouped GEMV with the SwiGLU epilogue, w2 grouped GEMV, combine to bf16
@@ -253,10 +253,62 @@ def producers_entry(rows, t_norm, t_rq):
             "quant_remote_tokens": {"ms": t_rq, "GBps": b_rq / (t_rq * 1e-3) / 1e9}}
 
 
+def bench_remote(T, steps, warmup, rng):
+    """The remote-expert transport kernels at D = 4096, K = 6, E = 256 with every other expert held elsewhere (the
+    remote side's buffers are device buffers on one GPU). T <= 32: moe_dispatch_small with every remote-side output
+    (staging, compact tokens, their bf16 rows and fp8 codes). All T: remote_tokens, remote_combine and
+    moe_combine_partial_link. Returns ms per call and algorithmic bytes per call of each."""
+    import oracle
+    from unholy_amd import call
+    from unholy_amd.device import DeviceBuffer
+    E_, K_ = 256, 6
+    P = T * K_
+    sel = np.stack([rng.permutation(E_)[:K_] for _ in range(T)]).astype(np.int32)
+    wt = rng.random((T, K_)).astype(np.float32)
+    resident = (np.arange(E_) % 2).astype(np.uint8)
+    d = oracle.dispatch(sel, wt, E_, 8 if T <= 32 else 128, resident)
+    rt = oracle.remote_tokens(d["pidx"], d["eidx"], d["plan"][1])
+    U, r0 = rt["U"], int(d["plan"][1])
+    plan = d["plan"].copy()
+    plan[4] = U
+    dv = DeviceBuffer.from_array
+    dplan, dpidx, deidx, dtok2u = dv(plan), dv(d["pidx"]), dv(d["eidx"]), dv(rt["tok2u"])
+    tok2u, u2t, p2u, u2p = DeviceBuffer(T * 4), DeviceBuffer(T * 4), DeviceBuffer(P * 4), DeviceBuffer(P * 4)
+    pair_out = dv(to_bf16(rng.standard_normal((P, D), dtype=np.float32)))
+    shared = dv(to_bf16(rng.standard_normal((T, D), dtype=np.float32)))
+    partial, out = DeviceBuffer(T * D * 2), DeviceBuffer(T * D * 2)
+    du2p = dv(rt["u2p"] if U else np.full((1, K_), -1, np.int32))
+    res = {"T": T, "remote0": r0, "remote_tokens_U": U}
+    # remote_tokens rewrites plan[4] with the same U, so the later kernels see the oracle's count
+    t = time_graph(lambda i, st: call("uh_remote_tokens", dpidx, deidx, T, K_, dplan, tok2u, u2t, p2u, u2p,
+                                      st.handle), steps, warmup)
+    res["remote_tokens"] = {"ms": t, "bytes": P * 4 * 2 + T * 4 * 2 + (P - r0) * 4 + U * K_ * 4}
+    t = time_graph(lambda i, st: call("uh_remote_combine", pair_out, du2p, dplan, partial, K_, D, T, st.handle),
+                   steps, warmup)
+    b = (P - r0) * D * 2 + U * D * 2
+    res["remote_combine"] = {"ms": t, "bytes": b, "GBps": b / (t * 1e-3) / 1e9}
+    t = time_graph(lambda i, st: call("uh_moe_combine_partial_link", pair_out, dpidx, dplan, dtok2u, partial, shared,
+                                      out, T, K_, D, None, None, None, 0, st.handle), steps, warmup)
+    b = r0 * D * 2 + U * D * 2 + T * D * 2 * 2
+    res["moe_combine_partial_link"] = {"ms": t, "bytes": b, "GBps": b / (t * 1e-3) / 1e9}
+    if T <= 32:
+        mt = P + E_
+        o = [DeviceBuffer(n) for n in (20, mt * 12, mt * 12, P * 4, P * 4, P * 4, P * 4, 20, mt * 12, P * 4,
+                                       P * 4, T * D * 2, T * D, T * D // 128, 4)]
+        x, dsel, dwt, dres = dv(to_bf16(rng.standard_normal((T, D), dtype=np.float32))), dv(sel), dv(wt), \
+            dv(resident)
+        t = time_graph(lambda i, st: call(
+            "uh_moe_dispatch_small_remote", dsel, dwt, T, K_, E_, P, mt, 8, o[0], o[1], o[2], o[3], o[4], o[5], o[6],
+            dres, None, None, 0.0, 1, 1, tok2u, u2t, p2u, u2p, o[7], o[8], o[9], o[10], x, D, o[11], o[12], o[13],
+            o[14], i + 1, st.handle), steps, warmup)
+        res["moe_dispatch_small_remote"] = {"ms": t}
+    return res
+
+
 def bench_pack(n_experts=16, reps=3):
     """The expert pack's loader: a pack of n_experts experts of the headline shape (13.4 MB each) written to a
-    temporary file (its pages stay in the host's page cache), then its slots loaded into device memory through the
-    pinned double-buffered staging, with and without the per-slot xxh64 check. Returns GB/s of slot bytes (best of
+    temporary file (its pages stay in the host's page cache), then its slots loaded into device memory by the
+    loader's reader threads through pinned staging, with and without the per-slot xxh64 check. Returns GB/s of slot bytes (best of
     reps), host page cache to HBM."""
     import ctypes
     import tempfile
@@ -340,6 +392,10 @@ def run_only(name, args, rng):
             call("uh_memcpy_d2d", dst, src, n, None)
         synchronize()
         return {"workload": "copy", "bytes_per_copy": n, "copies": 4}
+    if name == "remote":
+        rng = np.random.default_rng(5)
+        return {"remote_transport_T8": bench_remote(8, args.steps, args.warmup, rng),
+                "remote_transport_T4096": bench_remote(4096, args.steps, args.warmup, rng)}
     if name == "pack":
         return {"expert_pack_load": bench_pack()}
     if name == "producers":
@@ -371,7 +427,7 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["decode", "single", "verify", "prefill", "fp8", "grouped", "producers",
-                                       "pack", "copy"])
+                                       "pack", "remote", "copy"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the MoE expert path runs on a single MI355X in this build "
@@ -456,6 +512,8 @@ def main():
         for r in (8, 4096):
             wl[f"producers_rows{r}"] = producers_entry(r, *bench_producers(r, 64, 16, rng))
         wl["expert_pack_load"] = bench_pack()
+        wl["remote_transport_T8"] = bench_remote(8, 64, 16, rng)
+        wl["remote_transport_T4096"] = bench_remote(4096, 64, 16, rng)
         result["workloads"] = wl
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()

@@ -510,10 +510,12 @@ __global__ __launch_bounds__(SMALL_NT) void moe_dispatch_small_kernel(MoeSmallAr
     for (size_t base = 0; base < items; base += SMALL_NT)
       quant_token_item(a.x, a.dim, su2t, a.q_dst, a.qs_dst, base + tid, items);
   }
-  __threadfence_system();
-  if (a.req_flag) {  // the remote side's request flag, after every write above
-    __syncthreads();
-    if (tid == 0) __hip_atomic_store(a.req_flag, a.req_value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+  // One system-scope release, by wave 0 after the barrier (cumulative over it), then the request flag from the same
+  // wave, so the flag is seen only after every write above.
+  __syncthreads();
+  if (tid < 64) {
+    __threadfence_system();
+    if (a.req_flag && tid == 0) __hip_atomic_store(a.req_flag, a.req_value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
   }
 }
 
@@ -575,7 +577,13 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const bf16* __restrict
 }
 
 // ---- remote experts: staging, compact tokens, partial combines (moe_dispatch.hip:111-278) ---------------------------
-// Device-side extents (plan) with grids sized for the maximum: grid-stride loops over 16-byte units.
+// Device-side extents (plan) with grids sized for the maximum: grid-stride loops over 16-byte units. Each kernel ends
+// with a system-scope release so a host or peer reader of pinned memory sees its writes; one wave per workgroup runs
+// it after a barrier (release is cumulative over the barrier), since each run waits on an L2 write-back.
+__device__ __forceinline__ void fence_system_once() {
+  __syncthreads();
+  if (threadIdx.x < 64) __threadfence_system();
+}
 __global__ __launch_bounds__(256) void copy_rows16_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst,
                                                           const MoePlan* __restrict__ plan, int units_per_row,
                                                           int mode) {
@@ -587,7 +595,7 @@ __global__ __launch_bounds__(256) void copy_rows16_kernel(const uint4* __restric
   uint4* o = dst + r0;
   for (size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
     o[i] = s[i];
-  __threadfence_system();
+  fence_system_once();
 }
 
 __global__ __launch_bounds__(256) void stage_remote_kernel(const MoePlan* __restrict__ plan,
@@ -607,7 +615,7 @@ __global__ __launch_bounds__(256) void stage_remote_kernel(const MoePlan* __rest
     w_dst[i] = ewt[i];
     e_dst[i] = row_expert[i];
   }
-  __threadfence_system();
+  fence_system_once();
 }
 
 // One workgroup: an exclusive scan of "has a remote pair" over the tokens, 1024 at a time, then p2u over the remote
@@ -644,7 +652,7 @@ __global__ __launch_bounds__(RT_NT) void remote_tokens_kernel(const int32_t* __r
   __syncthreads();
   if (tid == 0) plan->n_remote_tokens = carry;
   for (int p = r0 + tid; p < P; p += RT_NT) p2u[p] = tok2u[eidx[p]];
-  __threadfence_system();
+  fence_system_once();
 }
 
 __device__ __forceinline__ void add_bf16x8(float (&acc)[8], const bf16* p) {
@@ -663,23 +671,26 @@ __device__ __forceinline__ uint4 pack_bf16x8(const float (&acc)[8]) {
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
-// dst[u] = bf16(sum of token u's remote pair rows, fp32 adds from 0 in pick order): items (u, 8 columns).
+// dst[u] = bf16(sum of token u's remote pair rows, fp32 adds from 0 in pick order): workgroup (2048-column chunk,
+// token stride), a thread per 8 columns. The closing system-scope fence costs a write-back wait per wave that runs
+// it, so one wave per workgroup runs it and the grid stays small (at most 256 token rows of workgroups, each striding
+// over the compact tokens); rows are stored nontemporal (streamed past the cache).
 __global__ __launch_bounds__(256) void remote_combine_kernel(const bf16* __restrict__ pair_out,
                                                              const int32_t* __restrict__ u2p,
                                                              const MoePlan* __restrict__ plan, bf16* __restrict__ dst,
                                                              int K, int dim) {
-  const int cols = dim / 8;
-  const size_t n = size_t(plan->n_remote_tokens) * cols;
-  for (size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
-    const int u = int(i / cols), c = int(i % cols);
+  const int d = (blockIdx.x * 256 + threadIdx.x) * 8, U = plan->n_remote_tokens;
+  for (int u = blockIdx.y; u < U && d < dim; u += gridDim.y) {
     float acc[8] = {};
     for (int j = 0; j < K; ++j) {
       const int p = u2p[size_t(u) * K + j];
-      if (p >= 0) add_bf16x8(acc, pair_out + size_t(p) * dim + 8 * c);
+      if (p >= 0) add_bf16x8(acc, pair_out + size_t(p) * dim + d);
     }
-    *reinterpret_cast<uint4*>(dst + size_t(u) * dim + 8 * c) = pack_bf16x8(acc);
+    const uint4 o = pack_bf16x8(acc);
+    using u32x4 = unsigned int __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store(u32x4{o.x, o.y, o.z, o.w}, reinterpret_cast<u32x4*>(dst + size_t(u) * dim + d));
   }
-  __threadfence_system();
+  fence_system_once();
 }
 
 // out[t] = bf16(local pair rows (p < remote0, pick order) + the token's remote row + shared[t]), fp32 adds from 0;
@@ -771,7 +782,7 @@ __global__ __launch_bounds__(256) void gather_tokens16_kernel(const bf16* __rest
     const size_t u = i / cols, c = i % cols;
     reinterpret_cast<uint4*>(dst + u * dim)[c] = reinterpret_cast<const uint4*>(x + size_t(u2t[u]) * dim)[c];
   }
-  __threadfence_system();
+  fence_system_once();
 }
 
 }  // namespace
@@ -900,8 +911,9 @@ void remote_combine(const uint16_t* pair_out, const int32_t* u2p, const MoePlan*
   if (max_tokens <= 0) return;
   if (dim <= 0 || dim % 8 || !a16(pair_out) || !a16(dst)) throw std::runtime_error("remote_combine: dim % 8");
   if (!u2p || !plan || K <= 0) throw std::runtime_error("remote_combine: null operand");
-  remote_combine_kernel<<<stride_grid(size_t(max_tokens) * (dim / 8)), 256, 0, st>>>(pair_out, u2p, plan, dst, K,
-                                                                                      dim);
+  remote_combine_kernel<<<dim3(unsigned(cdiv(size_t(dim / 8), 256)), unsigned(std::min(max_tokens, 256))), 256, 0,
+                          st>>>(
+      pair_out, u2p, plan, dst, K, dim);
   UH_CHECK_LAUNCH();
 }
 namespace {
