@@ -34,6 +34,12 @@ void mx_repack_to(const uint8_t* w, const uint8_t* s, uint8_t* tw, uint8_t* ts, 
 // xa[r] = bf16(fq8_128(x[x_rows ? x_rows[r] : r])) for rows whose expert is resident. Ref mx_moe.hpp:33-34.
 void mx_xform_in(const bf16* x, int ldx, const int32_t* row_expert, const uint8_t* const* s_tab, bf16* xa, int P,
                  int K, hipStream_t st, const int32_t* x_rows = nullptr);
+// Ref mx_moe.hpp:36-40: the same xa rows rebuilt from compact fp8 inputs (quant_remote_tokens): row r in
+// [plan->remote0, plan->P) whose expert is resident (s_tab entry non-null; s_tab null: all) takes token p2u[r]'s codes
+// q [U, K] and exponents s [U, K / 128]. Bit-identical to mx_xform_in on the rows those tokens would have been
+// gathered into.
+void mx_xform_in_q(const uint8_t* q, const uint8_t* s, const int32_t* p2u, const MoePlan* plan,
+                   const int32_t* row_expert, const uint8_t* const* s_tab, bf16* xa, int P, int K, hipStream_t st);
 // hh[r] = bf16(fq8_128(bf16(w[r] * silu(min(g, lim)) * clamp(u, +-lim)))). Ref mx_moe.hpp:41-42.
 void mx_swiglu(const bf16* g, const bf16* u, const float* w, const int32_t* row_expert, const uint8_t* const* s_tab,
                bf16* hh, int P, int I, float limit, hipStream_t st);
@@ -104,6 +110,11 @@ void mx_grouped_gemv(const bf16* xa, int K, const Exl3Tile* tiles, int ntiles, c
 // q [P, K] e4m3 + qs [P, K/128] e8m0: act_quant_fp8 of x[x_rows[r]] per 128 (rows of non-resident experts skipped).
 void mx_xform_in_fp8(const bf16* x, int ldx, const int32_t* row_expert, const uint8_t* const* s_tab, uint8_t* q,
                      uint8_t* qs, int P, int K, hipStream_t st, const int32_t* x_rows = nullptr);
+// mx_xform_in_q's rows as the fp8 operand: token p2u[r]'s codes and exponents copied to pair row r of qo / qso
+// (equal to mx_xform_in_fp8 on the gathered rows).
+void mx_xform_in_q_fp8(const uint8_t* q, const uint8_t* s, const int32_t* p2u, const MoePlan* plan,
+                       const int32_t* row_expert, const uint8_t* const* s_tab, uint8_t* qo, uint8_t* qso, int P, int K,
+                       hipStream_t st);
 // mx_grouped_gemv / gemm / gemm_glu with the activations as (q, qs).
 void mx_grouped_gemv_q(const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles, int ntiles,
                        const uint8_t* const* w_tab, const uint8_t* const* s_tab, bf16* out, int ldo, int N,

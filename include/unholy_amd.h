@@ -57,6 +57,14 @@ int uh_mx_repack_to(const uint8_t* w, const uint8_t* s, uint8_t* tw, uint8_t* ts
 /* mx_moe.hpp:33-34 (x_rows may be NULL) */
 int uh_mx_xform_in(const uint16_t* x, int ldx, const int32_t* row_expert, const uint8_t* const* s_tab, uint16_t* xa,
                    int P, int K, void* stream, const int32_t* x_rows);
+/* mx_moe.hpp:36-40: xa rows [plan[1], plan[0]) of resident experts rebuilt from compact fp8 token rows q [U, K] /
+ * s [U, K/128] of token p2u[r]; the _fp8 form (no reference counterpart) copies the codes / exponents to pair rows of
+ * qo [P, K] / qso [P, K/128] instead. */
+int uh_mx_xform_in_q(const uint8_t* q, const uint8_t* s, const int32_t* p2u, const int32_t* plan,
+                     const int32_t* row_expert, const uint8_t* const* s_tab, uint16_t* xa, int P, int K, void* stream);
+int uh_mx_xform_in_q_fp8(const uint8_t* q, const uint8_t* s, const int32_t* p2u, const int32_t* plan,
+                         const int32_t* row_expert, const uint8_t* const* s_tab, uint8_t* qo, uint8_t* qso, int P,
+                         int K, void* stream);
 /* No reference counterpart: mx_xform_in emitting e4m3 codes [P, K] + e8m0 scales [P, K/128] (the MFMA operand). */
 int uh_mx_xform_in_fp8(const uint16_t* x, int ldx, const int32_t* row_expert, const uint8_t* const* s_tab,
                        uint8_t* q, uint8_t* qs, int P, int K, void* stream, const int32_t* x_rows);

@@ -202,3 +202,51 @@ def test_dispatch_small_remote_rejects_inconsistent_args():
     with pytest.raises(UhError, match="need qin"):
         call("uh_moe_dispatch_small_remote", b, b, 2, 2, 8, 4, 12, 8, b, b, b, b, b, b, b, b, None, None, 0.0, 1, 0,
              None, None, None, None, b, b, b, b, b, 128, b, None, None, None, 0, None)
+
+
+@pytest.mark.parametrize("T,K", [(40, 4096), (1, 1024), (300, 2048)])
+def test_xform_in_q_matches_gathered_rows(T, K):
+    """The remote side's input transform from compact fp8 tokens equals mx_xform_in / mx_xform_in_fp8 on the pair
+    rows gathered from the tokens, bit for bit, and the oracle's fake_quant_fp8 / act_quant_fp8 of those rows; rows of
+    experts absent from the table and rows below remote0 untouched."""
+    rng = np.random.default_rng(T + K)
+    E, Kp = 64, 6
+    _, _, resident, d = _routed(rng, T, E, Kp, 0.5)
+    P, r0 = T * Kp, d["plan"][1]
+    rt = oracle.remote_tokens(d["pidx"], d["eidx"], r0)
+    U = rt["U"]
+    x = randn_bf16(rng, (T, K), scale=3.0)
+    plan = d["plan"].copy()
+    plan[4] = U
+    dplan, dx = dev(plan), dev(x)
+    q, qs = DeviceBuffer(max(U, 1) * K), DeviceBuffer(max(U, 1) * K // 128)
+    call("uh_quant_remote_tokens", dx, K, dev(rt["u2t"] if U else np.zeros(1, np.int32)), dplan, q, qs, T, None)
+    # the remote side holds the non-resident experts, except expert `gone` (its rows must stay untouched)
+    held = resident == 0
+    gone = int(np.nonzero(held)[0][0]) if held.any() else -1
+    if gone >= 0:
+        held[gone] = False
+    s_tab = DeviceBuffer.from_array(np.where(held, 0x1000, 0).astype(np.uint64))
+    p2u = np.full(P, 0, np.int32)
+    p2u[r0:] = rt["p2u"][r0:]
+    dp2u, drex = dev(p2u), dev(d["row_expert"])
+    xa = filled((P, K), np.uint16, 0x7E57)
+    call("uh_mx_xform_in_q", q, qs, dp2u, dplan, drex, s_tab, xa, P, K, None)
+    got = xa.download((P, K), np.uint16)
+    live = np.zeros(P, bool)
+    live[r0:] = held[d["row_expert"][r0:]]
+    gathered = x[d["eidx"]]
+    print(f"xform_in_q T={T} K={K}: U={U} rebuilt rows {live.sum()}")
+    assert np.array_equal(got[live], oracle.fake_quant_fp8(gathered[live]))
+    assert (got[~live] == 0x7E57).all()
+    xa2 = filled((P, K), np.uint16, 0x7E57)  # mx_xform_in on the gathered rows, restricted to the same rows
+    tab2 = DeviceBuffer.from_array(np.where(held, 0x1000, 0).astype(np.uint64))
+    call("uh_mx_xform_in", dx, K, drex, tab2, xa2, P, K, None, dev(d["eidx"]))
+    assert np.array_equal(xa2.download((P, K), np.uint16)[live], got[live])
+    qo, qso = filled((P, K), np.uint8, 0xEE), filled((P, K // 128), np.uint8, 0xEE)
+    call("uh_mx_xform_in_q_fp8", q, qs, dp2u, dplan, drex, s_tab, qo, qso, P, K, None)
+    q_ref, s_ref = oracle.act_quant_fp8(gathered[live]) if live.any() else (None, None)
+    gq, gs = qo.download((P, K), np.uint8), qso.download((P, K // 128), np.uint8)
+    if live.any():
+        assert np.array_equal(gq[live], q_ref) and np.array_equal(gs[live], s_ref)
+    assert (gq[~live] == 0xEE).all() and (gs[~live] == 0xEE).all()

@@ -531,6 +531,20 @@ int uh_quant_remote_tokens(const uint16_t* x, int dim, const int32_t* u2t, const
     k::quant_remote_tokens(x, dim, u2t, reinterpret_cast<const k::MoePlan*>(plan), q, s, max_tokens, S(st));
   });
 }
+int uh_mx_xform_in_q(const uint8_t* q, const uint8_t* s, const int32_t* p2u, const int32_t* plan,
+                     const int32_t* row_expert, const uint8_t* const* s_tab, uint16_t* xa, int P, int K, void* st) {
+  return guard([&] {
+    k::mx_xform_in_q(q, s, p2u, reinterpret_cast<const k::MoePlan*>(plan), row_expert, s_tab, xa, P, K, S(st));
+  });
+}
+int uh_mx_xform_in_q_fp8(const uint8_t* q, const uint8_t* s, const int32_t* p2u, const int32_t* plan,
+                         const int32_t* row_expert, const uint8_t* const* s_tab, uint8_t* qo, uint8_t* qso, int P,
+                         int K, void* st) {
+  return guard([&] {
+    k::mx_xform_in_q_fp8(q, s, p2u, reinterpret_cast<const k::MoePlan*>(plan), row_expert, s_tab, qo, qso, P, K,
+                         S(st));
+  });
+}
 int uh_copy_remote_rows(const uint16_t* src, uint16_t* dst, const int32_t* plan, int dim, int max_rows, void* st) {
   return guard([&] { k::copy_remote_rows(src, dst, reinterpret_cast<const k::MoePlan*>(plan), dim, max_rows, S(st)); });
 }

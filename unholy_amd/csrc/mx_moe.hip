@@ -557,6 +557,37 @@ void launch_gemv_t(const MxGemvArgs& a, int ntiles, hipStream_t st) {
   launch_gemv_w<NP, GM, AM, GV_WAVES>(a, ntiles, st);
 }
 
+// mx_xform_in_q (mx_moe.hip:132-176, kMode 1): rows r in [plan->remote0, plan->P) of a resident expert rebuilt from
+// the compact fp8 token rows (quant_remote_tokens' codes q [U, K] and exponents qs [U, K / 128]) of token p2u[r].
+// FP8 = false: xa[r] = bf16(e4m3 * 2^(e - 127)), exact with the scaled conversion (every such product is a bf16
+// number), so bit-identical to mx_xform_in on the gathered rows; FP8 = true: the codes and exponents copied to the
+// pair row (the MFMA operand form). 8 values per thread.
+template <bool FP8>
+__global__ __launch_bounds__(256) void mx_xform_q_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__ qs,
+                                                         const int32_t* __restrict__ p2u,
+                                                         const MoePlan* __restrict__ plan,
+                                                         const int32_t* __restrict__ row_expert,
+                                                         const uint8_t* const* __restrict__ s_tab,
+                                                         bf16* __restrict__ xa, uint8_t* __restrict__ qo,
+                                                         uint8_t* __restrict__ qso, int K) {
+  const int r0 = plan->remote0, per = K / 8, ks = K / 128;
+  const size_t n = plan->P > r0 ? size_t(plan->P - r0) * per : 0;
+  for (size_t it = blockIdx.x * size_t(blockDim.x) + threadIdx.x; it < n; it += size_t(gridDim.x) * blockDim.x) {
+    const int r = r0 + int(it / per), c = int(it % per);
+    if (s_tab && !s_tab[row_expert[r]]) continue;  // expert not on this device
+    const size_t t = size_t(p2u[r]);
+    const uint2 cc = *reinterpret_cast<const uint2*>(q + t * K + 8 * c);
+    const uint8_t se = qs[t * ks + c / 16];
+    if constexpr (FP8) {
+      *reinterpret_cast<uint2*>(qo + size_t(r) * K + 8 * c) = cc;
+      if ((c & 15) == 0) qso[size_t(r) * ks + c / 16] = se;
+    } else {
+      const bf16x8 v = fp8x8_to_bf16(cc.x, cc.y, e8m0_to_f32(se));
+      *reinterpret_cast<bf16x8*>(xa + size_t(r) * K + 8 * c) = v;
+    }
+  }
+}
+
 }  // namespace
 
 // ---- internal launchers (mx_internal.hpp) -----------------------------------------------------------------------------
@@ -667,6 +698,35 @@ void mx_xform_in_fp8(const bf16* x, int ldx, const int32_t* row_expert, const ui
                      uint8_t* qs, int P, int K, hipStream_t st, const int32_t* x_rows) {
   if (!q || !qs) throw std::runtime_error("mx_xform_in_fp8: null q / qs");
   launch_mx_transform(1, x, ldx, x_rows, nullptr, nullptr, 0.0f, row_expert, s_tab, nullptr, q, qs, K, P, st);
+}
+
+namespace {
+void launch_xform_q(bool fp8, const uint8_t* q, const uint8_t* s, const int32_t* p2u, const MoePlan* plan,
+                    const int32_t* row_expert, const uint8_t* const* s_tab, bf16* xa, uint8_t* qo, uint8_t* qso, int P,
+                    int K, hipStream_t st) {
+  if (P <= 0) return;
+  if (K <= 0 || K % 128) throw std::runtime_error("mx_xform_in_q: K % 128");
+  if (!q || !s || !p2u || !plan || (s_tab && !row_expert)) throw std::runtime_error("mx_xform_in_q: null operand");
+  if (reinterpret_cast<uintptr_t>(q) % 8) throw std::runtime_error("mx_xform_in_q: q not 8-byte aligned");
+  if (fp8 ? (!qo || !qso || reinterpret_cast<uintptr_t>(qo) % 8) : (!xa || reinterpret_cast<uintptr_t>(xa) % 16))
+    throw std::runtime_error("mx_xform_in_q: output null or misaligned");
+  const unsigned blocks = unsigned(std::max<size_t>(1, std::min<size_t>((size_t(P) * (K / 8) + 255) / 256, 8192)));
+  if (fp8)
+    mx_xform_q_kernel<true><<<blocks, 256, 0, st>>>(q, s, p2u, plan, row_expert, s_tab, nullptr, qo, qso, K);
+  else
+    mx_xform_q_kernel<false><<<blocks, 256, 0, st>>>(q, s, p2u, plan, row_expert, s_tab, xa, nullptr, nullptr, K);
+  UH_CHECK_LAUNCH();
+}
+}  // namespace
+
+void mx_xform_in_q(const uint8_t* q, const uint8_t* s, const int32_t* p2u, const MoePlan* plan,
+                   const int32_t* row_expert, const uint8_t* const* s_tab, bf16* xa, int P, int K, hipStream_t st) {
+  launch_xform_q(false, q, s, p2u, plan, row_expert, s_tab, xa, nullptr, nullptr, P, K, st);
+}
+void mx_xform_in_q_fp8(const uint8_t* q, const uint8_t* s, const int32_t* p2u, const MoePlan* plan,
+                       const int32_t* row_expert, const uint8_t* const* s_tab, uint8_t* qo, uint8_t* qso, int P, int K,
+                       hipStream_t st) {
+  launch_xform_q(true, q, s, p2u, plan, row_expert, s_tab, nullptr, qo, qso, P, K, st);
 }
 
 void mx_swiglu(const bf16* g, const bf16* u, const float* w, const int32_t* row_expert, const uint8_t* const* s_tab,
