@@ -351,7 +351,7 @@ def grouped_entry(M, ms):
     return e
 
 
-def cpu_baseline(seconds=10.0, max_reps=5):
+def cpu_baseline(seconds=12.0, max_reps=20):
     """The CPU oracle (reference arithmetic, oracle/uh_oracle.cpp) on one decode step of the headline workload:
     T = 8 tokens, softmax top-6 over 256 experts; host weights are generated for the experts the step touches only
     (the others are never read). Threads: one per host core up to 16 (the box's CPU share)."""
