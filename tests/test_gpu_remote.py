@@ -250,3 +250,52 @@ def test_xform_in_q_matches_gathered_rows(T, K):
     if live.any():
         assert np.array_equal(gq[live], q_ref) and np.array_equal(gs[live], s_ref)
     assert (gq[~live] == 0xEE).all() and (gs[~live] == 0xEE).all()
+
+
+@pytest.mark.parametrize("T,E,K,tile_rows,frac", [(4096, 256, 6, 128, 0.5), (100, 16, 4, 8, 0.25), (33, 64, 8, 16, 1.0)])
+def test_dispatch_multi_kernel_resident(T, E, K, tile_rows, frac):
+    """moe_count + moe_plan(resident) + moe_scatter against the host-order dispatch: resident rows first, then the
+    others, each expert-ascending; local and remote tiles; remote0."""
+    rng = np.random.default_rng(T + 1)
+    sel, wt, resident, d = _routed(rng, T, E, K, frac, tile_rows)
+    P = T * K
+    mt = P // tile_rows + E + 1
+    count = DeviceBuffer(E * 4)
+    count.zero()
+    off, fill, plan = DeviceBuffer(E * 4), DeviceBuffer(E * 4), DeviceBuffer(20)
+    lt, rtl = DeviceBuffer(mt * 12), DeviceBuffer(mt * 12)
+    eidx, ewt, rex, pidx = (DeviceBuffer(P * 4) for _ in range(4))
+    dsel, dwt = dev(sel), dev(wt)
+    call("uh_moe_count", dsel, T, K, count, E, None, None)
+    call("uh_moe_plan", count, dev(resident), E, P, plan, lt, rtl, off, fill, mt, None, tile_rows)
+    call("uh_moe_scatter", dsel, dwt, T, K, off, fill, eidx, ewt, rex, pidx, None)
+    p = plan.download(5, np.int32)
+    print(f"multi-kernel resident T={T}: plan={p.tolist()}")
+    assert np.array_equal(p[:4], d["plan"][:4])
+    assert np.array_equal(off.download(E, np.int32), d["off"])
+    assert np.array_equal(eidx.download(P, np.int32), d["eidx"])
+    assert np.array_equal(ewt.download(P, np.float32), d["ewt"])
+    assert np.array_equal(rex.download(P, np.int32), d["row_expert"])
+    assert np.array_equal(pidx.download((T, K), np.int32), d["pidx"])
+    assert np.array_equal(lt.download((mt, 3), np.int32)[:p[2]], d["tiles"][:p[2]])
+    assert np.array_equal(rtl.download((mt, 3), np.int32)[:p[3]], d["remote_tiles"])
+
+
+def test_dispatch_small_resident_without_remote():
+    """The resident split alone (remote off): plan, local and remote tiles, rows; no staging outputs needed."""
+    rng = np.random.default_rng(99)
+    T, E, K, tile_rows = 16, 128, 6, 8
+    sel, wt, resident, d = _routed(rng, T, E, K, 0.5, tile_rows)
+    P, mt = T * K, T * K + E
+    o = {n: filled(s, t, -1) for n, s, t in [("plan", 5, np.int32), ("tiles", (mt, 3), np.int32),
+                                             ("rtiles", (mt, 3), np.int32), ("eidx", P, np.int32),
+                                             ("ewt", P, np.float32), ("rex", P, np.int32), ("pidx", (T, K), np.int32)]}
+    call("uh_moe_dispatch_small_remote", dev(sel), dev(wt), T, K, E, P, mt, tile_rows, o["plan"], o["tiles"],
+         o["rtiles"], o["eidx"], o["ewt"], o["rex"], o["pidx"], dev(resident), None, None, 0.0, 0, 0, None, None, None,
+         None, None, None, None, None, None, 0, None, None, None, None, 0, None)
+    p = o["plan"].download(5, np.int32)
+    assert np.array_equal(p, d["plan"])
+    assert np.array_equal(o["tiles"].download((mt, 3), np.int32)[:p[2]], d["tiles"][:p[2]])
+    assert np.array_equal(o["rtiles"].download((mt, 3), np.int32)[:p[3]], d["remote_tiles"])
+    assert np.array_equal(o["pidx"].download((T, K), np.int32), d["pidx"])
+    assert np.array_equal(o["eidx"].download(P, np.int32), d["eidx"])
