@@ -85,8 +85,9 @@ struct MxGlu {
 };
 bool mx_gemm_glu();
 void mx_gemm_force_glu(int on);
-// Remote token sums (ref mx_moe.hpp:90-96) belong to the cross-device transport, which this single-GPU library
-// does not implement: a non-null dst is rejected.
+// Remote token sums (ref mx_moe.hpp:90-96): with dst, mx_grouped_gemv also writes dst[u] = bf16(sum over token u's
+// remote pair rows u2p[u][j] >= 0 of out, fp32 adds in pick order) for u < plan->n_remote_tokens (N % 128; no second
+// projection or GLU epilogue). Done as a second launch (remote_combine over out); counters are not used.
 struct MxSums {
   const int32_t* u2p = nullptr;
   const MoePlan* plan = nullptr;

@@ -89,6 +89,12 @@ int uh_mx_grouped_gemv(const uint16_t* xa, int K, const int32_t* tiles, int ntil
                        const int* ntiles_dev, const uint8_t* const* w_tab2, const uint8_t* const* s_tab2,
                        uint16_t* out2, int max_rows, const float* glu_w, const int32_t* glu_row_expert,
                        const uint8_t* const* glu_s_tab, uint16_t* glu_hh, float glu_limit, uint32_t* glu_counters);
+/* mx_moe.hpp:90-96, 100-104: uh_mx_grouped_gemv with the MxSums epilogue: sums_dst [U, N] = bf16 sums of each
+ * compact token's remote pair rows (sums_u2p [U, sums_K], U = sums_plan[4]) of out (N % 128). */
+int uh_mx_grouped_gemv_sums(const uint16_t* xa, int K, const int32_t* tiles, int ntiles, const uint8_t* const* w_tab,
+                            const uint8_t* const* s_tab, uint16_t* out, int ldo, int N, void* stream,
+                            const int* ntiles_dev, int max_rows, const int32_t* sums_u2p, const int32_t* sums_plan,
+                            int sums_K, uint16_t* sums_dst, uint32_t* sums_counters);
 /* mx_moe.hpp:49-52 */
 int uh_mx_grouped_gemm(const uint16_t* xa, int K, const int32_t* tiles, int ntiles, const uint8_t* const* w_tab,
                        const uint8_t* const* s_tab, uint16_t* out, int ldo, int N, void* stream,

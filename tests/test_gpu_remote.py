@@ -299,3 +299,38 @@ def test_dispatch_small_resident_without_remote():
     assert np.array_equal(o["rtiles"].download((mt, 3), np.int32)[:p[3]], d["remote_tiles"])
     assert np.array_equal(o["pidx"].download((T, K), np.int32), d["pidx"])
     assert np.array_equal(o["eidx"].download(P, np.int32), d["eidx"])
+
+
+@pytest.mark.parametrize("T,ldo_pad", [(8, 0), (40, 128)])
+def test_grouped_gemv_sums(T, ldo_pad):
+    """mx_grouped_gemv with MxSums on the remote side (its tiles are the remote experts' rows): out is the plain
+    GEMV's bit for bit, and sums.dst is remote_combine of those output rows (the oracle's)."""
+    from tests.test_gpu_mx import _expert_tables, _make_experts
+    from unholy_amd.device import pointer_table  # noqa: F401
+    rng = np.random.default_rng(T + ldo_pad)
+    E, Kp, N, K = 16, 4, 256, 512
+    _, _, _, d = _routed(rng, T, E, Kp, 0.5, tile_rows=8)
+    P, r0 = T * Kp, d["plan"][1]
+    rt = oracle.remote_tokens(d["pidx"], d["eidx"], r0)
+    U = rt["U"]
+    plan = d["plan"].copy()
+    plan[4] = U
+    rtiles = d["remote_tiles"]
+    nt = len(rtiles)
+    assert nt > 0 and U > 0
+    _, tabs = _expert_tables(_make_experts(rng, E, N, K), ("w", "s"))
+    xa = dev(oracle.fake_quant_fp8(randn_bf16(rng, (P, K))))
+    ldo = N + ldo_pad
+    dtiles = dev(rtiles.astype(np.int32))
+    out_a, out_b = filled((P, ldo), np.uint16, 0), filled((P, ldo), np.uint16, 0)
+    call("uh_mx_grouped_gemv", xa, K, dtiles, nt, tabs["w"], tabs["s"], out_a, ldo, N, None, None, None, None, None, 8,
+         None, None, None, None, 0.0, None)
+    dst = filled((U, N), np.uint16, 0x7777)
+    call("uh_mx_grouped_gemv_sums", xa, K, dtiles, nt, tabs["w"], tabs["s"], out_b, ldo, N, None, None, 8,
+         dev(rt["u2p"]), dev(plan), Kp, dst, None)
+    a, b = out_a.download((P, ldo), np.uint16), out_b.download((P, ldo), np.uint16)
+    assert np.array_equal(a, b)
+    ref = oracle.remote_combine(np.ascontiguousarray(b[:, :N]), rt["u2p"])
+    got = dst.download((U, N), np.uint16)
+    print(f"gemv sums T={T} ldo={ldo}: U={U}, tiles={nt}, bit-identical {np.mean(got == ref):.6f}")
+    assert np.array_equal(got, ref)

@@ -264,6 +264,16 @@ int uh_mx_grouped_gemv(const uint16_t* xa, int K, const int32_t* tiles, int ntil
                        max_rows, glu);
   });
 }
+int uh_mx_grouped_gemv_sums(const uint16_t* xa, int K, const int32_t* tiles, int ntiles, const uint8_t* const* w_tab,
+                            const uint8_t* const* s_tab, uint16_t* out, int ldo, int N, void* st,
+                            const int* ntiles_dev, int max_rows, const int32_t* sums_u2p, const int32_t* sums_plan,
+                            int sums_K, uint16_t* sums_dst, uint32_t* sums_counters) {
+  return guard([&] {
+    k::MxSums sums{sums_u2p, reinterpret_cast<const k::MoePlan*>(sums_plan), sums_K, sums_dst, sums_counters};
+    k::mx_grouped_gemv(xa, K, T3(tiles), ntiles, w_tab, s_tab, out, ldo, N, S(st), ntiles_dev, nullptr, nullptr,
+                       nullptr, max_rows, k::MxGlu{}, sums);
+  });
+}
 int uh_mx_grouped_gemm(const uint16_t* xa, int K, const int32_t* tiles, int ntiles, const uint8_t* const* w_tab,
                        const uint8_t* const* s_tab, uint16_t* out, int ldo, int N, void* st, const int* ntiles_dev,
                        const uint8_t* const* w_tab2, const uint8_t* const* s_tab2, uint16_t* out2, int max_rows) {

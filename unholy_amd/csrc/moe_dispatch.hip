@@ -678,13 +678,13 @@ __device__ __forceinline__ uint4 pack_bf16x8(const float (&acc)[8]) {
 __global__ __launch_bounds__(256) void remote_combine_kernel(const bf16* __restrict__ pair_out,
                                                              const int32_t* __restrict__ u2p,
                                                              const MoePlan* __restrict__ plan, bf16* __restrict__ dst,
-                                                             int K, int dim) {
+                                                             int K, int dim, int ld) {
   const int d = (blockIdx.x * 256 + threadIdx.x) * 8, U = plan->n_remote_tokens;
   for (int u = blockIdx.y; u < U && d < dim; u += gridDim.y) {
     float acc[8] = {};
     for (int j = 0; j < K; ++j) {
       const int p = u2p[size_t(u) * K + j];
-      if (p >= 0) add_bf16x8(acc, pair_out + size_t(p) * dim + d);
+      if (p >= 0) add_bf16x8(acc, pair_out + size_t(p) * ld + d);
     }
     const uint4 o = pack_bf16x8(acc);
     using u32x4 = unsigned int __attribute__((ext_vector_type(4)));
@@ -908,12 +908,17 @@ void remote_tokens(const int32_t* pidx, const int32_t* eidx, int T, int K, MoePl
 }
 void remote_combine(const uint16_t* pair_out, const int32_t* u2p, const MoePlan* plan, uint16_t* dst, int K, int dim,
                     int max_tokens, hipStream_t st) {
+  launch_remote_combine(pair_out, dim, u2p, plan, dst, K, dim, max_tokens, st);
+}
+void launch_remote_combine(const uint16_t* pair_out, int ld, const int32_t* u2p, const MoePlan* plan, uint16_t* dst,
+                           int K, int dim, int max_tokens, hipStream_t st) {
   if (max_tokens <= 0) return;
-  if (dim <= 0 || dim % 8 || !a16(pair_out) || !a16(dst)) throw std::runtime_error("remote_combine: dim % 8");
+  if (dim <= 0 || dim % 8 || ld < dim || ld % 8 || !a16(pair_out) || !a16(dst))
+    throw std::runtime_error("remote_combine: dim % 8, ld % 8, 16-byte aligned rows");
   if (!u2p || !plan || K <= 0) throw std::runtime_error("remote_combine: null operand");
   remote_combine_kernel<<<dim3(unsigned(cdiv(size_t(dim / 8), 256)), unsigned(std::min(max_tokens, 256))), 256, 0,
                           st>>>(
-      pair_out, u2p, plan, dst, K, dim);
+      pair_out, u2p, plan, dst, K, dim, ld);
   UH_CHECK_LAUNCH();
 }
 namespace {

@@ -49,6 +49,10 @@ unsigned long long fp8_check_encode(unsigned long long* total);
 unsigned long long bf16_check_encode(unsigned long long* nan_bad);
 // Zeroes n int32 words (a kernel, so that a captured graph records no memset node).
 void launch_zero_words(int32_t* p, size_t n, hipStream_t st);
+struct MoePlan;
+// remote_combine over rows of stride ld (the grid strides over the device-side token count; max_tokens only sizes it).
+void launch_remote_combine(const uint16_t* pair_out, int ld, const int32_t* u2p, const MoePlan* plan, uint16_t* dst,
+                           int K, int dim, int max_tokens, hipStream_t st);
 void launch_mx_gemm(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st);
 void launch_mx_transform(int mode, const uint16_t* x, int ldx, const int32_t* x_rows, const uint16_t* u,
                          const float* w, float limit, const int32_t* row_expert, const uint8_t* const* s_tab,

@@ -836,11 +836,16 @@ void mx_grouped_gemv(const bf16* xa, int K, const Exl3Tile* tiles, int ntiles, c
                      const uint8_t* const* s_tab, bf16* out, int ldo, int N, hipStream_t st, const int* ntiles_dev,
                      const uint8_t* const* w_tab2, const uint8_t* const* s_tab2, bf16* out2, int max_rows,
                      const MxGlu& glu, const MxSums& sums) {
-  if (sums.dst) throw std::runtime_error("mx_grouped_gemv: MxSums (remote token sums) is not supported");
+  if (sums.dst && (out2 || glu.hh || glu.hq || N % 128 || !sums.u2p || !sums.plan || sums.K <= 0))
+    throw std::runtime_error("mx_grouped_gemv: sums shape");
   if ((glu.hh || glu.hq) && ldo != N) throw std::runtime_error("mx_grouped_gemv: glu shape (ldo != N)");
   launch_mx_gemv(gemv_args(xa, nullptr, nullptr, K, tiles, w_tab, s_tab, out, ldo, N, ntiles_dev, w_tab2, s_tab2,
                            out2, max_rows, glu),
                  ntiles, 1, st);
+  // MxSums: each compact token's remote pair rows of out summed into sums.dst [U, N] (remote_combine's arithmetic),
+  // as a second launch on the same stream; sums.counters are not used (the reference's are zero before and after).
+  if (sums.dst && ntiles > 0)
+    launch_remote_combine(out, ldo, sums.u2p, sums.plan, sums.dst, sums.K, N, 256, st);
 }
 
 void mx_grouped_gemv_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles, int ntiles,
