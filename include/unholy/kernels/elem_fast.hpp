@@ -24,6 +24,14 @@ struct HcPostArgs {
 // launched) where the reference's is: in place, or slices not whole multiples of 256 values.
 bool rmsnorm_quant_slices(const bf16* x, int ldx, const bf16* w, bf16* y, int ldy, uint8_t* q, uint8_t* qs, int rows,
                           int dim, float eps, hipStream_t st);
+// Ref elem_fast.hpp:10-12: rmsnorm of rows x [rows, dim] (any dim) into y, out of place only, over (row, slice)
+// workgroups; the same values as rmsnorm_quant_slices' y.
+void rmsnorm_slices(const bf16* x, int ldx, const bf16* w, bf16* y, int ldy, int rows, int dim, float eps,
+                    hipStream_t st);
+// Ref elem_fast.hpp:21-22: the mHC post-mix out [T][hc][dim] of the rows x [T][dim] with the streams res [T][hc][dim]
+// (post [T][hc], comb [T][hc][hc], hc <= 4); out may be res.
+void hc_post_slices(const bf16* x, const bf16* res, const float* post, const float* comb, bf16* out, int T, int hc,
+                    int dim, hipStream_t st);
 // Ref elem_fast.hpp:40-41: slices per row so that a launch of `rows` rows has ~64 workgroups, each >= 256 values.
 int row_slices(int rows, int dim);
 

@@ -26,6 +26,8 @@ struct MoePlan {  // ref moe_dispatch.hpp:14-20
 };
 
 // count[e] += picks of e (count zero on entry; moe_plan clears it again); hist[e] += the same. Ref :26.
+// Ref moe_dispatch.hpp:25: dst[i] = sel[i] as a byte, i < n (dst: pinned host memory; the routing trace).
+void moe_trace(const int32_t* sel, int n, uint8_t* dst, hipStream_t st);
 void moe_count(const int32_t* sel, int T, int K, int32_t* count, int E, hipStream_t st, uint32_t* hist = nullptr);
 // Offsets (resident experts first, then the others, each ascending), tiles of <= tile_rows rows, plan; clears
 // fill and count. resident may be null (all resident). E <= 1024. Ref :29-31.

@@ -162,6 +162,14 @@ int uh_route_glm(const float* logits, const float* bias, int32_t* sel, float* we
                  float route_scale, void* stream);
 /* No reference counterpart: the synthetic workload's softmax top-K, renormalised over the picks. */
 int uh_route_softmax(const float* logits, int32_t* sel, float* weights, int T, int E, int K, void* stream);
+/* moe_dispatch.hpp:25: dst[i] = (uint8) sel[i], the routing trace (dst may be pinned host memory). */
+int uh_moe_trace(const int32_t* sel, int n, uint8_t* dst, void* stream);
+/* elem_fast.hpp:10-12, 21-22: rmsnorm of rows (any dim, out of place); the mHC post-mix of rows x [T, dim] into
+ * out [T, hc, dim] from the streams res (out may be res; post [T, hc], comb [T, hc, hc], hc <= 4). */
+int uh_rmsnorm_slices(const uint16_t* x, int ldx, const uint16_t* w, uint16_t* y, int ldy, int rows, int dim, float eps,
+                      void* stream);
+int uh_hc_post_slices(const uint16_t* x, const uint16_t* res, const float* post, const float* comb, uint16_t* out,
+                      int T, int hc, int dim, void* stream);
 /* moe_dispatch.hpp:26 */
 int uh_moe_count(const int32_t* sel, int T, int K, int32_t* count, int E, void* stream, uint32_t* hist);
 /* moe_dispatch.hpp:29-31 (resident may be NULL: all resident) */

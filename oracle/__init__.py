@@ -51,6 +51,7 @@ _SIGS = {
     "or_moe_combine": (None, [_P, _P, _P, _P, _I, _I, _I]),
     "or_remote_tokens": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _P, _P]),
     "or_remote_combine": (None, [_P, _P, _I, _I, _I, _P]),
+    "or_hc_post": (None, [_P, _P, _P, _P, _P, _I, _I, _I]),
     "or_moe_combine_partial": (None, [_P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _I]),
     "or_moe_forward": (None, [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _F, _P, _P, _I, _P, _I]),
 }
@@ -400,6 +401,15 @@ def moe_combine_partial(pair_out, pidx, remote0, tok2u, remote, shared=None, hc_
     lib().or_moe_combine_partial(_p(pair_out), _p(pidx), int(remote0), _p(_c(tok2u, np.int32)), _p(rem), _p(sh),
                                  _p(out), T, K, dim, _p(hx), _p(po), _p(co), hc)
     return out if hx is None else (out, hx)
+
+
+def hc_post(x, res, post, comb):
+    """The mHC post-mix (ref_elem.hip hc_post): x [T, dim], res [T, hc, dim] -> out [T, hc, dim]."""
+    x, res = _c(x, np.uint16), _c(res, np.uint16)
+    T, hc, dim = res.shape
+    out = np.empty_like(res)
+    lib().or_hc_post(_p(x), _p(res), _p(_c(post, np.float32)), _p(_c(comb, np.float32)), _p(out), T, hc, dim)
+    return out
 
 
 def moe_forward(x, sel, wt, experts, D, I, limit, tiled=True, threads=8, subset=None):

@@ -635,6 +635,23 @@ void or_moe_combine_partial(const uint16_t* pair_out, const int32_t* pidx, int r
     }
 }
 
+// hc_post (ref_elem.hip hc_post, dev.hip.hpp:185-201): out[t][j][d] = bf16(fma(post[t][j], x[t][d], s_j)), s_j an
+// fma chain from 0 over i of comb[t][i][j] * res[t][i][d]. out may be res (a column's res values are read first).
+void or_hc_post(const uint16_t* x, const uint16_t* res, const float* post, const float* comb, uint16_t* out, int T,
+                int hc, int dim) {
+  for (int t = 0; t < T; ++t)
+    for (int d = 0; d < dim; ++d) {
+      float r[4];
+      for (int i = 0; i < hc; ++i) r[i] = bf16_to_f32(res[(size_t(t) * hc + i) * dim + d]);
+      for (int j = 0; j < hc; ++j) {
+        float s = 0.0f;
+        for (int i = 0; i < hc; ++i) s = std::fma(comb[(size_t(t) * hc + i) * hc + j], r[i], s);
+        out[(size_t(t) * hc + j) * dim + d] =
+            f32_to_bf16(std::fma(post[size_t(t) * hc + j], bf16_to_f32(x[size_t(t) * dim + d]), s));
+      }
+    }
+}
+
 // ---- the routed-expert FFN (forward_ref.hip:268-304 per expert, then moe_combine) ------------------------------------
 // x bf16 [T, D]; sel / wt [T, K]; per-expert tables of code and scale pointers for w1, w3 ([I, D]) and w2
 // ([D, I]), raw or tile-major (tiled). Experts with a null w1 code pointer are skipped (their pair rows are

@@ -77,3 +77,34 @@ def test_quant_remote_tokens(U, T, dim):
         assert np.array_equal(qg[:U], q_ref)
         assert np.array_equal(sg[:U], s_ref)
     assert (qg[U:] == 0xAB).all() and (sg[U:] == 0xCD).all()  # rows past the device count untouched
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 4096), (8, 1000), (300, 4096), (3, 7168), (16, 130)])
+def test_rmsnorm_slices(rows, dim):
+    """rmsnorm_slices (any dim, no quantization) bit-exact against the oracle."""
+    rng = np.random.default_rng(rows * 7 + dim)
+    x, w = randn_bf16(rng, (rows, dim), scale=2.0), randn_bf16(rng, (dim,))
+    y = DeviceBuffer(rows * dim * 2)
+    call("uh_rmsnorm_slices", dev(x), dim, dev(w), y, dim, rows, dim, 1e-6, None)
+    assert np.array_equal(y.download((rows, dim), np.uint16), oracle.rmsnorm_quant(x, w, 1e-6, quant=False))
+
+
+@pytest.mark.parametrize("T,hc,dim,inplace", [(8, 4, 4096, False), (8, 4, 4096, True), (3, 2, 1000, True),
+                                              (40, 1, 512, False)])
+def test_hc_post_slices(T, hc, dim, inplace):
+    rng = np.random.default_rng(T + hc + dim)
+    x, res = randn_bf16(rng, (T, dim)), randn_bf16(rng, (T, hc, dim))
+    post = rng.random((T, hc)).astype(np.float32)
+    comb = rng.random((T, hc, hc)).astype(np.float32)
+    dres = dev(res)
+    out = dres if inplace else DeviceBuffer(res.nbytes)
+    call("uh_hc_post_slices", dev(x), dres, dev(post), dev(comb), out, T, hc, dim, None)
+    assert np.array_equal(out.download(res.shape, np.uint16), oracle.hc_post(x, res, post, comb))
+
+
+def test_moe_trace():
+    rng = np.random.default_rng(2)
+    sel = rng.integers(0, 256, 6 * 37, dtype=np.int32)
+    dst = DeviceBuffer(sel.size)
+    call("uh_moe_trace", dev(sel), sel.size, dst, None)
+    assert np.array_equal(dst.download(sel.size, np.uint8), sel.astype(np.uint8))

@@ -79,3 +79,20 @@ def test_partial_combine_close_to_fp64_and_hc_post():
     one = oracle.moe_combine_partial(pair_out, d["pidx"], r0, rt["tok2u"], partial, shared, x[:, :1],
                                      np.ones((T, 1), np.float32), np.zeros((T, 1, 1), np.float32))
     assert np.array_equal(one[1][:, 0], out)
+
+
+def test_hc_post_closed_forms():
+    rng = np.random.default_rng(8)
+    T, hc, D = 5, 4, 96
+    x = randn_bf16(rng, (T, D))
+    res = randn_bf16(rng, (T, hc, D))
+    eye = np.broadcast_to(np.eye(hc, dtype=np.float32), (T, hc, hc))
+    assert np.array_equal(oracle.hc_post(x, res, np.zeros((T, hc), np.float32), eye), res)  # comb = I, post = 0
+    one = oracle.hc_post(x, res[:, :1], np.ones((T, 1), np.float32), np.zeros((T, 1, 1), np.float32))
+    assert np.array_equal(one[:, 0], x)  # hc = 1, post = 1, comb = 0
+    post = rng.random((T, hc)).astype(np.float32)
+    comb = rng.random((T, hc, hc)).astype(np.float32)
+    got = oracle.bf16_to_f32(oracle.hc_post(x, res, post, comb))
+    want = (post[:, :, None] * oracle.bf16_to_f32(x).astype(np.float64)[:, None, :]
+            + np.einsum("tij,tid->tjd", comb.astype(np.float64), oracle.bf16_to_f32(res).astype(np.float64)))
+    np.testing.assert_allclose(got, want, rtol=8e-3, atol=1e-6)

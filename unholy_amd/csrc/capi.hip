@@ -555,6 +555,17 @@ int uh_mx_xform_in_q_fp8(const uint8_t* q, const uint8_t* s, const int32_t* p2u,
                          S(st));
   });
 }
+int uh_moe_trace(const int32_t* sel, int n, uint8_t* dst, void* st) {
+  return guard([&] { k::moe_trace(sel, n, dst, S(st)); });
+}
+int uh_rmsnorm_slices(const uint16_t* x, int ldx, const uint16_t* w, uint16_t* y, int ldy, int rows, int dim, float eps,
+                      void* st) {
+  return guard([&] { k::rmsnorm_slices(x, ldx, w, y, ldy, rows, dim, eps, S(st)); });
+}
+int uh_hc_post_slices(const uint16_t* x, const uint16_t* res, const float* post, const float* comb, uint16_t* out,
+                      int T, int hc, int dim, void* st) {
+  return guard([&] { k::hc_post_slices(x, res, post, comb, out, T, hc, dim, S(st)); });
+}
 int uh_copy_remote_rows(const uint16_t* src, uint16_t* dst, const int32_t* plan, int dim, int max_rows, void* st) {
   return guard([&] { k::copy_remote_rows(src, dst, reinterpret_cast<const k::MoePlan*>(plan), dim, max_rows, S(st)); });
 }

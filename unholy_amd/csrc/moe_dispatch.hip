@@ -576,6 +576,12 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const bf16* __restrict
   *reinterpret_cast<uint4*>(out + size_t(t) * dim + d) = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// moe_trace (moe_dispatch.hpp:25): dst[i] = sel[i] as a byte, the routing trace written to pinned host memory.
+__global__ __launch_bounds__(256) void moe_trace_kernel(const int32_t* __restrict__ sel, int n, uint8_t* __restrict__ dst) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) dst[i] = uint8_t(sel[i]);
+}
+
 // ---- remote experts: staging, compact tokens, partial combines (moe_dispatch.hip:111-278) ---------------------------
 // Device-side extents (plan) with grids sized for the maximum: grid-stride loops over 16-byte units. Each kernel ends
 // with a system-scope release so a host or peer reader of pinned memory sees its writes; one wave per workgroup runs
@@ -861,6 +867,12 @@ unsigned stride_grid(size_t units) { return unsigned(std::max<size_t>(1, std::mi
 bool a16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 }  // namespace
 
+void moe_trace(const int32_t* sel, int n, uint8_t* dst, hipStream_t st) {
+  if (n <= 0) return;
+  if (!sel || !dst) throw std::runtime_error("moe_trace: null operand");
+  moe_trace_kernel<<<unsigned(cdiv(size_t(n), 256)), 256, 0, st>>>(sel, n, dst);
+  UH_CHECK_LAUNCH();
+}
 void stage_remote(const MoePlan* plan, const Exl3Tile* rtiles, const float* ewt, const int32_t* row_expert,
                   MoePlan* plan_dst, Exl3Tile* tiles_dst, float* w_dst, int32_t* e_dst, int max_rows, hipStream_t st) {
   if (!plan || !rtiles || !ewt || !row_expert || !plan_dst || !tiles_dst || !w_dst || !e_dst)

@@ -115,6 +115,42 @@ __global__ __launch_bounds__(RQ_NT) void rmsnorm_quant_kernel(const bf16* __rest
   }
 }
 
+// rmsnorm_slices (elem_fast.hip:20-38): rmsnorm_quant_kernel's scale and outputs, any dim, no quantization; workgroup
+// (row, slice of `per` columns), one value per thread.
+__global__ __launch_bounds__(RQ_NT) void rmsnorm_slices_kernel(const bf16* __restrict__ x, int ldx,
+                                                               const bf16* __restrict__ w, bf16* __restrict__ y, int ldy,
+                                                               int dim, float eps, int per) {
+  __shared__ float red[RQ_NT / 32];
+  const bf16* xr = x + size_t(blockIdx.x) * ldx;
+  const float r = 1.0f / sqrtf(row_sumsq(xr, dim, red) / float(dim) + eps);
+  bf16* yr = y + size_t(blockIdx.x) * ldy;
+  const int d1 = min(dim, int(blockIdx.y + 1) * per);
+  for (int d = blockIdx.y * per + threadIdx.x; d < d1; d += RQ_NT)
+    yr[d] = f32_to_bf16(bf16_to_f32(w[d]) * (bf16_to_f32(xr[d]) * r));
+}
+
+// hc_post_slices (elem_fast.hip:40-47, dev.hip.hpp:185-201): out[t][j][d] = bf16(fma(post[t][j], x[t][d], s_j)),
+// s_j = fma chain over i of comb[t][i][j] * res[t][i][d]; every res value of a column is read before any out value of
+// it is written, so out may be res.
+__global__ __launch_bounds__(RQ_NT) void hc_post_slices_kernel(const bf16* x, const bf16* res,
+                                                               const float* __restrict__ post,
+                                                               const float* __restrict__ comb, bf16* out, int hc,
+                                                               int dim, int per) {
+  const int t = blockIdx.x, d1 = min(dim, int(blockIdx.y + 1) * per);
+  const float* pt = post + size_t(t) * hc;
+  const float* ct = comb + size_t(t) * hc * hc;
+  for (int d = blockIdx.y * per + threadIdx.x; d < d1; d += RQ_NT) {
+    const float xv = bf16_to_f32(x[size_t(t) * dim + d]);
+    float r[4];
+    for (int i = 0; i < hc; ++i) r[i] = bf16_to_f32(res[(size_t(t) * hc + i) * dim + d]);
+    for (int j = 0; j < hc; ++j) {
+      float s = 0.0f;
+      for (int i = 0; i < hc; ++i) s = fmaf(ct[i * hc + j], r[i], s);
+      out[(size_t(t) * hc + j) * dim + d] = f32_to_bf16(fmaf(pt[j], xv, s));
+    }
+  }
+}
+
 // 8 values per thread, 16 threads per 128-block (16-byte loads, the amax a DPP row max); items over the device-side
 // count, in a grid-stride loop whose bound is uniform so every 16-lane group stays whole.
 __global__ __launch_bounds__(256) void quant_remote_tokens_kernel(const bf16* __restrict__ x, int dim,
@@ -146,6 +182,27 @@ bool rmsnorm_quant_slices(const bf16* x, int ldx, const bf16* w, bf16* y, int ld
     rmsnorm_quant_kernel<false><<<grid, RQ_NT, 0, st>>>(x, ldx, w, y, ldy, q, qs, dim, eps, dim / sl);
   UH_CHECK_LAUNCH();
   return true;
+}
+
+void rmsnorm_slices(const bf16* x, int ldx, const bf16* w, bf16* y, int ldy, int rows, int dim, float eps,
+                    hipStream_t st) {
+  if (x == y) throw std::runtime_error("rmsnorm_slices: in place");
+  if (rows <= 0) return;
+  if (!x || !w || !y || dim <= 0 || ldx < dim || ldy < dim) throw std::runtime_error("rmsnorm_slices: operands");
+  const int s = row_slices(rows, dim);
+  rmsnorm_slices_kernel<<<dim3(unsigned(rows), unsigned(s)), RQ_NT, 0, st>>>(x, ldx, w, y, ldy, dim, eps,
+                                                                              (dim + s - 1) / s);
+  UH_CHECK_LAUNCH();
+}
+void hc_post_slices(const bf16* x, const bf16* res, const float* post, const float* comb, bf16* out, int T, int hc,
+                    int dim, hipStream_t st) {
+  if (hc > 4) throw std::runtime_error("hc_post_slices: hc > 4");
+  if (T <= 0) return;
+  if (hc < 1 || dim <= 0 || !x || !res || !post || !comb || !out) throw std::runtime_error("hc_post_slices: operands");
+  const int s = row_slices(T, dim);
+  hc_post_slices_kernel<<<dim3(unsigned(T), unsigned(s)), RQ_NT, 0, st>>>(x, res, post, comb, out, hc, dim,
+                                                                           (dim + s - 1) / s);
+  UH_CHECK_LAUNCH();
 }
 
 void quant_remote_tokens(const uint16_t* x, int dim, const int32_t* u2t, const MoePlan* plan, uint8_t* q_dst,
