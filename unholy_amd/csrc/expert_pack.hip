@@ -327,10 +327,16 @@ void load_slots(int fd, const Header& h, size_t first, size_t count, void* dst, 
   std::atomic<bool> failed{false};
   std::mutex err_mu;
   std::exception_ptr err;
+  // O_DIRECT reads cannot target the pinned staging (the kernel cannot pin those pages for the transfer: pread fails
+  // with EFAULT), so with an O_DIRECT descriptor each reader reads into an ordinary aligned buffer and copies from it.
+  const int fl = fcntl(fd, F_GETFL);
+  const bool direct = fl != -1 && (fl & O_DIRECT) != 0;
   const auto reader = [&] {
     void* stage[2] = {nullptr, nullptr};
     hipEvent_t done[2] = {nullptr, nullptr};
+    uint8_t* bounce = nullptr;
     try {
+      if (direct) bounce = alloc_aligned(aligned_buffer_bytes(h.slot_bytes));
       UH_CHECK(hipSetDevice(device));
       for (int b = 0; b < 2; ++b) {
         stage[b] = staging_pool().take(h.slot_bytes + kAlign);
@@ -342,7 +348,11 @@ void load_slots(int fd, const Header& h, size_t first, size_t count, void* dst, 
         const int b = n & 1;
         UH_CHECK(hipEventSynchronize(done[b]));  // the copy that last used this buffer is over
         uint8_t* a = reinterpret_cast<uint8_t*>(align_up(reinterpret_cast<uintptr_t>(stage[b])));
-        read_aligned(fd, h.slots_offset + (first + i) * h.slot_bytes, h.slot_bytes, a);
+        if (direct)
+          std::memcpy(a, read_aligned(fd, h.slots_offset + (first + i) * h.slot_bytes, h.slot_bytes, bounce),
+                      h.slot_bytes);
+        else
+          read_aligned(fd, h.slots_offset + (first + i) * h.slot_bytes, h.slot_bytes, a);
         if (verify) {
           const ChecksumEntry& e = table[first + i];
           if (!e.present) throw std::runtime_error("expert pack: slot " + std::to_string(first + i) + " is absent");
@@ -358,6 +368,7 @@ void load_slots(int fd, const Header& h, size_t first, size_t count, void* dst, 
       const std::lock_guard<std::mutex> lock(err_mu);
       if (!err) err = std::current_exception();
     }
+    if (bounce) free_aligned(bounce);
     for (int b = 0; b < 2; ++b) {  // a buffer is freed only once its copy is over
       if (done[b]) (void)hipEventSynchronize(done[b]), (void)hipEventDestroy(done[b]);
       if (stage[b]) staging_pool().give(stage[b]);
