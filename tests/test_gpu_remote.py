@@ -29,7 +29,8 @@ def _routed(rng, T, E, K, frac, tile_rows=16):
     return sel, wt, resident, oracle.dispatch(sel, wt, E, tile_rows, resident)
 
 
-@pytest.mark.parametrize("T,E,K,frac", [(1, 8, 2, 1.0), (40, 64, 6, 0.3), (1500, 256, 6, 0.5), (300, 256, 6, 0.0)])
+@pytest.mark.parametrize("T,E,K,frac", [(1, 8, 2, 1.0), (40, 64, 6, 0.3), (1500, 256, 6, 0.5), (300, 256, 6, 0.0),
+                                         (4097, 256, 6, 0.5), (9000, 64, 4, 0.2)])
 def test_remote_tokens(T, E, K, frac):
     rng = np.random.default_rng(T + E)
     _, _, _, d = _routed(rng, T, E, K, frac)
