@@ -89,8 +89,8 @@ void write_pack(const char* path, const Geometry& g, const uint8_t* const* parts
 
 // The loader: slots [first, first + count) of an open pack into device memory at dst (slot i at dst + i * stride,
 // stride >= slot_bytes, 256-byte aligned). Eight reader threads, each with two pinned staging buffers taken from a
-// process-wide pool (kept and reused by later calls), read whole slots, so file reads, checksums and host-to-device
-// copies overlap; with verify, each slot's xxh64 against the checksum table (throws on a mismatch or an absent
+// process-wide pool (kept and reused by later calls), read whole slots (or, unverified with fewer slots than threads,
+// 4 KiB-aligned chunks of them), so file reads, checksums and host-to-device copies overlap; with verify, each slot's xxh64 against the checksum table (throws on a mismatch or an absent
 // slot; the first error of any thread is the one thrown). Synchronous on `stream` at return.
 void load_slots(int fd, const Header& h, size_t first, size_t count, void* dst, size_t stride, bool verify,
                 void* stream);

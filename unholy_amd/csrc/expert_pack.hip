@@ -322,7 +322,12 @@ void load_slots(int fd, const Header& h, size_t first, size_t count, void* dst, 
   // checksum of one slot overlap the host-to-device copy of its previous one and the other threads' work.
   int device = 0;
   UH_CHECK(hipGetDevice(&device));
-  const int nthreads = int(std::min<size_t>(count, kLoadThreads));
+  // Fewer unverified slots than threads: each slot is read as nch 4 KiB-aligned chunks (work items), so every thread
+  // has work. A verified slot stays whole: its XXH64 runs over it in order.
+  const size_t want = (!verify && count < kLoadThreads) ? (kLoadThreads + count - 1) / count : 1;
+  const uint64_t cb = want > 1 ? align_up((h.slot_bytes + want - 1) / want) : h.slot_bytes;
+  const size_t nch = size_t((h.slot_bytes + cb - 1) / cb), items = count * nch;
+  const int nthreads = int(std::min<size_t>(items, kLoadThreads));
   std::atomic<size_t> next{0};
   std::atomic<bool> failed{false};
   std::mutex err_mu;
@@ -336,31 +341,32 @@ void load_slots(int fd, const Header& h, size_t first, size_t count, void* dst, 
     hipEvent_t done[2] = {nullptr, nullptr};
     uint8_t* bounce = nullptr;
     try {
-      if (direct) bounce = alloc_aligned(aligned_buffer_bytes(h.slot_bytes));
+      if (direct) bounce = alloc_aligned(aligned_buffer_bytes(cb));
       UH_CHECK(hipSetDevice(device));
       for (int b = 0; b < 2; ++b) {
-        stage[b] = staging_pool().take(h.slot_bytes + kAlign);
+        stage[b] = staging_pool().take(cb + kAlign);
         UH_CHECK(hipEventCreateWithFlags(&done[b], hipEventDisableTiming));
       }
       for (int n = 0; !failed.load(std::memory_order_relaxed); ++n) {
-        const size_t i = next.fetch_add(1);
-        if (i >= count) break;
+        const size_t item = next.fetch_add(1);
+        if (item >= items) break;
+        const size_t i = item / nch, c = item % nch;
+        const uint64_t len = std::min<uint64_t>(cb, h.slot_bytes - c * cb);
+        const uint64_t off = h.slots_offset + (first + i) * h.slot_bytes + c * cb;
         const int b = n & 1;
         UH_CHECK(hipEventSynchronize(done[b]));  // the copy that last used this buffer is over
         uint8_t* a = reinterpret_cast<uint8_t*>(align_up(reinterpret_cast<uintptr_t>(stage[b])));
         if (direct)
-          std::memcpy(a, read_aligned(fd, h.slots_offset + (first + i) * h.slot_bytes, h.slot_bytes, bounce),
-                      h.slot_bytes);
+          std::memcpy(a, read_aligned(fd, off, len, bounce), len);
         else
-          read_aligned(fd, h.slots_offset + (first + i) * h.slot_bytes, h.slot_bytes, a);
-        if (verify) {
+          read_aligned(fd, off, len, a);
+        if (verify) {  // nch == 1: the whole slot
           const ChecksumEntry& e = table[first + i];
           if (!e.present) throw std::runtime_error("expert pack: slot " + std::to_string(first + i) + " is absent");
           if (xxh64(a, h.slot_bytes) != e.hash)
             throw std::runtime_error("expert pack: slot " + std::to_string(first + i) + " checksum mismatch");
         }
-        UH_CHECK(hipMemcpyAsync(static_cast<uint8_t*>(dst) + i * stride, a, h.slot_bytes, hipMemcpyHostToDevice,
-                                st));
+        UH_CHECK(hipMemcpyAsync(static_cast<uint8_t*>(dst) + i * stride + c * cb, a, len, hipMemcpyHostToDevice, st));
         UH_CHECK(hipEventRecord(done[b], st));
       }
     } catch (...) {
