@@ -351,17 +351,27 @@ def grouped_entry(M, ms):
     return e
 
 
-def cpu_baseline(seconds=12.0, max_reps=20):
-    """The CPU oracle (reference arithmetic, oracle/uh_oracle.cpp) on one decode step of the headline workload:
-    T = 8 tokens, softmax top-6 over 256 experts; host weights are generated for the experts the step touches only
-    (the others are never read). Threads: one per host core up to 16 (the box's CPU share)."""
-    import oracle
-    rng = np.random.default_rng(1234)
-    T = 8
-    x = to_bf16(rng.standard_normal((T, D), dtype=np.float32))
-    logits = rng.standard_normal((T, E), dtype=np.float32)
-    sel, wt = oracle.route_softmax(logits, TOPK)
-    touched = sorted(set(sel.ravel().tolist()))
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads():
+    """Host threads for the CPU oracle: the cores this process may run on, at most 16 (a one-GPU box's CPU share)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def _host_experts(rng, touched):
     experts = [None] * E
     for e in touched:
         ex = {}
@@ -369,15 +379,92 @@ def cpu_baseline(seconds=12.0, max_reps=20):
             ex[wn] = rng.integers(0, 256, n * k // 2, dtype=np.uint8)
             ex[sn] = rng.integers(119, 126, n * k // 32, dtype=np.uint8)
         experts[e] = ex
-    threads = max(1, min(16, os.cpu_count() or 1))
+    return experts
+
+
+def _timed(fn, min_s, max_reps=50):
+    """(reps, seconds) of back-to-back calls until min_s seconds or max_reps calls."""
     reps, t0 = 0, time.perf_counter()
-    while reps < max_reps and (time.perf_counter() - t0) < seconds:
-        oracle.moe_forward(x, sel, wt, experts, D, I, LIMIT, tiled=True, threads=threads)
+    while True:
+        fn()
         reps += 1
-    dt = time.perf_counter() - t0
-    return dict(value=T * reps / dt, unit="tokens/s", cores=threads, kind="port",
-                sample=f"{reps} decode step(s) of T=8 tokens, 256 experts, top-6 ({len(touched)} experts touched, "
-                       f"{dt:.1f} s on {threads} threads)")
+        dt = time.perf_counter() - t0
+        if dt >= min_s or reps >= max_reps:
+            return reps, dt
+
+
+def cpu_baselines(min_s=1.0):
+    """The CPU oracle (oracle/uh_oracle.cpp: the reference's arithmetic restated in C++, the same code the parity
+    tests check against) on every BASELINE configuration, at 1 thread and at cpu_threads() threads, on the same
+    kind of seeded synthetic inputs as the GPU workloads. Each figure is tokens (rows) per second of the whole
+    workload. configs[3] (T = 4096) and configs[4] at M = 4096 run a sample (4 experts' rows; 64 rows) and are
+    extrapolated linearly in rows, labelled so. About 20-30 s of CPU time in all."""
+    import oracle
+    rng = np.random.default_rng(1234)
+    nt = cpu_threads()
+    out = {"cpu_model": cpu_model(), "threads": nt, "kind": "port"}
+
+    def both(name, fn, tokens, note, scale=1.0):
+        e = {"sample": note}
+        for th in (1, nt):
+            reps, dt = _timed(lambda: fn(th), min_s)
+            one = th == 1 and nt > 1
+            e["tokens_per_s_1t" if one else "tokens_per_s"] = tokens * reps / (dt * scale)
+            e["seconds_per_step_1t" if one else "seconds_per_step"] = dt * scale / reps
+        e["threads"] = nt
+        out[name] = e
+
+    # configs[0]: one MXFP4 GEMV (act_quant of x, then [2048, 4096] weights)
+    x1 = to_bf16(rng.standard_normal((1, D), dtype=np.float32))
+    w0 = rng.integers(0, 256, (I, D // 2), dtype=np.uint8)
+    s0 = rng.integers(119, 126, (I, D // 32), dtype=np.uint8)
+
+    def gemv0(th):
+        q, qs = oracle.act_quant_fp8(x1)
+        oracle.gemm_a8w4(q, qs, w0, s0, I, threads=th)
+
+    both("configs0_single_gemv_M1", gemv0, 1, "act_quant + one [2048, 4096] MXFP4 GEMV")
+    # configs[1], [2]: the whole routed-expert FFN step (routing, dispatch, act_quant, w1/w3, SwiGLU, w2, combine)
+    for name, T, bias in (("configs1_moe_decode_T8", 8, 0.0), ("configs2_moe_verify_T64", 64, 0.5)):
+        x = to_bf16(rng.standard_normal((T, D), dtype=np.float32))
+        logits = rng.standard_normal((T, E), dtype=np.float32)
+        if bias:
+            logits = logits + rng.standard_normal(E, dtype=np.float32) * np.float32(bias)
+        sel, wt = oracle.route_softmax(logits, TOPK)
+        touched = sorted(set(sel.ravel().tolist()))
+        experts = _host_experts(rng, touched)
+        both(name, lambda th: oracle.moe_forward(x, *oracle.route_softmax(logits, TOPK), experts, D, I, LIMIT,
+                                                 threads=th),
+             T, f"whole step, {len(touched)} experts touched")
+        del experts
+    # configs[3]: T = 4096 routed over 256 experts; the sample runs 4 experts' rows, scaled by P / sample rows
+    T = 4096
+    x = to_bf16(rng.standard_normal((T, D), dtype=np.float32))
+    logits = rng.standard_normal((T, E), dtype=np.float32)
+    sel, wt = oracle.route_softmax(logits, TOPK)
+    cnt = np.bincount(sel.ravel(), minlength=E)
+    sample = [int(e) for e in rng.choice(E, 4, replace=False)]
+    experts = _host_experts(rng, sample)
+    rows = int(cnt[sample].sum())
+    both("configs3_moe_prefill_T4096", lambda th: oracle.moe_forward(x, sel, wt, experts, D, I, LIMIT, threads=th,
+                                                                     subset=sample),
+         T, f"4 of 256 experts ({rows} of {T * TOPK} pair rows), extrapolated linearly in rows",
+         scale=T * TOPK / rows)
+    del experts
+    # configs[4]: fp8 dense 4096 x 4096 with fp32 scales (act_quant_fp8_f32s + gemm_w8a8)
+    wq = rng.integers(0, 256, (D, D), dtype=np.uint8)
+    wq[(wq & 0x7F) == 0x7F] = 0
+    wsc = (rng.random((D // 128, D // 128), dtype=np.float32) * np.float32(1e-3)).astype(np.float32)
+    for M, rows_s in ((1, 1), (64, 64), (4096, 64)):
+        xm = to_bf16(rng.standard_normal((rows_s, D), dtype=np.float32))
+
+        def fp8(th, xm=xm):
+            q, sa = oracle.act_quant_fp8_f32s(xm)
+            oracle.gemm_w8a8(q, sa, wq, wsc, threads=th)
+
+        both(f"configs4_fp8_dense_M{M}", fp8, M, "whole GEMM" if rows_s == M else
+             f"{rows_s} of {M} rows, extrapolated linearly in rows", scale=M / rows_s)
+    return out
 
 
 def run_only(name, args, rng):
@@ -516,7 +603,15 @@ def main():
         wl["remote_transport_T4096"] = bench_remote(4096, 64, 16, rng)
         result["workloads"] = wl
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline()
+        cb = cpu_baselines()
+        head = cb["configs1_moe_decode_T8"]
+        result["cpu_baseline"] = {
+            "value": head["tokens_per_s"], "unit": "tokens/s", "cores": cb["threads"], "kind": "port",
+            "sample": "one decode step of configs[1] (T=8, 256 experts, top-6; " + head["sample"] + ") through the "
+                      "CPU oracle, repeated for >= 1 s; per_config holds every BASELINE configuration at 1 thread "
+                      "and at `cores` threads",
+            "value_1_thread": head["tokens_per_s_1t"], "cpu_model": cb["cpu_model"],
+            "per_config": {k: v for k, v in cb.items() if k.startswith("configs")}}
     print(json.dumps(result))
 
 

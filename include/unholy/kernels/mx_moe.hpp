@@ -11,8 +11,9 @@
 // activation row's e8m0 scale per 128 inputs and sw the weight's per 32 (the reference's act_quant_fp8 +
 // gemm_a8w4, ref_gemm.hip:180-183). Here both operands are dequantized exactly in registers (every e4m3 x 2^k
 // and e2m1 x 2^k value is a bf16 number) and multiplied on the bf16 MFMA with fp32 accumulation: the same exact
-// products summed in another fp32 order. (The block-scaled f8f6f4 MFMA is not used for results: its internal
-// sums lose bits, measured at ~3e-3 of the output against fp64 on this hardware.)
+// products summed in another fp32 order. The block-scaled f8f6f4 MFMA is only a selectable speed mode of the prefill
+// GEMM (mx_gemm_set_exact(0)): its internal sums lose bits, measured at ~3e-3 of the output against fp64 on this
+// hardware, outside the parity tolerance.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -139,10 +140,11 @@ void mx_grouped_gemm_x(const bf16* x, int ldx, const int32_t* x_rows, int K, con
 void mx_grouped_gemm_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles, int ntiles,
                               const uint8_t* const* w_tab, const uint8_t* const* s_tab, float* out, int ldo, int N,
                               hipStream_t st, const int* ntiles_dev = nullptr);
-// The arithmetic of the prefill GEMM on e4m3 codes (no reference counterpart): 0 (default) the block-scaled MFMA
-// (fp8 x fp4 with the e8m0 scales in the instruction), 1 exact dequantization to bf16 + bf16 MFMA (fp32 sums of
-// exact products, the reference's arithmetic in another order). UH_GEMM_EXACT=1 sets the default to 1. Returns the
-// previous setting.
+// The arithmetic of the prefill GEMM on e4m3 codes (no reference counterpart): 1 (default) exact dequantization to
+// bf16 + bf16 MFMA (fp32 sums of exact products, the reference's arithmetic in another order); 0 the block-scaled
+// MFMA (fp8 x fp4 with the e8m0 scales in the instruction), a labelled speed mode outside the parity tolerance: its
+// internal sums lose bits (~3e-3 of the output at the 2^-8 rms floor against fp64). UH_GEMM_EXACT=0 sets the
+// default to 0. Returns the previous setting.
 int mx_gemm_set_exact(int on);
 bool mx_gemm_exact();
 // The GEMV with fp32 outputs (no bf16 rounding): for accuracy checks against an fp64 oracle.

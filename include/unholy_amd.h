@@ -78,6 +78,9 @@ int uh_check_fp8_encode(unsigned long long* bad, unsigned long long* total);
  * round-to-nearest-even over all 2^32 fp32 bit patterns; *bad = mismatches at non-NaN inputs plus NaN inputs whose
  * result is not a NaN, *nan_bad = NaN inputs whose NaN payload differs. */
 int uh_check_bf16_encode(unsigned long long* bad, unsigned long long* nan_bad);
+/* No reference counterpart: y[i] = e^x[i] as the SwiGLU epilogues and the softmax / sigmoid routers compute it (IEEE
+ * operations only, the same bits as the CPU oracle's), for checks. */
+int uh_exp_f32_array(const float* x, float* y, size_t n, void* stream);
 /* mx_moe.hpp:61: exhaustive MFMA block-scaled decode check; *bad = mismatches among normal results. */
 int uh_mx_check_dequant(unsigned long long* bad, unsigned long long* total);
 
@@ -132,8 +135,9 @@ int uh_mx_grouped_gemm_x(const uint16_t* x, int ldx, const int32_t* x_rows, int 
 int uh_mx_grouped_gemm_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const int32_t* tiles, int ntiles,
                                 const uint8_t* const* w_tab, const uint8_t* const* s_tab, float* out, int ldo, int N,
                                 void* stream, const int* ntiles_dev);
-/* No reference counterpart: the prefill GEMM's arithmetic on e4m3 codes: 0 (default) the block-scaled MFMA, 1 exact
- * bf16 dequantization + bf16 MFMA. Process-wide; returns the previous setting. */
+/* No reference counterpart: the prefill GEMM's arithmetic on e4m3 codes: 1 (default) exact bf16 dequantization +
+ * bf16 MFMA (the parity arithmetic), 0 the block-scaled MFMA (a speed mode outside the parity tolerance).
+ * Process-wide; returns the previous setting. */
 int uh_mx_gemm_set_exact(int on);
 /* No reference counterpart: uh_mx_grouped_gemv_q with fp32 outputs (before bf16 rounding), for accuracy checks. */
 int uh_mx_grouped_gemv_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const int32_t* tiles, int ntiles,

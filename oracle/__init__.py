@@ -27,6 +27,7 @@ _SIGS = {
     "or_f32_to_e4m3": (ctypes.c_uint8, [_F]),
     "or_e8m0_to_f32": (_F, [ctypes.c_uint8]),
     "or_e2m1_to_f32": (_F, [ctypes.c_uint32]),
+    "or_exp_f32_array": (None, [_P, _P, ctypes.c_size_t]),
     "or_pow2_ceil_e8m0": (ctypes.c_uint8, [_F]),
     "or_f32_to_bf16_array": (None, [_P, _P, ctypes.c_size_t]),
     "or_f32_to_e4m3_array": (None, [_P, _P, ctypes.c_size_t]),
@@ -133,6 +134,14 @@ def e4m3_to_f32(c) -> np.ndarray:
 
 
 # ---- quantization ----------------------------------------------------------------------------------------------
+def exp_f32(x) -> np.ndarray:
+    """e^x as the library computes it (uh_oracle.cpp exp_f32), elementwise over fp32 values."""
+    x = _c(x, np.float32)
+    y = np.empty_like(x)
+    lib().or_exp_f32_array(_p(x), _p(y), x.size)
+    return y
+
+
 def act_quant_fp8(x_bf16, block=128):
     x = _c(x_bf16, np.uint16)
     rows, cols = x.shape

@@ -40,6 +40,7 @@
 //
 // Build: oracle/Makefile (g++ -O2 -ffp-contract=off: every fp32 operation rounds where written).
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -104,6 +105,29 @@ inline uint8_t pow2_ceil_e8m0(float v) {
   return uint8_t(e + 127);
 }
 
+// e^x as the library computes it (IEEE operations only, so both sides produce the same bits; the reference's device
+// expf is an ocml routine no CPU restatement reproduces): Cody-Waite reduction with ln2 split into a 16-bit-exact
+// high part and the rest, the degree-7 Taylor polynomial of e^r in Horner form with fused multiply-adds, and 2^n as
+// two exact power-of-two factors.
+inline float pow2_f32(int e) { return u2f(uint32_t(e + 127) << 23); }
+inline float exp_f32(float x) {
+  if (!(x < 88.7228394f)) return x != x ? x : INFINITY;
+  if (x < -103.972084f) return 0.0f;
+  const float n = std::rint(x * 1.44269504f);
+  float r = std::fma(-n, 0.693145751953125f, x);
+  r = std::fma(-n, 1.42860677e-06f, r);
+  float p = 1.0f / 5040.0f;
+  p = std::fma(p, r, 1.0f / 720.0f);
+  p = std::fma(p, r, 1.0f / 120.0f);
+  p = std::fma(p, r, 1.0f / 24.0f);
+  p = std::fma(p, r, 1.0f / 6.0f);
+  p = std::fma(p, r, 0.5f);
+  p = std::fma(p, r, 1.0f);
+  p = std::fma(p, r, 1.0f);
+  const int ni = int(n), h = ni / 2;
+  return (p * pow2_f32(h)) * pow2_f32(ni - h);
+}
+
 // Runs f(i) for i in [0, n) on up to nthreads threads (contiguous ranges).
 template <class F>
 void parallel_for(int n, int nthreads, F f) {
@@ -148,6 +172,9 @@ float or_e4m3_to_f32(uint8_t v) { return e4m3_to_f32(v); }
 uint8_t or_f32_to_e4m3(float x) { return f32_to_e4m3(x); }
 float or_e8m0_to_f32(uint8_t v) { return e8m0_to_f32(v); }
 float or_e2m1_to_f32(uint32_t nib) { return e2m1_to_f32(nib); }
+void or_exp_f32_array(const float* x, float* y, size_t n) {
+  for (size_t i = 0; i < n; ++i) y[i] = exp_f32(x[i]);
+}
 uint8_t or_pow2_ceil_e8m0(float v) { return pow2_ceil_e8m0(v); }
 
 void or_f32_to_bf16_array(const float* x, uint16_t* y, size_t n) {
@@ -234,22 +261,57 @@ void or_mx_dequant(const uint8_t* w, const uint8_t* s, float* out, int N, int K,
 // block order (ref_gemm.hip:26-58 with G = 32). c: bf16 (c16) or fp32 (c32) or both.
 void or_gemm_a8w4(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, uint16_t* c16, float* c32,
                   int ldc, int M, int N, int K, int tiled, int nthreads) {
-  parallel_for(N, nthreads, [&](int n) {
-    std::vector<float> wv(static_cast<size_t>(K));
-    for (int k = 0; k < K; ++k) wv[size_t(k)] = e2m1_at(w, N, K, n, k, tiled != 0);
-    for (int m = 0; m < M; ++m) {
-      float acc = 0.0f;
-      for (int kb = 0; kb < K / 32; ++kb) {
-        float part = 0.0f;
-        for (int k = kb * 32; k < kb * 32 + 32; ++k)
-          part = std::fma(e4m3_to_f32(a[size_t(m) * K + k]), wv[size_t(k)], part);
-        const float sc = e8m0_to_f32(sa[size_t(m) * (K / 128) + kb / 4]) *
-                         e8m0_to_f32(e2m1_scale(sw, N, K, n, kb, tiled != 0));
-        acc += part * sc;
+  // Every output is the fma chain of ref_gemm.hip:54-63 in its order. The activations are decoded once; NB adjacent
+  // columns are decoded one 64-input slab at a time (a tile that stays in L1), and their chains run side by side
+  // (the same chains, interleaved for the CPU's pipelines).
+  constexpr int NB = 32;
+  static const auto lut = [] {
+    std::array<std::array<float, 2>, 256> t{};
+    for (int b = 0; b < 256; ++b) t[size_t(b)] = {e2m1_to_f32(uint32_t(b) & 0xf), e2m1_to_f32(uint32_t(b) >> 4)};
+    return t;
+  }();
+  std::vector<float> af(size_t(M) * K), asc(size_t(M) * (K / 128));
+  for (size_t i = 0; i < af.size(); ++i) af[i] = e4m3_to_f32(a[i]);
+  for (size_t i = 0; i < asc.size(); ++i) asc[i] = e8m0_to_f32(sa[i]);
+  parallel_for((N + NB - 1) / NB, nthreads, [&](int nb) {
+    const int n0 = nb * NB, cols = std::min(NB, N - n0);
+    std::vector<float> part(size_t(M) * NB, 0.0f), acc(size_t(M) * NB, 0.0f);
+    alignas(64) float wt[64][NB];
+    float wsc[2][NB];
+    for (int kt = 0; kt < K / 64; ++kt) {
+      for (int j = 0; j < NB; ++j) {
+        const int n = n0 + std::min(j, cols - 1);
+        const uint8_t* src = &w[tiled ? (size_t(kt) * (N / 16) + n / 16) * 512 + (n % 16) * 32
+                                      : size_t(n) * (K / 2) + size_t(kt) * 32];
+        for (int i = 0; i < 32; ++i) {
+          wt[2 * i][j] = lut[src[i]][0];
+          wt[2 * i + 1][j] = lut[src[i]][1];
+        }
+        for (int h = 0; h < 2; ++h) wsc[h][j] = e8m0_to_f32(e2m1_scale(sw, N, K, n, 2 * kt + h, tiled != 0));
       }
-      if (c16) c16[size_t(m) * ldc + n] = f32_to_bf16(acc);
-      if (c32) c32[size_t(m) * ldc + n] = acc;
+      for (int m = 0; m < M; ++m) {
+        const float* ar = &af[size_t(m) * K + size_t(kt) * 64];
+        float* pm = &part[size_t(m) * NB];
+        float* am = &acc[size_t(m) * NB];
+        for (int h = 0; h < 2; ++h) {
+          for (int k = 32 * h; k < 32 * h + 32; ++k) {
+            const float ak = ar[k];
+            for (int j = 0; j < NB; ++j) pm[j] = std::fma(ak, wt[k][j], pm[j]);
+          }
+          const float sam = asc[size_t(m) * (K / 128) + kt / 2];
+          for (int j = 0; j < NB; ++j) {
+            am[j] += pm[j] * (sam * wsc[h][j]);
+            pm[j] = 0.0f;
+          }
+        }
+      }
     }
+    for (int m = 0; m < M; ++m)
+      for (int j = 0; j < cols; ++j) {
+        const float v = acc[size_t(m) * NB + j];
+        if (c16) c16[size_t(m) * ldc + n0 + j] = f32_to_bf16(v);
+        if (c32) c32[size_t(m) * ldc + n0 + j] = v;
+      }
   });
 }
 void or_gemm_a8w4_f64(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, double* c, int ldc,
@@ -270,22 +332,38 @@ void or_gemm_a8w4_f64(const uint8_t* a, const uint8_t* sa, const uint8_t* w, con
 // sa32 / sw32 non-null: fp32 scales instead (kernel.py fp8_gemm with scale_fmt=None; gemm_wmma.hip:89-100 fold).
 void or_gemm_w8a8(const uint8_t* a, const uint8_t* sa, const float* sa32, const uint8_t* w, const uint8_t* sw,
                   const float* sw32, uint16_t* c16, float* c32, int ldc, int M, int N, int K, int nthreads) {
+  // The chains of ref_gemm.hip:130-137 in their order; activations decoded once, each column's weights once, NB
+  // adjacent columns' chains side by side.
+  constexpr int NB = 32;
   const int kbs = K / 128;
-  parallel_for(N, nthreads, [&](int n) {
-    std::vector<float> wv(static_cast<size_t>(K));
-    for (int k = 0; k < K; ++k) wv[size_t(k)] = e4m3_to_f32(w[size_t(n) * K + k]);
+  std::vector<float> af(size_t(M) * K);
+  for (size_t i = 0; i < af.size(); ++i) af[i] = e4m3_to_f32(a[i]);
+  parallel_for((N + NB - 1) / NB, nthreads, [&](int nb) {
+    const int n0 = nb * NB, cols = std::min(NB, N - n0);
+    std::vector<float> wv(size_t(K) * NB, 0.0f);  // [k][column]
+    for (int j = 0; j < cols; ++j)
+      for (int k = 0; k < K; ++k) wv[size_t(k) * NB + j] = e4m3_to_f32(w[size_t(n0 + j) * K + k]);
     for (int m = 0; m < M; ++m) {
-      float acc = 0.0f;
+      const float* ar = &af[size_t(m) * K];
+      float acc[NB] = {};
       for (int kb = 0; kb < kbs; ++kb) {
-        float part = 0.0f;
-        for (int k = kb * 128; k < kb * 128 + 128; ++k)
-          part = std::fma(e4m3_to_f32(a[size_t(m) * K + k]), wv[size_t(k)], part);
-        const float sc = sa32 ? sa32[size_t(m) * kbs + kb] * sw32[size_t(n / 128) * kbs + kb]
-                              : e8m0_to_f32(sa[size_t(m) * kbs + kb]) * e8m0_to_f32(sw[size_t(n / 128) * kbs + kb]);
-        acc += part * sc;
+        float part[NB] = {};
+        for (int k = kb * 128; k < kb * 128 + 128; ++k) {
+          const float ak = ar[k];
+          const float* wk = &wv[size_t(k) * NB];
+          for (int j = 0; j < NB; ++j) part[j] = std::fma(ak, wk[j], part[j]);
+        }
+        for (int j = 0; j < cols; ++j) {
+          const int n = n0 + j;
+          const float sc = sa32 ? sa32[size_t(m) * kbs + kb] * sw32[size_t(n / 128) * kbs + kb]
+                                : e8m0_to_f32(sa[size_t(m) * kbs + kb]) * e8m0_to_f32(sw[size_t(n / 128) * kbs + kb]);
+          acc[j] += part[j] * sc;
+        }
       }
-      if (c16) c16[size_t(m) * ldc + n] = f32_to_bf16(acc);
-      if (c32) c32[size_t(m) * ldc + n] = acc;
+      for (int j = 0; j < cols; ++j) {
+        if (c16) c16[size_t(m) * ldc + n0 + j] = f32_to_bf16(acc[j]);
+        if (c32) c32[size_t(m) * ldc + n0 + j] = acc[j];
+      }
     }
   });
 }
@@ -394,7 +472,7 @@ void or_swiglu(const uint16_t* gate, const uint16_t* up, const float* w, uint16_
       u = std::fmin(std::fmax(u, -limit), limit);
       g = std::fmin(g, limit);
     }
-    float x = (g / (1.0f + std::exp(-g))) * u;
+    float x = (g / (1.0f + exp_f32(-g))) * u;
     if (w) x = w[i / size_t(dim)] * x;
     h[i] = f32_to_bf16(x);
   }
@@ -450,7 +528,7 @@ void or_route_glm(const float* logits, const float* bias, int32_t* sel, float* w
   for (int t = 0; t < T; ++t) {
     const float* lr = logits + size_t(t) * E;
     std::vector<float> sv(static_cast<size_t>(E));
-    for (int e = 0; e < E; ++e) sv[size_t(e)] = 1.0f / (1.0f + std::exp(-lr[e])) + bias[e];
+    for (int e = 0; e < E; ++e) sv[size_t(e)] = 1.0f / (1.0f + exp_f32(-lr[e])) + bias[e];
     int chosen[8];
     for (int k = 0; k < K; ++k) {
       int bi = -1;
@@ -462,7 +540,7 @@ void or_route_glm(const float* logits, const float* bias, int32_t* sel, float* w
     std::sort(chosen, chosen + K);
     float s[8], sum = 0.0f;
     for (int k = 0; k < K; ++k) {
-      s[k] = 1.0f / (1.0f + std::exp(-lr[chosen[k]]));
+      s[k] = 1.0f / (1.0f + exp_f32(-lr[chosen[k]]));
       sum += s[k];
     }
     for (int k = 0; k < K; ++k) {
@@ -489,7 +567,7 @@ void or_route_softmax(const float* logits, int32_t* sel, float* wt, int T, int E
     const float m = lr[chosen[0]];
     float ev[8], sum = 0.0f;
     for (int k = 0; k < K; ++k) {
-      ev[k] = std::exp(lr[chosen[k]] - m);
+      ev[k] = exp_f32(lr[chosen[k]] - m);
       sum += ev[k];
     }
     for (int k = 0; k < K; ++k) {
@@ -672,7 +750,15 @@ void or_moe_forward(const uint16_t* x, const int32_t* sel, const float* wt, int 
     experts.assign(experts_subset, experts_subset + n_subset);
   else
     for (int e = 0; e < E; ++e) experts.push_back(e);
-  // Experts in parallel (each has its own rows); within an expert the GEMMs run single-threaded.
+  // Experts with rows in parallel (each has its own rows); when there are fewer of them than threads, the GEMMs of
+  // each expert split their output columns over the rest.
+  {
+    std::vector<int> live;
+    for (int e : experts)
+      if (count[size_t(e)] > 0 && w1[e]) live.push_back(e);
+    experts.swap(live);
+  }
+  const int inner = std::max(1, nthreads / std::max(1, int(experts.size())));
   parallel_for(int(experts.size()), nthreads, [&](int ie) {
     const int e = experts[size_t(ie)];
     const int cnt = count[size_t(e)], r0 = off[size_t(e)];
@@ -682,11 +768,11 @@ void or_moe_forward(const uint16_t* x, const int32_t* sel, const float* wt, int 
       std::memcpy(&in[size_t(r) * D], x + size_t(eidx[size_t(r0 + r)]) * D, size_t(D) * 2);
     std::vector<uint8_t> q(size_t(cnt) * std::max(D, I)), qs(size_t(cnt) * (std::max(D, I) / 128));
     or_act_quant_fp8(in.data(), D, q.data(), qs.data(), cnt, D, 128);
-    or_gemm_a8w4(q.data(), qs.data(), w1[e], s1[e], h1.data(), nullptr, I, cnt, I, D, tiled, 1);
-    or_gemm_a8w4(q.data(), qs.data(), w3[e], s3[e], h3.data(), nullptr, I, cnt, I, D, tiled, 1);
+    or_gemm_a8w4(q.data(), qs.data(), w1[e], s1[e], h1.data(), nullptr, I, cnt, I, D, tiled, inner);
+    or_gemm_a8w4(q.data(), qs.data(), w3[e], s3[e], h3.data(), nullptr, I, cnt, I, D, tiled, inner);
     or_swiglu(h1.data(), h3.data(), &ewt[size_t(r0)], hh.data(), cnt, I, limit);
     or_act_quant_fp8(hh.data(), I, q.data(), qs.data(), cnt, I, 128);
-    or_gemm_a8w4(q.data(), qs.data(), w2[e], s2[e], pair_out + size_t(r0) * D, nullptr, D, cnt, D, I, tiled, 1);
+    or_gemm_a8w4(q.data(), qs.data(), w2[e], s2[e], pair_out + size_t(r0) * D, nullptr, D, cnt, D, I, tiled, inner);
   });
   if (out) or_moe_combine(pair_out, pidx.data(), nullptr, out, T, K, D);
 }

@@ -12,9 +12,10 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) and the built libunholy_amd.so")
 
 
-@pytest.fixture(params=["scaled", "exact"])
+@pytest.fixture(params=["exact", "scaled"])
 def gemm_arith(request):
-    """The prefill GEMM's arithmetic for one test: the block-scaled MFMA (default) or exact bf16 dequantization."""
+    """The prefill GEMM's arithmetic for one test: exact bf16 dequantization (the default, the parity arithmetic) or
+    the block-scaled MFMA (a speed mode; its tests hold it to the looser bars written in each test)."""
     from unholy_amd import call
     prev = call("uh_mx_gemm_set_exact", 1 if request.param == "exact" else 0)
     yield request.param

@@ -1,0 +1,282 @@
+"""GPU parity at the full BASELINE shapes (D = 4096, I = 2048, E = 256, top-6) and the DSV4 dense projection shapes,
+the sizes the reference's own kernel tests run at (tools/kernel_test/mx_moe.hip:47,79-106; gemv.hip:91-96).
+
+- configs[1] decode T = 8 and configs[2] verify T = 64 (skewed routing): routing bit-exact; the forward bit-identical to
+  the flow composed from the public entry points; every stage of that flow against the oracle on identical inputs
+  for every touched expert (GEMM outputs max-rel <= 1e-2 per element, floor 2^-8 rms; h's codes bit-exact); end to
+  end against the oracle's whole forward.
+- configs[3] prefill T = 4096: the same at full size (the forward == composed flow is a size-independent property),
+  stage by stage on a sample of experts (the largest, the smallest and two more).
+- configs[4] fp8 dense 4096 x 4096 at M = 64 and M = 4096 (fp32 scales), against the oracle (M = 4096: a sample of
+  512 rows, the first and last included).
+- The DSV4 W8A8 projection shapes (e8m0 scales) at M = 1 / 8 / 64 through every W8A8 entry point.
+Weights are made on the device (splitmix64 bytes, e8m0 scales in [119, 125]) and the touched experts copied back for
+the oracle."""
+import numpy as np
+import pytest
+
+import oracle
+from tests.helpers import from_bf16, max_rel, randn_bf16, rel_l2
+from unholy_amd import call
+from unholy_amd.device import DeviceBuffer, fill_random_bytes, pointer_table, synchronize
+
+pytestmark = pytest.mark.gpu
+
+D, I, E, K = 4096, 2048, 256, 6
+LIMIT = 10.0
+SHAPES = [(I, D), (I, D), (D, I)]  # w1, w3, w2 as [N, K]
+KEYS = (("w1", "s1"), ("w3", "s3"), ("w2", "s2"))
+
+
+def dev(a):
+    return DeviceBuffer.from_array(np.ascontiguousarray(a))
+
+
+class Experts:
+    """E experts of tile-major MXFP4 weights in one device buffer; host copies of single experts on demand."""
+
+    def __init__(self, seed):
+        self.mat = [n * k // 2 + n * k // 32 for n, k in SHAPES]
+        self.ebytes = sum(self.mat)
+        self.buf = DeviceBuffer(E * self.ebytes)
+        fill_random_bytes(self.buf, E * self.ebytes, seed, 0, 255)
+        tab = [[0] * E for _ in range(6)]
+        for e in range(E):
+            off = e * self.ebytes
+            for m, (n, k) in enumerate(SHAPES):
+                tab[2 * m][e] = self.buf.ptr + off
+                tab[2 * m + 1][e] = self.buf.ptr + off + n * k // 2
+                fill_random_bytes(tab[2 * m + 1][e], n * k // 32, seed + 1 + 3 * e + m, 119, 125)
+                off += self.mat[m]
+        self.tab = tab
+        self.table = pointer_table([p for row in tab for p in row])
+        self._host = {}
+
+    def host(self, e):
+        if e not in self._host:
+            ex = {}
+            off = e * self.ebytes
+            for m, ((wn, sn), (n, k)) in enumerate(zip(KEYS, SHAPES)):
+                ex[wn] = self.buf.download(n * k // 2, np.uint8, off)
+                ex[sn] = self.buf.download(n * k // 32, np.uint8, off + n * k // 2)
+                off += self.mat[m]
+            self._host[e] = ex
+        return self._host[e]
+
+    def host_list(self, experts):
+        return [self.host(e) if e in experts else None for e in range(E)]
+
+
+@pytest.fixture(scope="module")
+def experts():
+    ex = Experts(seed=2024)
+    yield ex
+    ex.buf.free()
+
+
+def _forward(ex, x, logits, T):
+    ws_bytes = call("uh_mx_moe_workspace_size", T, K, E, D, I)
+    ws, out = DeviceBuffer(ws_bytes), DeviceBuffer(T * D * 2)
+    sel, wt = DeviceBuffer(T * K * 4), DeviceBuffer(T * K * 4)
+    dx = dev(x)
+    call("uh_mx_moe_forward", dx, dev(logits), T, K, E, D, I, ex.table, LIMIT, ws, ws_bytes, out, sel, wt, None)
+    synchronize()
+    return dx, out, sel, wt
+
+
+def _composed(ex, dx, dsel, dwt, T):
+    """The forward composed from the public entry points, keeping every intermediate: dispatch, w1 / w3 with the
+    SwiGLU + requantization epilogue (g, u and the e4m3 codes hq / hs of h), w2, combine. T <= 64: the GEMVs (16-row
+    tiles); larger T: the prefill GEMM (128-row tiles) on the gathered pair rows' codes."""
+    P = T * K
+    tile_rows = 16 if T <= 64 else 128
+    max_tiles = P // tile_rows + E + 1
+    b = dict(plan=DeviceBuffer(20), tiles=DeviceBuffer(max_tiles * 12), eidx=DeviceBuffer(P * 4),
+             ewt=DeviceBuffer(P * 4), row_expert=DeviceBuffer(P * 4), pidx=DeviceBuffer(P * 4))
+    count, off, fill = DeviceBuffer(E * 4), DeviceBuffer(E * 4), DeviceBuffer(E * 4)
+    count.zero()
+    call("uh_moe_count", dsel, T, K, count, E, None, None)
+    call("uh_moe_plan", count, None, E, P, b["plan"], b["tiles"], None, off, fill, max_tiles, None, tile_rows)
+    call("uh_moe_scatter", dsel, dwt, T, K, off, fill, b["eidx"], b["ewt"], b["row_expert"], b["pidx"], None)
+    nt = int(b["plan"].download(5, np.int32)[2])
+    t = ex.tab
+    w1, s1, w3, s3, w2, s2 = (pointer_table(t[i]) for i in range(6))
+    g, u = DeviceBuffer(P * I * 2), DeviceBuffer(P * I * 2)
+    hq, hs, pair = DeviceBuffer(P * I), DeviceBuffer(P * (I // 128)), DeviceBuffer(P * D * 2)
+    if T <= 64:
+        call("uh_mx_grouped_gemv_x", dx, D, b["eidx"], D, b["tiles"], nt, w1, s1, g, I, I, None, None, w3, s3, u,
+             tile_rows, b["ewt"], b["row_expert"], s2, None, hq, hs, LIMIT)
+        call("uh_mx_grouped_gemv_q", hq, hs, I, b["tiles"], nt, w2, s2, pair, D, D, None, None, None, None, None,
+             tile_rows, None, None, None, None, None, None, 0.0)
+    else:
+        xq, xs = DeviceBuffer(P * D), DeviceBuffer(P * (D // 128))
+        call("uh_mx_xform_in_fp8", dx, D, None, None, xq, xs, P, D, None, b["eidx"])
+        call("uh_mx_grouped_gemm_q", xq, xs, D, b["tiles"], nt, w1, s1, g, I, I, None, None, w3, s3, u, tile_rows,
+             b["ewt"], b["row_expert"], s2, None, hq, hs, LIMIT)
+        call("uh_mx_grouped_gemm_q", hq, hs, I, b["tiles"], nt, w2, s2, pair, D, D, None, None, None, None, None,
+             tile_rows, None, None, None, None, None, None, 0.0)
+    comp = DeviceBuffer(T * D * 2)
+    call("uh_moe_combine", pair, b["pidx"], None, comp, T, K, D, None)
+    synchronize()
+    return dict(comp=comp.download((T, D), np.uint16), eidx=b["eidx"].download(P, np.int32),
+                ewt=b["ewt"].download(P, np.float32), pidx=b["pidx"].download((T, K), np.int32),
+                tiles=b["tiles"].download((nt, 3), np.int32), g=g.download((P, I), np.uint16),
+                u=u.download((P, I), np.uint16), hq=hq.download((P, I), np.uint8),
+                hs=hs.download((P, I // 128), np.uint8), pair=pair.download((P, D), np.uint16))
+
+
+def _stagewise(ex, x, c, sel_ref, experts, label):
+    """Each stage of the composed flow against the oracle on the same inputs, per expert: g and u (the w1 / w3 GEMMs
+    on act_quant of the token rows) and the pair rows (the w2 GEMM on the GPU's own codes of h) within max-rel 1e-2
+    per element; the codes of h (SwiGLU + act_quant of the GPU's g and u, elementwise) bit-exact. Returns the
+    fractions of bit-identical g / u and pair values."""
+    cnt = np.bincount(sel_ref.ravel(), minlength=E)
+    offs = np.concatenate([[0], np.cumsum(cnt)[:-1]])
+    same_gu, same_pair, n_gu, n_pair, worst = 0, 0, 0, 0, 0.0
+    for e in experts:
+        r0, n = int(offs[e]), int(cnt[e])
+        if n == 0:
+            continue
+        h = ex.host(e)
+        q, qs = oracle.act_quant_fp8(x[c["eidx"][r0:r0 + n]])
+        sl = slice(r0, r0 + n)
+        for key, wn, sn in (("g", "w1", "s1"), ("u", "w3", "s3")):
+            ref = oracle.gemm_a8w4(q, qs, h[wn], h[sn], I, tiled=True, threads=16)[0]
+            mr = max_rel(from_bf16(c[key][sl]), from_bf16(ref))
+            worst = max(worst, mr)
+            assert mr <= 1e-2, (label, e, key, mr)
+            same_gu += np.count_nonzero(c[key][sl] == ref)
+            n_gu += ref.size
+        hh = oracle.swiglu(c["g"][sl], c["u"][sl], c["ewt"][sl], LIMIT)
+        hq_ref, hs_ref = oracle.act_quant_fp8(hh)
+        assert np.array_equal(c["hq"][sl], hq_ref) and np.array_equal(c["hs"][sl], hs_ref), (label, e)
+        pref = oracle.gemm_a8w4(c["hq"][sl], c["hs"][sl], h["w2"], h["s2"], D, tiled=True, threads=16)[0]
+        mr = max_rel(from_bf16(c["pair"][sl]), from_bf16(pref))
+        worst = max(worst, mr)
+        assert mr <= 1e-2, (label, e, "pair", mr)
+        same_pair += np.count_nonzero(c["pair"][sl] == pref)
+        n_pair += pref.size
+    print(f"{label}: {len(experts)} experts stage by stage, worst per-element max_rel {worst:.3e}, bit-identical "
+          f"g/u {same_gu / max(n_gu, 1):.6f}, pair rows {same_pair / max(n_pair, 1):.6f}")
+
+
+@pytest.mark.parametrize("T,bias", [(8, 0.0), (64, 0.5)], ids=["configs1_decode_T8", "configs2_verify_T64"])
+def test_full_shape_forward_vs_oracle(experts, T, bias):
+    """configs[1] / configs[2] at full shape. Stage by stage against the oracle on identical inputs, every touched
+    expert (routing bit-exact; each GEMM's bf16 outputs max-rel <= 1e-2 per element; h's codes bit-exact); the
+    forward bit-identical to the composed flow; and end to end against the oracle's whole forward: rel L2 <= 1e-4 and
+    >= 99.9% of the outputs bit-identical. (End to end, a g or u value one bf16 ulp away from the oracle's -- a
+    32-block whose exact sum needs more than 24 bits, rounded once by the MFMA and per step by the reference's fma
+    chain -- can move one e4m3 code of h by one step, which changes every output of that pair row slightly; a
+    per-element bar there would measure that discontinuity, not the arithmetic.)"""
+    rng = np.random.default_rng(100 + T)
+    x = randn_bf16(rng, (T, D))
+    logits = rng.standard_normal((T, E), dtype=np.float32)
+    if bias:
+        logits = logits + rng.standard_normal(E, dtype=np.float32) * np.float32(bias)
+    dx, out, dsel, dwt = _forward(experts, x, logits, T)
+    sel, wt = dsel.download((T, K), np.int32), dwt.download((T, K), np.float32)
+    sel_ref, wt_ref = oracle.route_softmax(logits, K)
+    assert np.array_equal(sel, sel_ref) and np.array_equal(wt, wt_ref)
+    c = _composed(experts, dx, dsel, dwt, T)
+    got_bits = out.download((T, D), np.uint16)
+    assert np.array_equal(got_bits, c["comp"])
+    ref_d = oracle.dispatch(sel_ref, wt_ref, E, 16)
+    assert np.array_equal(c["eidx"], ref_d["eidx"]) and np.array_equal(c["pidx"], ref_d["pidx"])
+    touched = sorted(set(sel_ref.ravel().tolist()))
+    _stagewise(experts, x, c, sel_ref, touched, f"T={T}")
+    assert np.array_equal(oracle.moe_combine(c["pair"], c["pidx"]), got_bits)
+    ref, _ = oracle.moe_forward(x, sel_ref, wt_ref, experts.host_list(set(touched)), D, I, LIMIT, threads=16)
+    got, r = from_bf16(got_bits), from_bf16(ref)
+    same, l2 = np.mean(got_bits == ref), rel_l2(got, r)
+    print(f"full-shape forward T={T}: {len(touched)} experts end to end: rel_l2 {l2:.3e}, bit-identical {same:.6f}, "
+          f"max_rel {max_rel(got, r):.3e}")
+    assert l2 <= 1e-4 and same >= 0.999
+
+
+def test_full_shape_prefill_T4096(experts):
+    """configs[3] at full shape: the forward bit-identical to the composed flow at T = 4096; routing and dispatch
+    bit-exact against the oracle's host order; stage by stage on sampled experts (the largest, the smallest and two
+    more), as for decode."""
+    T = 4096
+    rng = np.random.default_rng(4096)
+    x = randn_bf16(rng, (T, D))
+    logits = rng.standard_normal((T, E), dtype=np.float32)
+    dx, out, dsel, dwt = _forward(experts, x, logits, T)
+    sel, wt = dsel.download((T, K), np.int32), dwt.download((T, K), np.float32)
+    sel_ref, wt_ref = oracle.route_softmax(logits, K)
+    assert np.array_equal(sel, sel_ref) and np.array_equal(wt, wt_ref)
+    c = _composed(experts, dx, dsel, dwt, T)
+    assert np.array_equal(out.download((T, D), np.uint16), c["comp"])
+    ref_d = oracle.dispatch(sel_ref, wt_ref, E, 128)
+    assert np.array_equal(c["eidx"], ref_d["eidx"]) and np.array_equal(c["pidx"], ref_d["pidx"])
+    assert np.array_equal(c["tiles"], ref_d["tiles"][: len(c["tiles"])])
+    cnt = np.bincount(sel_ref.ravel(), minlength=E)
+    order = np.argsort(cnt, kind="stable")
+    sample = sorted({int(order[-1]), int(order[0]), int(rng.integers(E)), int(rng.integers(E))})
+    _stagewise(experts, x, c, sel_ref, sample, "prefill T=4096")
+
+
+def _fp8_f32s_weights(rng, N, Kd):
+    w = rng.standard_normal((N, Kd), dtype=np.float32) * np.float32(0.02)
+    q, s = DeviceBuffer(N * Kd), DeviceBuffer(((N + 127) // 128) * (Kd // 128) * 4)
+    call("uh_quant_weight_fp8_f32s", dev(w), q, s, N, Kd, None)
+    return q, s
+
+
+@pytest.mark.parametrize("M", [64, 4096])
+def test_full_shape_fp8_dense_config4(M):
+    """A bf16 [M, 4096] -> e4m3 per 1 x 128 (fp32 scales), W e4m3 [4096, 4096] with fp32 128 x 128
+    scales, against the oracle on every row (M = 64) or 512 sampled rows (M = 4096)."""
+    N = Kd = 4096
+    rng = np.random.default_rng(M + 4)
+    x = randn_bf16(rng, (M, Kd))
+    q, sa = DeviceBuffer(M * Kd), DeviceBuffer(M * (Kd // 128) * 4)
+    call("uh_act_quant_fp8_f32s", dev(x), Kd, q, sa, M, Kd, 128, None)
+    wq, ws = _fp8_f32s_weights(rng, N, Kd)
+    c = DeviceBuffer(M * N * 2)
+    call("uh_gemm_fp8_f32s", q, sa, wq, ws, c, N, M, N, Kd, None)
+    rows = np.arange(M) if M <= 64 else np.unique(np.concatenate([[0, M - 1], rng.choice(M, 510, replace=False)]))
+    qh, sah = q.download((M, Kd), np.uint8)[rows], sa.download((M, Kd // 128), np.float32)[rows]
+    ref16, _ = oracle.gemm_w8a8(qh, sah, wq.download((N, Kd), np.uint8), ws.download((N // 128, Kd // 128), np.float32),
+                                threads=16)
+    got = from_bf16(c.download((M, N), np.uint16)[rows])
+    mr = max_rel(got, from_bf16(ref16))
+    print(f"fp8 dense 4096x4096 M={M} ({len(rows)} rows checked): max_rel {mr:.3e}")
+    assert mr <= 1e-2
+
+
+# tools/kernel_test/gemv.hip:91-96: the W8A8 projections of DSV4 (N, K); the head's shape with fp8 weights too (the
+# reference keeps that one in bf16; here it exercises the widest N through the fp8 path)
+DSV4 = [("wq_a", 1024, 4096), ("wkv", 512, 4096), ("wq_b", 32768, 1024), ("wo_b", 4096, 8192), ("sw1", 2048, 4096),
+        ("sw2", 4096, 2048), ("idx_wq_b", 8192, 1024), ("head_fp8", 129280, 4096)]
+
+
+@pytest.mark.parametrize("name,N,Kd", DSV4, ids=[s[0] for s in DSV4])
+def test_dsv4_w8a8_shapes(name, N, Kd):
+    """e8m0 scales on both sides (the reference's W8A8 contract) at M = 1, 8 and 64 through gemm_w8a8, gemm_w8a8_wmma
+    and (M <= 32) gemv_w8a8: against the oracle within the bf16 bar, and every entry point bit-identical."""
+    rng = np.random.default_rng(N + Kd)
+    w = DeviceBuffer(N * Kd)
+    fill_random_bytes(w, N * Kd, N * 7 + Kd, 0, 255)
+    wh = w.download((N, Kd), np.uint8)
+    wh[(wh & 0x7F) == 0x7F] &= 0xFE  # finite codes only (no 0x7f / 0xff)
+    w.upload(wh)
+    sw = rng.integers(118, 126, ((N + 127) // 128, Kd // 128), dtype=np.uint8)
+    dsw = dev(sw)
+    for M in (1, 8, 64):
+        x = randn_bf16(rng, (M, Kd))
+        q_ref, sa_ref = oracle.act_quant_fp8(x)
+        ref16, _ = oracle.gemm_w8a8(q_ref, sa_ref, wh, sw, threads=16)
+        ref = from_bf16(ref16)
+        dq, dsa = dev(q_ref), dev(sa_ref)
+        outs = []
+        for fn in ["uh_gemm_w8a8", "uh_gemm_w8a8_wmma"] + (["uh_gemv_w8a8"] if M <= 32 else []):
+            c = DeviceBuffer(M * N * 2)
+            call(fn, dq, dsa, w, dsw, c, N, M, N, Kd, None)
+            outs.append(c.download((M, N), np.uint16))
+            mr = max_rel(from_bf16(outs[-1]), ref)
+            print(f"{name} M={M} {fn}: max_rel {mr:.3e}")
+            assert mr <= 1e-2, fn
+        for o in outs[1:]:
+            assert np.array_equal(o, outs[0])

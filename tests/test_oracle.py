@@ -267,6 +267,34 @@ def test_rmsnorm_quant_closed_form():
         assert np.array_equal(oracle.rmsnorm_quant(x, w, eps, quant=False), y)
 
 
+def _ulp32(v):
+    """The fp32 ulp at |v| (float64 values), subnormal spacing below 2^-126."""
+    e = np.floor(np.log2(np.maximum(np.abs(v), 2.0 ** -126)))
+    return np.exp2(e - 23)
+
+
+def test_exp_f32_within_2_ulp():
+    """The library's e^x (IEEE operations only, shared bit for bit by the kernels and the oracle) against float64
+    e^x: every 97th fp32 bit pattern of [-103.97, 88.72], every bf16 value, and the special cases."""
+    hi = np.float32(88.7228394).view(np.uint32)
+    lo = np.float32(103.972084).view(np.uint32)
+    pos = np.arange(0, int(hi), 97, dtype=np.uint32).view(np.float32)
+    neg = -np.arange(0, int(lo), 97, dtype=np.uint32).view(np.float32)
+    bfv = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    bfv = bfv[np.isfinite(bfv) & (bfv < 88.72) & (bfv > -103.97)]
+    for x in (pos, neg, bfv):
+        y = oracle.exp_f32(x).astype(np.float64)
+        want = np.exp(x.astype(np.float64))
+        err = np.abs(y - want) / _ulp32(want)
+        assert err.max() <= 2.0, (err.max(), x[np.argmax(err)])
+    special = np.array([0.0, -0.0, 1.0, 89.0, 1e30, -104.0, -1e30, np.inf, -np.inf], np.float32)
+    y = oracle.exp_f32(special)
+    assert y[0] == 1.0 and y[1] == 1.0 and abs(y[2] - np.e) <= 2.4e-7
+    assert np.isposinf(y[3]) and np.isposinf(y[4]) and np.isposinf(y[7])
+    assert y[5] == 0.0 and y[6] == 0.0 and y[8] == 0.0
+    assert np.isnan(oracle.exp_f32(np.array([np.nan], np.float32))[0])
+
+
 # ---- MoE pieces ------------------------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("limit", [10.0, 0.0])
 def test_swiglu_closed_form(limit):

@@ -73,6 +73,11 @@ __global__ __launch_bounds__(256) void quant_weight_kernel(const float* w, uint8
   if (threadIdx.x == 0) s[size_t(bn) * kb + bk] = sc;
 }
 
+__global__ void exp_f32_kernel(const float* x, float* y, size_t n) {
+  for (size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
+    y[i] = uh::exp_f32(x[i]);
+}
+
 // Workspace carve-up of uh_mx_moe_forward.
 struct MoeWs {
   int32_t *count, *off, *fill, *plan, *tiles, *eidx, *row_expert, *pidx, *sel;
@@ -705,6 +710,14 @@ int uh_quant_weight_fp8_f32s(const float* w, uint8_t* q, float* s, int N, int K,
   return guard([&] {
     if (K % 128 || N <= 0) throw std::runtime_error("uh_quant_weight_fp8_f32s: K % 128");
     quant_weight_kernel<<<dim3(unsigned(K / 128), uh::cdiv(size_t(N), 128)), 256, 0, S(st)>>>(w, q, s, N, K);
+    UH_CHECK_LAUNCH();
+  });
+}
+
+int uh_exp_f32_array(const float* x, float* y, size_t n, void* st) {
+  return guard([&] {
+    if (!n) return;
+    exp_f32_kernel<<<std::min<unsigned>(uh::cdiv(n, 256), 4096u), 256, 0, S(st)>>>(x, y, n);
     UH_CHECK_LAUNCH();
   });
 }

@@ -189,13 +189,17 @@ __device__ __forceinline__ void wave_topk(float key[NV], int E, int K, int* chos
 }
 
 __device__ __forceinline__ float ds_score(float x) { return sqrtf(x > 20.0f ? x : log1pf(expf(x))); }
-__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+__device__ __forceinline__ float sigmoid(float x) {
+#pragma clang fp contract(off)
+  return 1.0f / (1.0f + uh::exp_f32(-x));
+}
 
 // Lane 0's part of a router: GLM reports its picks in ascending id; weights in selection (or id) order:
 // mode 0 score / sum * scale, 1 sigmoid / (sum + 1e-20) * scale, 2 exp(l - l_first) / sum. Loops are unrolled
 // over kMaxK so that the picks stay in registers.
 __device__ __forceinline__ void route_weights(int mode, const float* lr, int* chosen, int K, float route_scale,
                                               int32_t* sel_t, float* wt_t, int* ssel, float* swt) {
+#pragma clang fp contract(off)
   if (mode == 1) {
 #pragma unroll
     for (int x = 1; x < kMaxK; ++x)
@@ -213,7 +217,7 @@ __device__ __forceinline__ void route_weights(int mode, const float* lr, int* ch
   for (int k = 0; k < kMaxK; ++k)
     if (k < K) {
       const float l = lr[chosen[k]];
-      w[k] = mode == 2 ? expf(l - l0) : mode == 1 ? sigmoid(l) : ds_score(l);
+      w[k] = mode == 2 ? uh::exp_f32(l - l0) : mode == 1 ? sigmoid(l) : ds_score(l);
       sum += w[k];
     }
 #pragma unroll

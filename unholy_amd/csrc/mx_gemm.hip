@@ -404,7 +404,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
       const uint8_t* sb = sq[sc_q] + size_t(2 * s + sc_j) * sslab + size_t((colq0 + sc_q * colq_step) / 16) * 32;
       if (lane < 16) dma16(sb, uint32_t(lane) * 16, st + uint32_t(GP_A + GP_B + (sc_q * 2 + sc_j) * 256));
     };
-    const int rb_live = __builtin_amdgcn_readfirstlane((M + 31) / 32);
     issue(0);
     {  // activation scales, after stage 0 is in flight (every thread keeps one row: 256 % 128 == 0)
       const int r = min(tid & 127, M - 1);
@@ -532,48 +531,53 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
               for (int i = 0; i < 4; ++i) f(rb * 16 + 4 * g + i, cb * 16 + m16, acc[rb][cb][i]);
         });
       } else {
-        v16f_t acc[RB][2];
+        // Exact dequantization + bf16 MFMA 16x16x32, 16-row blocks: one MFMA per 32-input block, so every output
+        // accumulates acc + (block sum) x (scales) block after block in input order, as the reference's fma chain
+        // over the block and fold (ref_gemm.hip:54-63) does. The block's 32 products are exact (e4m3 x 2^a and
+        // e2m1 x 2^w are bf16 numbers), their sum is exact in fp32 for the activation blocks act_quant produces,
+        // and the MFMA adds it to the accumulator with one rounding: the same fp32 value as the reference order.
+        // Lane (row or column l % 16, g = l / 16) holds inputs 8g .. 8g + 7 of the block on both sides.
+        v4f acc[RB][4];
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-          for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = v16f_t{};
+          for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        const int m16 = lane & 15, g = lane >> 4;
         for (int s = 0; s < KS; ++s) {
           wait_vm<0>();     // this wave's part of stage s (the only stage in flight)
           __syncthreads();  // every wave's part has landed; the other slot (stage s - 1) is free
           if (s + 1 < KS) issue(s + 1);
           const uint8_t* stb = smem + (s % GP_S) * GP_STAGE;
+          float asc[RB];
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) asc[rb] = __uint_as_float(uint32_t(as_lds[s * 128 + rb * 16 + m16]) << 23);
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
-            v4i bq[2];
-            float bs[2];
+            uint32_t bsc2[4];  // the two 32-block scales (h = 0, 1) of this 64-input slab, per column block
 #pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-              const int c = (cq & 1) * 2 + cb, u = q_own * 8 + j * 4 + c, n = c * 32 + l32;
-              bq[cb] = *reinterpret_cast<const v4i*>(stb + GP_A + u * 1024 + (h * 32 + l32) * 16);
-              bs[cb] = __uint_as_float(
-                  uint32_t(stb[GP_A + GP_B + (q_own * 2 + j) * 256 + (n >> 4) * 32 + (n & 15) * 2 + h]) << 23);
-            }
-            v4i aq[RB][2];
-            float asc[RB];
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb) {
-              const int r = rb * 32 + l32;
-#pragma unroll
-              for (int x = 0; x < 2; ++x)
-                aq[rb][x] = *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 * j + 2 * h + x) ^ lds_swz(r))) * 16);
-              asc[rb] = __uint_as_float(uint32_t(as_lds[s * 128 + r]) << 23);
+            for (int cb = 0; cb < 4; ++cb) {
+              const int n = (cq & 1) * 64 + cb * 16 + m16;
+              bsc2[cb] = *reinterpret_cast<const uint16_t*>(stb + GP_A + GP_B + (q_own * 2 + j) * 256 + (n >> 4) * 32 +
+                                                            (n & 15) * 2);
             }
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              bf16x8 bf[2];
+            for (int h = 0; h < 2; ++h) {  // 32-block b = 2 j + h of the stage
+              const int b = 2 * j + h;
+              bf16x8 bf[4];
 #pragma unroll
-              for (int cb = 0; cb < 2; ++cb) bf[cb] = fp4x8_to_bf16(uint32_t(bq[cb][t]), bs[cb]);
+              for (int cb = 0; cb < 4; ++cb) {
+                const int n = (cq & 1) * 64 + cb * 16 + m16, c = n >> 5;
+                const uint32_t w = *reinterpret_cast<const uint32_t*>(
+                    stb + GP_A + (q_own * 8 + j * 4 + c) * 1024 + (h * 32 + (n & 31)) * 16 + 4 * g);
+                bf[cb] = fp4x8_to_bf16(w, __uint_as_float(((bsc2[cb] >> (8 * h)) & 0xffu) << 23));
+              }
 #pragma unroll
               for (int rb = 0; rb < RB; ++rb) {
-                const bf16x8 af = fp8x8_to_bf16(uint32_t(aq[rb][t >> 1][(t & 1) * 2]),
-                                                uint32_t(aq[rb][t >> 1][(t & 1) * 2 + 1]), asc[rb]);
+                const int r = rb * 16 + m16, piece = 2 * b + (g >> 1);
+                const uint2 av = *reinterpret_cast<const uint2*>(stb + (r * 8 + (piece ^ lds_swz(r))) * 16 + (g & 1) * 8);
+                const bf16x8 af = fp8x8_to_bf16(av.x, av.y, asc[rb]);
 #pragma unroll
-                for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = mfma32_bf16(af, bf[cb], acc[rb][cb]);
+                for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = mfma_bf16(af, bf[cb], acc[rb][cb]);
               }
             }
           }
@@ -582,13 +586,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
 #pragma unroll
           for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-            for (int cb = 0; cb < 2; ++cb)
+            for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-              for (int i = 0; i < 16; ++i) f(rb * 32 + 8 * (i / 4) + 4 * h + (i % 4), cb * 32 + l32, acc[rb][cb][i]);
+              for (int i = 0; i < 4; ++i) f(rb * 16 + 4 * g + i, cb * 16 + m16, acc[rb][cb][i]);
         });
       }
     };
-    if constexpr (SC) {
+    {
       const int rb16 = __builtin_amdgcn_readfirstlane((M + 15) / 16);
       if (rb16 == 8) tile_body(std::integral_constant<int, 8>{});
       else if (rb16 == 7) tile_body(std::integral_constant<int, 7>{});
@@ -597,11 +601,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
       else if (rb16 == 4) tile_body(std::integral_constant<int, 4>{});
       else if (rb16 == 3) tile_body(std::integral_constant<int, 3>{});
       else if (rb16 == 2) tile_body(std::integral_constant<int, 2>{});
-      else tile_body(std::integral_constant<int, 1>{});
-    } else {
-      if (rb_live == 4) tile_body(std::integral_constant<int, 4>{});
-      else if (rb_live == 3) tile_body(std::integral_constant<int, 3>{});
-      else if (rb_live == 2) tile_body(std::integral_constant<int, 2>{});
       else tile_body(std::integral_constant<int, 1>{});
     }
   }
@@ -756,10 +755,12 @@ void mx_grouped_gemm_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const 
 namespace {
 int g_gemm_exact = -1;
 }
+// Exact dequantization is the default (the parity arithmetic); UH_GEMM_EXACT=0 in the environment selects the
+// block-scaled MFMA, a speed mode whose sums are not exact (not a parity arithmetic).
 bool mx_gemm_exact() {
   static const bool env = [] {
     const char* v = std::getenv("UH_GEMM_EXACT");
-    return v && v[0] == '1';
+    return !(v && v[0] == '0');
   }();
   return g_gemm_exact < 0 ? env : g_gemm_exact > 0;
 }

@@ -270,33 +270,47 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
 #pragma unroll
     for (int p = 0; p < NP; ++p) acc[p] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     const bool arow = nl < M;
-    const uint8_t* ap = sA + nl * ldA + g * 32;
+    const uint8_t* ap = sA + nl * ldA + g * 8;
     const uint8_t* asp = sS + nl * KS;
-    // One step: the lane's activation inputs 32g .. 32g + 31 of step s (row nl), dequantized to bf16 once for both
-    // projections, then MFMA sub-step t on inputs 32g + 8t .. + 7 of both operands; weights from ring slot i.
+    // One step (128 inputs = four 32-blocks): MFMA t sums block t of the step, so that every output accumulates
+    // acc + (block sum) x (scales) block after block in input order, the reference's order (ref_gemm.hip:54-63: the
+    // 32 products are exact, their sum is exact in fp32 and the MFMA adds it with one rounding). Lane (nl, g)
+    // supplies inputs 8g .. 8g + 7 of block t on both sides. The weights arrive as block g of the step in lane group
+    // g (16 bytes); a 4 x 4 transpose of dwords across the lane groups (two permlane32 and two permlane16 swaps)
+    // hands each group its dword of every block.
     const auto step = [&](int s, int i) {
       bf16x8 af[4];
       if (arow) {
-        const v4i lo = *reinterpret_cast<const v4i*>(ap + s * 128);
-        const v4i hi = *reinterpret_cast<const v4i*>(ap + s * 128 + 16);
         const float sc = e8m0_to_f32(asp[s]);
-        af[0] = fp8x8_to_bf16(lo[0], lo[1], sc);
-        af[1] = fp8x8_to_bf16(lo[2], lo[3], sc);
-        af[2] = fp8x8_to_bf16(hi[0], hi[1], sc);
-        af[3] = fp8x8_to_bf16(hi[2], hi[3], sc);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const uint2 v = *reinterpret_cast<const uint2*>(ap + s * 128 + 32 * t);
+          af[t] = fp8x8_to_bf16(v.x, v.y, sc);
+        }
       } else {
 #pragma unroll
         for (int t = 0; t < 4; ++t) af[t] = bf16x8{};
       }
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
-        // the byte of slab 2 (i % 4) + g / 2 of word i / 4, column nl, 32-block g % 2: dword nl / 2 of that slab,
-        // byte 2 (nl % 2) + g % 2
-        const int src = ((2 * (i % 4) + (g >> 1)) * 8 + (nl >> 1)) * 4;
-        const uint32_t word = uint32_t(__builtin_amdgcn_ds_bpermute(src, int(sq_cur[i / 4][p])));
-        const float sc = __uint_as_float(((word >> (8 * (2 * (nl & 1) + (g & 1)))) & 0xffu) << 23);
+        // the scale bytes of column nl in slabs 2 (i % 4) and 2 (i % 4) + 1 (dword nl / 2 of each, bytes
+        // 2 (nl % 2) + h): blocks t = 2 slab' + h of the step
+        uint32_t sw[2];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[p] = mfma_bf16(af[t], fp4x8_to_bf16(uint32_t(bq[i][p][t]), sc), acc[p]);
+        for (int j = 0; j < 2; ++j) {
+          const int src = ((2 * (i % 4) + j) * 8 + (nl >> 1)) * 4;
+          sw[j] = uint32_t(__builtin_amdgcn_ds_bpermute(src, int(sq_cur[i / 4][p]))) >> (16 * (nl & 1));
+        }
+        const auto r02 = __builtin_amdgcn_permlane32_swap(uint32_t(bq[i][p][0]), uint32_t(bq[i][p][2]), false, false);
+        const auto r13 = __builtin_amdgcn_permlane32_swap(uint32_t(bq[i][p][1]), uint32_t(bq[i][p][3]), false, false);
+        const auto r01 = __builtin_amdgcn_permlane16_swap(r02[0], r13[0], false, false);
+        const auto r23 = __builtin_amdgcn_permlane16_swap(r02[1], r13[1], false, false);
+        const uint32_t wd[4] = {r01[0], r01[1], r23[0], r23[1]};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float sc = __uint_as_float(((sw[t >> 1] >> (8 * (t & 1))) & 0xffu) << 23);
+          acc[p] = mfma_bf16(af[t], fp4x8_to_bf16(wd[t], sc), acc[p]);
+        }
       }
     };
     if (active) {

@@ -188,14 +188,41 @@ __device__ __forceinline__ void quant_token_item(const uint16_t* __restrict__ x,
   if (l == 0) s[size_t(u) * (dim / 128) + b] = blk.se;
 }
 
-// SwiGLU with the clamp and optional routing weight (ref_moe.hip:66-72): x = silu(min(g, l)) * clamp(u, +-l),
-// then w * x; limit <= 0 turns the clamp off.
+// e^x from IEEE operations only (fma, mul, rint; no hardware approximation), so that the kernels and the CPU oracle
+// compute the same bits everywhere e^x decides a stored value (the SwiGLU's silu, the softmax and sigmoid routers'
+// weights). Cody-Waite reduction x = n ln2 + r with ln2 split into a 16-significant-bit high part (n ln2_hi is
+// exact for |n| <= 150) and the rest, |r| <= ln2 / 2; e^r by its degree-7 Taylor polynomial in Horner form with
+// fused multiply-adds (truncation below 2^-27 relative); 2^n applied as two exact power-of-two factors so that
+// results down to the subnormal range are one rounding of p 2^n. Within 2 ulp of e^x (tests/test_oracle.py).
+__device__ __forceinline__ float pow2_f32(int e) { return __uint_as_float(uint32_t(e + 127) << 23); }  // -126..127
+__device__ __forceinline__ float exp_f32(float x) {
+#pragma clang fp contract(off)  // every rounding as written (no multiply-add fused into the caller's add)
+  if (!(x < 88.7228394f)) return x != x ? x : __builtin_inff();
+  if (x < -103.972084f) return 0.0f;
+  const float n = rintf(x * 1.44269504f);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+  r = __builtin_fmaf(-n, 1.42860677e-06f, r);
+  float p = 1.0f / 5040.0f;
+  p = __builtin_fmaf(p, r, 1.0f / 720.0f);
+  p = __builtin_fmaf(p, r, 1.0f / 120.0f);
+  p = __builtin_fmaf(p, r, 1.0f / 24.0f);
+  p = __builtin_fmaf(p, r, 1.0f / 6.0f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  const int ni = int(n), h = ni / 2;
+  return (p * pow2_f32(h)) * pow2_f32(ni - h);
+}
+
+// SwiGLU with the clamp and optional routing weight (ref_moe.hip:62-74): x = silu(min(g, l)) * clamp(u, +-l), then
+// w * x; limit <= 0 turns the clamp off. e^x is exp_f32.
 __device__ __forceinline__ float swiglu_value(float g, float u, float w, bool has_w, float limit) {
+#pragma clang fp contract(off)
   if (limit > 0.0f) {
     u = fminf(fmaxf(u, -limit), limit);
     g = fminf(g, limit);
   }
-  float x = (g / (1.0f + expf(-g))) * u;
+  float x = (g / (1.0f + exp_f32(-g))) * u;
   if (has_w) x = w * x;
   return x;
 }
