@@ -335,6 +335,17 @@ int uh_mx_moe_forward_ev(const uint16_t* x, const float* logits, int T, int K, i
                          const uint8_t* const* tab, float limit, void* ws, size_t ws_bytes, uint16_t* out, int32_t* sel,
                          float* wt, void* stream, void* const* events);
 
+/* No reference counterpart: uh_mx_moe_forward for callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). The workspace is a fixed device array of
+ * uh_mx_moe_noalloc_max_bytes() bytes (8 MiB, one per GPU, held until the process ends; decode and verify batches:
+ * T <= 64 at E = 256, D = 4096, I = 2048 and top-6); shapes whose uh_mx_moe_workspace_size exceeds it fail with an
+ * error. No allocation happens in the call. Every call on one GPU shares that array: calls that overlap on one GPU
+ * (concurrent streams, threads) race and must be serialized by the caller. */
+size_t uh_mx_moe_noalloc_max_bytes(void);
+int uh_mx_moe_forward_noalloc(const uint16_t* x, const float* logits, int T, int K, int E, int D, int I,
+                              const uint8_t* const* tab, float limit, uint16_t* out, int32_t* sel, float* wt,
+                              void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,6 +5,7 @@
 #include <unistd.h>
 
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "common.hpp"
@@ -119,6 +120,30 @@ MoeWs carve(char* base, int T, int K, int E, int D, int I) {
   w.pair_out = reinterpret_cast<bf16*>(take(P * D * 2));
   w.bytes = o;
   return w;
+}
+
+// The no-allocation forward's workspace: one fixed array per device, for callers that cannot allocate (code under
+// graph capture, serving loops). Each GPU holds its own copy until the process ends; host code reaches it only
+// through the address hipGetSymbolAddress returns on that device (the array's name is a host-side stand-in there).
+constexpr size_t kScratchBytes = size_t(8) << 20;
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
+
+// The current device's scratch address, looked up once per device with that device current.
+void* scratch_ptr() {
+  int dev = 0;
+  UH_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) throw std::runtime_error("uh_mx_moe_forward_noalloc: device id out of range");
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    UH_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) throw std::runtime_error("uh_mx_moe_forward_noalloc: no scratch address on device " + std::to_string(dev));
+    g_scratch_ptr[dev] = p;
+  });
+  if (!g_scratch_ptr[dev]) throw std::runtime_error("uh_mx_moe_forward_noalloc: scratch lookup failed earlier");
+  return g_scratch_ptr[dev];
 }
 
 }  // namespace
@@ -806,6 +831,26 @@ int uh_mx_moe_forward_ev(const uint16_t* x, const float* logits, int T, int K, i
     k::moe_combine(w.pair_out, w.pidx, nullptr, out, T, K, D, st);
     mark(5);
   });
+}
+
+size_t uh_mx_moe_noalloc_max_bytes(void) { return kScratchBytes; }
+
+int uh_mx_moe_forward_noalloc(const uint16_t* x, const float* logits, int T, int K, int E, int D, int I,
+                              const uint8_t* const* tab, float limit, uint16_t* out, int32_t* sel, float* wt,
+                              void* stream) {
+  void* ws = nullptr;
+  size_t need = 0;
+  const int rc = guard([&] {
+    need = carve(nullptr, T, K, E, D, I).bytes;
+    if (need > kScratchBytes)
+      throw std::runtime_error("uh_mx_moe_forward_noalloc: the workspace of T=" + std::to_string(T) + ", K=" +
+                               std::to_string(K) + ", E=" + std::to_string(E) + ", D=" + std::to_string(D) +
+                               ", I=" + std::to_string(I) + " is " + std::to_string(need) +
+                               " bytes, above the fixed scratch of " + std::to_string(kScratchBytes) + " bytes");
+    ws = scratch_ptr();
+  });
+  if (rc) return rc;
+  return uh_mx_moe_forward_ev(x, logits, T, K, E, D, I, tab, limit, ws, kScratchBytes, out, sel, wt, stream, nullptr);
 }
 
 }  // extern "C"
