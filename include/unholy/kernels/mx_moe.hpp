@@ -135,6 +135,13 @@ void mx_grouped_gemm_x(const bf16* x, int ldx, const int32_t* x_rows, int K, con
                        const uint8_t* const* w_tab, const uint8_t* const* s_tab, bf16* out, int ldo, int N,
                        hipStream_t st, const int* ntiles_dev = nullptr, const uint8_t* const* w_tab2 = nullptr,
                        const uint8_t* const* s_tab2 = nullptr, bf16* out2 = nullptr, const MxGlu& glu = {});
+// mx_grouped_gemm / mx_grouped_gemm_glu on bf16 rows gathered through x_rows: pair row r of a tile reads row
+// x_rows[r] of xa ([rows, K] bf16; null: row r itself). No reference counterpart (the reference gathers the pair rows
+// in mx_xform_in). K % 64, N % 128 (N % 256 without the epilogue).
+void mx_grouped_gemm_rows(const bf16* xa, const int32_t* x_rows, int K, const Exl3Tile* tiles, int ntiles,
+                          const uint8_t* const* w_tab, const uint8_t* const* s_tab, bf16* out, int ldo, int N,
+                          hipStream_t st, const int* ntiles_dev = nullptr, const uint8_t* const* w_tab2 = nullptr,
+                          const uint8_t* const* s_tab2 = nullptr, bf16* out2 = nullptr, const MxGlu& glu = {});
 // The prefill GEMM on e4m3 codes with fp32 outputs (no bf16 rounding): for accuracy checks against an fp64 oracle.
 // No reference counterpart.
 void mx_grouped_gemm_q_f32out(const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles, int ntiles,

@@ -4,6 +4,7 @@
 #include <fcntl.h>
 #include <unistd.h>
 
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -79,11 +80,23 @@ __global__ void exp_f32_kernel(const float* x, float* y, size_t n) {
     y[i] = uh::exp_f32(x[i]);
 }
 
+// UH_PREFILL_FP8=1: the prefill forward feeds the GEMMs e4m3 codes + scales (mx_grouped_gemm_q) instead of bf16
+// rows (comparison runs; both are bit-identical). The block-scaled speed mode (mx_gemm_set_exact(0)) always takes
+// the e4m3 codes, the operands of its MFMA.
+static bool prefill_fp8() {
+  static const bool on = [] {
+    const char* e = std::getenv("UH_PREFILL_FP8");
+    return e && e[0] == '1';
+  }();
+  return on;
+}
+
 // Workspace carve-up of uh_mx_moe_forward.
 struct MoeWs {
   int32_t *count, *off, *fill, *plan, *tiles, *eidx, *row_expert, *pidx, *sel;
   float *ewt, *wt;
   uint8_t *xq, *xs, *hq, *hs;
+  bf16 *xa, *hh;  // prefill: fake-quantized token rows [T, D] (in xq's bytes) and SwiGLU rows [P, I]
   bf16* h;  // raw SwiGLU rows [P, I] (T <= 64 path); shares xq's bytes (P * D >= P * I * 2), which only prefill uses
   bf16* pair_out;
   size_t bytes;
@@ -117,6 +130,8 @@ MoeWs carve(char* base, int T, int K, int E, int D, int I) {
   w.xs = reinterpret_cast<uint8_t*>(take(P * (D / 128)));
   w.hq = reinterpret_cast<uint8_t*>(take(P * I));
   w.hs = reinterpret_cast<uint8_t*>(take(P * (I / 128)));
+  w.xa = reinterpret_cast<bf16*>(w.xq);  // T * D * 2 <= P * D
+  w.hh = T > 64 ? reinterpret_cast<bf16*>(take(P * I * 2)) : nullptr;
   w.pair_out = reinterpret_cast<bf16*>(take(P * D * 2));
   w.bytes = o;
   return w;
@@ -816,6 +831,19 @@ int uh_mx_moe_forward_ev(const uint16_t* x, const float* logits, int T, int K, i
       mark(3);
       k::mx_grouped_gemv_x(w.h, I, nullptr, I, tiles, w.max_tiles, t(2, 0), t(2, 1), w.pair_out, D, D, st, ntd,
                            nullptr, nullptr, nullptr, rows, k::MxGlu{});
+    } else if (!prefill_fp8() && k::mx_gemm_exact()) {
+      // Each token row fake-quantized once to bf16 (exact e4m3 x 2^k values; its K picks would otherwise be
+      // quantized K times); the w1 / w3 GEMM gathers the pair rows through eidx and writes the fake-quantized
+      // SwiGLU rows hh, the w2 GEMM's bf16 input.
+      k::mx_xform_in(x, D, nullptr, nullptr, w.xa, T, D, st, nullptr);
+      mark(2);
+      k::MxGlu gb = glu;
+      gb.hq = gb.hs = nullptr;
+      gb.hh = w.hh;
+      k::mx_grouped_gemm_rows(w.xa, w.eidx, D, tiles, w.max_tiles, t(0, 0), t(0, 1), nullptr, I, I, st, ntd, t(1, 0),
+                              t(1, 1), nullptr, gb);
+      mark(3);
+      k::mx_grouped_gemm_rows(w.hh, nullptr, I, tiles, w.max_tiles, t(2, 0), t(2, 1), w.pair_out, D, D, st, ntd);
     } else {
       // Each token row quantized once (its K picks would otherwise be quantized K times); the GEMM's loads gather
       // the pair rows' codes through eidx.

@@ -352,6 +352,85 @@ constexpr int GP_LDC1 = 256 + 8, GP_LDC2 = 128 + 8;
 constexpr int GP_C1 = 128 * GP_LDC1 * 2, GP_C2 = 2 * 128 * GP_LDC2 * 2;
 static_assert(GP_C1 <= GP_RING, "the bf16 C tile reuses the ring");
 
+// The bf16 / fp32 / SwiGLU epilogue of the pipelined kernels. each(f) calls f(row, column within the wave's 64, value)
+// for every accumulator element; the ring is reused as the C tile.
+template <int NP, class Each>
+__device__ __forceinline__ void gp_epilogue(const MxGemvArgs& a, uint8_t* smem, int M, size_t row0, int bx, int cq,
+                                            int tid, const Each& each) {
+  const int N = a.N, q_own = cq >> 1;
+  // ---- the ring is free once every wave is past its last stage
+  __syncthreads();
+  if constexpr (NP == 1) {
+    const int c0 = cq * 64;
+    if (a.out32) {  // fp32 outputs (accuracy checks): two passes of 64 rows through the ring
+      constexpr int LDF = 256 + 4;
+      static_assert(64 * LDF * 4 <= GP_RING, "a 64-row fp32 half tile fits the ring");
+      float* sf = reinterpret_cast<float*>(smem);
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        if (half) __syncthreads();  // the first half's stores have read the tile
+        each([&](int row, int col, float v) {
+          if (row >= 64 * half && row < 64 * half + 64) sf[(row - 64 * half) * LDF + c0 + col] = v;
+        });
+        __syncthreads();
+        for (int e = tid; e < min(64, M - 64 * half) * 64; e += 256) {
+          const int r = e / 64, c4 = (e % 64) * 4;
+          *reinterpret_cast<float4*>(a.out32 + (row0 + 64 * half + r) * a.ldo + bx * 256 + c4) =
+              *reinterpret_cast<const float4*>(sf + r * LDF + c4);
+        }
+      }
+    } else {
+      uint16_t* sc = reinterpret_cast<uint16_t*>(smem);
+      each([&](int row, int col, float v) { sc[row * GP_LDC1 + c0 + col] = f32_to_bf16(v); });
+      __syncthreads();
+      for (int e = tid; e < M * 32; e += 256) {
+        const int r = e / 32, c8 = (e % 32) * 8;
+        *reinterpret_cast<uint4*>(a.out[0] + (row0 + r) * a.ldo + bx * 256 + c8) =
+            *reinterpret_cast<const uint4*>(sc + r * GP_LDC1 + c8);
+      }
+    }
+  } else {
+    // bf16 g (w1) and u (w3) tiles in LDS, then 8 consecutive outputs of one row per thread: h = bf16(SwiGLU(g, u)),
+    // the row's amax over its 128 outputs (16 threads: a DPP row max), fake quantization, 16-byte stores.
+    uint16_t* const tg = reinterpret_cast<uint16_t*>(smem);
+    uint16_t* const tu = tg + 128 * GP_LDC2;
+    uint16_t* const mine = q_own ? tu : tg;
+    const int chh = cq & 1;
+    each([&](int row, int col, float v) { mine[row * GP_LDC2 + chh * 64 + col] = f32_to_bf16(v); });
+    __syncthreads();
+    for (int e0 = 0; e0 < M * 16; e0 += 256) {  // uniform bound: every 16-lane group is whole
+      const int e = e0 + tid, r = min(e / 16, M - 1), c8 = (e % 16) * 8;
+      const size_t row = row0 + r;
+      const uint4 gv4 = *reinterpret_cast<const uint4*>(tg + r * GP_LDC2 + c8);
+      const uint4 uv4 = *reinterpret_cast<const uint4*>(tu + r * GP_LDC2 + c8);
+      const uint32_t gw4[4] = {gv4.x, gv4.y, gv4.z, gv4.w}, uw4[4] = {uv4.x, uv4.y, uv4.z, uv4.w};
+      const float w = a.gw ? a.gw[row] : 0.0f;
+      float hv[8], am = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        hv[q] = round_bf16(swiglu_value(bf16_to_f32(uint16_t(gw4[q / 2] >> (16 * (q % 2)))),
+                                        bf16_to_f32(uint16_t(uw4[q / 2] >> (16 * (q % 2)))), w, a.gw != nullptr,
+                                        a.limit));
+        am = fmaxf(am, fabsf(hv[q]));
+      }
+      am = row16_max(am);
+      if (e >= M * 16) continue;
+      const size_t oc = row * a.ldo + size_t(bx) * 128 + c8;
+      if (a.out[0]) *reinterpret_cast<uint4*>(a.out[0] + oc) = gv4;
+      if (a.out[1]) *reinterpret_cast<uint4*>(a.out[1] + oc) = uv4;
+      if (a.gs_tab && !a.gs_tab[a.grow_expert[row]]) continue;
+      const Fp8Block blk = fp8_block_scale(am);
+      uint32_t qb[2];
+      fp8_codes8(hv, blk, qb[0], qb[1]);
+      const size_t o = row * N + size_t(bx) * 128 + c8;
+      if (a.hq) *reinterpret_cast<uint2*>(a.hq + o) = make_uint2(qb[0], qb[1]);
+      if (a.hh)  // the fake-quantized rows (the codes decoded back, exact), only when asked for
+        *reinterpret_cast<uint4*>(a.hh + o) = __builtin_bit_cast(uint4, fp8x8_to_bf16(qb[0], qb[1], blk.sc));
+      if (a.hs && c8 == 0) a.hs[row * (N / 128) + bx] = blk.se;
+    }
+  }
+}
+
 template <int NP, bool SC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mx_gemm_pipe_kernel(MxGemvArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
@@ -405,85 +484,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
       if (lane < 16) dma16(sb, uint32_t(lane) * 16, st + uint32_t(GP_A + GP_B + (sc_q * 2 + sc_j) * 256));
     };
     issue(0);
-    {  // activation scales, after stage 0 is in flight (every thread keeps one row: 256 % 128 == 0)
+    {  // activation scales, after stage 0 is in flight (every thread keeps one row: 256 % 128 == 0). Row r of
+       // stage s sits at s * 128 + (r % 16) * 8 + r / 16, so a lane's 8 row blocks are one 8-byte read.
       const int r = min(tid & 127, M - 1);
       const uint8_t* srow = a.as + size_t(a.x_rows ? a.x_rows[row0 + r] : int(row0 + r)) * KS;
-      for (int e = tid; e < 128 * KS; e += 256) as_lds[e] = srow[e >> 7];
+      for (int e = tid; e < 128 * KS; e += 256) as_lds[(e & ~127) + (e & 15) * 8 + ((e >> 4) & 7)] = srow[e >> 7];
     }
     // The epilogue, given each(f): f(row, column in the wave's 64, value) for every accumulator element.
-    const auto epilogue = [&](const auto& each) {
-      // ---- the ring is free once every wave is past its last stage
-      __syncthreads();
-      if constexpr (NP == 1) {
-        const int c0 = cq * 64;
-        if (a.out32) {  // fp32 outputs (accuracy checks): two passes of 64 rows through the ring
-          constexpr int LDF = 256 + 4;
-          static_assert(64 * LDF * 4 <= GP_RING, "a 64-row fp32 half tile fits the ring");
-          float* sf = reinterpret_cast<float*>(smem);
-#pragma unroll
-          for (int half = 0; half < 2; ++half) {
-            if (half) __syncthreads();  // the first half's stores have read the tile
-            each([&](int row, int col, float v) {
-              if (row >= 64 * half && row < 64 * half + 64) sf[(row - 64 * half) * LDF + c0 + col] = v;
-            });
-            __syncthreads();
-            for (int e = tid; e < min(64, M - 64 * half) * 64; e += 256) {
-              const int r = e / 64, c4 = (e % 64) * 4;
-              *reinterpret_cast<float4*>(a.out32 + (row0 + 64 * half + r) * a.ldo + bx * 256 + c4) =
-                  *reinterpret_cast<const float4*>(sf + r * LDF + c4);
-            }
-          }
-        } else {
-          uint16_t* sc = reinterpret_cast<uint16_t*>(smem);
-          each([&](int row, int col, float v) { sc[row * GP_LDC1 + c0 + col] = f32_to_bf16(v); });
-          __syncthreads();
-          for (int e = tid; e < M * 32; e += 256) {
-            const int r = e / 32, c8 = (e % 32) * 8;
-            *reinterpret_cast<uint4*>(a.out[0] + (row0 + r) * a.ldo + bx * 256 + c8) =
-                *reinterpret_cast<const uint4*>(sc + r * GP_LDC1 + c8);
-          }
-        }
-      } else {
-        // bf16 g (w1) and u (w3) tiles in LDS, then 8 consecutive outputs of one row per thread: h = bf16(SwiGLU(g, u)),
-        // the row's amax over its 128 outputs (16 threads: a DPP row max), fake quantization, 16-byte stores.
-        uint16_t* const tg = reinterpret_cast<uint16_t*>(smem);
-        uint16_t* const tu = tg + 128 * GP_LDC2;
-        uint16_t* const mine = q_own ? tu : tg;
-        const int chh = cq & 1;
-        each([&](int row, int col, float v) { mine[row * GP_LDC2 + chh * 64 + col] = f32_to_bf16(v); });
-        __syncthreads();
-        for (int e0 = 0; e0 < M * 16; e0 += 256) {  // uniform bound: every 16-lane group is whole
-          const int e = e0 + tid, r = min(e / 16, M - 1), c8 = (e % 16) * 8;
-          const size_t row = row0 + r;
-          const uint4 gv4 = *reinterpret_cast<const uint4*>(tg + r * GP_LDC2 + c8);
-          const uint4 uv4 = *reinterpret_cast<const uint4*>(tu + r * GP_LDC2 + c8);
-          const uint32_t gw4[4] = {gv4.x, gv4.y, gv4.z, gv4.w}, uw4[4] = {uv4.x, uv4.y, uv4.z, uv4.w};
-          const float w = a.gw ? a.gw[row] : 0.0f;
-          float hv[8], am = 0.0f;
-#pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            hv[q] = round_bf16(swiglu_value(bf16_to_f32(uint16_t(gw4[q / 2] >> (16 * (q % 2)))),
-                                            bf16_to_f32(uint16_t(uw4[q / 2] >> (16 * (q % 2)))), w, a.gw != nullptr,
-                                            a.limit));
-            am = fmaxf(am, fabsf(hv[q]));
-          }
-          am = row16_max(am);
-          if (e >= M * 16) continue;
-          const size_t oc = row * a.ldo + size_t(bx) * 128 + c8;
-          if (a.out[0]) *reinterpret_cast<uint4*>(a.out[0] + oc) = gv4;
-          if (a.out[1]) *reinterpret_cast<uint4*>(a.out[1] + oc) = uv4;
-          if (a.gs_tab && !a.gs_tab[a.grow_expert[row]]) continue;
-          const Fp8Block blk = fp8_block_scale(am);
-          uint32_t qb[2];
-          fp8_codes8(hv, blk, qb[0], qb[1]);
-          const size_t o = row * N + size_t(bx) * 128 + c8;
-          if (a.hq) *reinterpret_cast<uint2*>(a.hq + o) = make_uint2(qb[0], qb[1]);
-          if (a.hh)  // the fake-quantized rows (the codes decoded back, exact), only when asked for
-            *reinterpret_cast<uint4*>(a.hh + o) = __builtin_bit_cast(uint4, fp8x8_to_bf16(qb[0], qb[1], blk.sc));
-          if (a.hs && c8 == 0) a.hs[row * (N / 128) + bx] = blk.se;
-        }
-      }
-    };
 
     // The K loop, specialised on the tile's live row blocks (RB): each stage is one basic block the compiler can
     // interleave, and only live accumulators exist (dead ones kept alive across the loop cost register copies in
@@ -517,12 +524,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
             const v4i lo = *reinterpret_cast<const v4i*>(stb + (r * 8 + (g ^ lds_swz(r))) * 16);
             const v4i hi = *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 + g) ^ lds_swz(r))) * 16);
             const v8i aq = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            const int asc = as_lds[s * 128 + r];
+            const int asc = as_lds[s * 128 + m16 * 8 + rb];
 #pragma unroll
             for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = mfma_fp8_fp4(aq, bq[cb], asc, bsc[cb], acc[rb][cb]);
           }
         }
-        epilogue([&](const auto& f) {
+        gp_epilogue<NP>(a, smem, M, row0, bx, cq, tid, [&](const auto& f) {
 #pragma unroll
           for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
@@ -537,52 +544,74 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
         // e2m1 x 2^w are bf16 numbers), their sum is exact in fp32 for the activation blocks act_quant produces,
         // and the MFMA adds it to the accumulator with one rounding: the same fp32 value as the reference order.
         // Lane (row or column l % 16, g = l / 16) holds inputs 8g .. 8g + 7 of the block on both sides.
+        //
+        // Software pipelined: a stage's B words, B scales and A scales are read right after its barrier, and the A
+        // pieces of block b + 1 are read while block b's conversions and MFMAs run, so LDS latency is hidden
+        // behind 4 x RB MFMAs instead of being waited for before each row block.
         v4f acc[RB][4];
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
           for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
         const int m16 = lane & 15, g = lane >> 4;
+        // A piece of row rb * 16 + m16 for block b: byte (a_lane ^ (b << 5)) + rb * 2048 of the stage. The swizzle
+        // lds_swz(r) depends on m16 only (rb * 16 >> 1 is a multiple of 8), and piece 2b + (g >> 1) = 2b ^ (g >> 1).
+        const uint32_t a_lane =
+            uint32_t(m16 * 128 + (((g >> 1) ^ lds_swz(m16)) << 4) + (g & 1) * 8);
+        // B word of column block cb, block b = 2j + h: byte b_lane + j * 4096 + (cb >> 1) * 1024 + h * 512 +
+        // (cb & 1) * 256 of the stage; its scales (both h of slab j) the u16 at s_lane + j * 256 + cb * 32.
+        const uint32_t b_lane = uint32_t(GP_A + q_own * 8192 + (cq & 1) * 2048 + m16 * 16 + 4 * g);
+        const uint32_t s_lane = uint32_t(GP_A + GP_B + q_own * 512 + (cq & 1) * 128 + m16 * 2);
         for (int s = 0; s < KS; ++s) {
           wait_vm<0>();     // this wave's part of stage s (the only stage in flight)
           __syncthreads();  // every wave's part has landed; the other slot (stage s - 1) is free
           if (s + 1 < KS) issue(s + 1);
           const uint8_t* stb = smem + (s % GP_S) * GP_STAGE;
+          const uint2 asw = *reinterpret_cast<const uint2*>(as_lds + s * 128 + m16 * 8);
+          uint32_t bsc[2][4], bw[4][4];
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+              bsc[j][cb] = *reinterpret_cast<const uint16_t*>(stb + s_lane + j * 256 + cb * 32);
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+              bw[b][cb] = *reinterpret_cast<const uint32_t*>(stb + b_lane + (b >> 1) * 4096 + (cb >> 1) * 1024 +
+                                                             (b & 1) * 512 + (cb & 1) * 256);
+          uint2 araw[2][RB];
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) araw[0][rb] = *reinterpret_cast<const uint2*>(stb + a_lane + rb * 2048);
           float asc[RB];
 #pragma unroll
-          for (int rb = 0; rb < RB; ++rb) asc[rb] = __uint_as_float(uint32_t(as_lds[s * 128 + rb * 16 + m16]) << 23);
+          for (int rb = 0; rb < RB; ++rb)
+            asc[rb] = __uint_as_float((((rb < 4 ? asw.x : asw.y) >> (8 * (rb & 3))) & 0xffu) << 23);
+          __builtin_amdgcn_sched_barrier(0);  // the stage's reads all issued before any use
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            uint32_t bsc2[4];  // the two 32-block scales (h = 0, 1) of this 64-input slab, per column block
+          for (int b = 0; b < 4; ++b) {
+            if (b < 3) {
+#pragma unroll
+              for (int rb = 0; rb < RB; ++rb)
+                araw[(b + 1) & 1][rb] =
+                    *reinterpret_cast<const uint2*>(stb + (a_lane ^ uint32_t((b + 1) << 5)) + rb * 2048);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep the reads of block b + 1 ahead of block b's MFMAs
+            bf16x8 bf[4];
 #pragma unroll
             for (int cb = 0; cb < 4; ++cb) {
-              const int n = (cq & 1) * 64 + cb * 16 + m16;
-              bsc2[cb] = *reinterpret_cast<const uint16_t*>(stb + GP_A + GP_B + (q_own * 2 + j) * 256 + (n >> 4) * 32 +
-                                                            (n & 15) * 2);
+              bf[cb] = fp4x8_to_bf16(bw[b][cb], __uint_as_float(((bsc[b >> 1][cb] >> (8 * (b & 1))) & 0xffu) << 23));
             }
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {  // 32-block b = 2 j + h of the stage
-              const int b = 2 * j + h;
-              bf16x8 bf[4];
+            for (int rb = 0; rb < RB; ++rb) {
+              const uint2 av = araw[b & 1][rb];
+              const bf16x8 af = fp8x8_to_bf16(av.x, av.y, asc[rb]);
 #pragma unroll
-              for (int cb = 0; cb < 4; ++cb) {
-                const int n = (cq & 1) * 64 + cb * 16 + m16, c = n >> 5;
-                const uint32_t w = *reinterpret_cast<const uint32_t*>(
-                    stb + GP_A + (q_own * 8 + j * 4 + c) * 1024 + (h * 32 + (n & 31)) * 16 + 4 * g);
-                bf[cb] = fp4x8_to_bf16(w, __uint_as_float(((bsc2[cb] >> (8 * h)) & 0xffu) << 23));
-              }
-#pragma unroll
-              for (int rb = 0; rb < RB; ++rb) {
-                const int r = rb * 16 + m16, piece = 2 * b + (g >> 1);
-                const uint2 av = *reinterpret_cast<const uint2*>(stb + (r * 8 + (piece ^ lds_swz(r))) * 16 + (g & 1) * 8);
-                const bf16x8 af = fp8x8_to_bf16(av.x, av.y, asc[rb]);
-#pragma unroll
-                for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = mfma_bf16(af, bf[cb], acc[rb][cb]);
-              }
+              for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = mfma_bf16(af, bf[cb], acc[rb][cb]);
             }
           }
         }
-        epilogue([&](const auto& f) {
+        gp_epilogue<NP>(a, smem, M, row0, bx, cq, tid, [&](const auto& f) {
 #pragma unroll
           for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
@@ -607,10 +636,167 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
 }
 
 
+// ---- Pipelined kernel for bf16 activation rows (exact e4m3 x 2^k values, the fake-quantized rows of mx_xform_in) ----
+//
+// The same workgroup shape as mx_gemm_pipe_kernel (256 threads, one tile x 256 output columns, wave w owns columns
+// 64 w .. 64 w + 63 over all rows, 16x16x32 bf16 MFMAs, one per 32-input block), but the activations arrive as bf16:
+// they go from LDS straight into the MFMA with no conversion, and only the weights are dequantized (half a
+// conversion per MFMA instead of one and a half). Stages are 64 inputs, three ring slots of 24.5 KB (73.5 KB, two
+// workgroups per CU), two stages in flight. Per stage a slot holds
+//   A  16 KB: 128 rows x 64 bf16, row r's 16-byte piece p at slot r * 8 + (p ^ lds_swz(r));
+//   B   8 KB: 8 blocks of 1 KB = (projection or column half q, 32-column block c), slot h * 32 + n <- piece 2n + h;
+//   Bs 512 B: the e8m0 weight scales of projection q at q * 256 in their global order.
+// Every wave issues 4 A, 2 B and 1 scale load per stage (7 vm operations).
+constexpr int GB_KS = 64, GB_A = 128 * 128, GB_B = 8 * 1024, GB_BS = 512;
+constexpr int GB_STAGE = GB_A + GB_B + GB_BS;
+constexpr int GB_S = 3, GB_RING = GB_S * GB_STAGE;
+static_assert(GP_C1 <= GB_RING && GP_C2 <= GB_RING && 64 * (256 + 4) * 4 <= GB_RING, "the C tiles reuse the ring");
+
+template <int NP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mx_gemm_pipe_bf16_kernel(MxGemvArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  int bx, by;
+  tile_block(gridDim.x, bx, by);
+  if (by >= a.ntiles || (a.ntiles_dev && by >= *a.ntiles_dev)) return;
+  const Exl3Tile tile = a.tiles[by];
+  if (tile.rows <= 0) return;
+  const uint8_t* wq[2];
+  const uint8_t* sq[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    wq[q] = a.w_tab[NP == 2 ? q : 0][tile.expert];
+    sq[q] = a.s_tab[NP == 2 ? q : 0][tile.expert];
+    if (!wq[q] || !sq[q]) return;
+  }
+  const int K = a.K, KS = K / GB_KS, N = a.N, ntn = N / 16;
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // column quarter
+  const int cq = wave, q_own = cq >> 1;
+  const int colq0 = NP == 2 ? bx * 128 : bx * 256, colq_step = NP == 2 ? 0 : 128;
+  const size_t cslab = size_t(ntn) * 512, sslab = size_t(ntn) * 32;
+  const uint32_t lds0 = lds_addr(smem);
+  const uint32_t boff = uint32_t((l32 * 2 + h) * 16);  // B block: slot h*32+n <- piece 2n+h
+  const int m16 = lane & 15, g = lane >> 4;
+  // A piece of row rb * 16 + m16, inputs 32 b + 8 g .. + 7 (piece 4b + g): byte a_lane[b] + rb * 2048 of the stage
+  // (lds_swz(rb * 16 + m16) == lds_swz(m16)).
+  const uint32_t a_lane0 = uint32_t(m16 * 128 + ((g ^ lds_swz(m16)) << 4));
+  const uint32_t a_lane1 = uint32_t(m16 * 128 + (((4 + g) ^ lds_swz(m16)) << 4));
+  // B word of column block cb, block b: byte b_lane + (cb >> 1) * 1024 + b * 512 + (cb & 1) * 256; the two scales
+  // of column block cb (b = 0, 1) the u16 at s_lane + cb * 32.
+  const uint32_t b_lane = uint32_t(GB_A + q_own * 4096 + (cq & 1) * 2048 + m16 * 16 + 4 * g);
+  const uint32_t s_lane = uint32_t(GB_A + GB_B + q_own * 256 + (cq & 1) * 128 + m16 * 2);
+  const uint32_t row_bytes = uint32_t(K) * 2u;
+
+  for (int rg = 0; rg < tile.rows; rg += 128) {
+    const int M = min(128, tile.rows - rg);
+    const size_t row0 = size_t(tile.row0) + rg;
+    __syncthreads();  // the previous row group's LDS use is over
+    uint32_t aoff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int slot = (wave * 4 + i) * 64 + lane, r = slot >> 3, p = (slot & 7) ^ lds_swz(r);
+      const int rr = min(r, M - 1);  // rows past the tile repeat its last
+      aoff[i] = (a.x_rows ? uint32_t(a.x_rows[row0 + rr]) : uint32_t(rr)) * row_bytes + uint32_t(p * 16);
+    }
+    const uint8_t* arow = reinterpret_cast<const uint8_t*>(a.x_rows ? a.xa : a.xa + row0 * size_t(K));
+    const auto issue = [&](int s) {
+      const uint32_t st = __builtin_amdgcn_readfirstlane(lds0 + uint32_t((s % GB_S) * GB_STAGE));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dma16(arow + s * 128, aoff[i], st + uint32_t(wave * 4 + i) * 1024);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int u = wave * 2 + i, q = u >> 2, c = u & 3;
+        const uint8_t* bb = wq[q] + size_t(s) * cslab + size_t((colq0 + q * colq_step) / 16) * 512 + c * 1024;
+        dma16_nt(bb, boff, st + uint32_t(GB_A + u * 1024));
+      }
+      {  // scales: wave w copies bytes 128 w .. + 127 (projection w / 2), 8 lanes of 16 bytes
+        const int q = wave >> 1;
+        const uint8_t* sb = sq[q] + size_t(s) * sslab + size_t((colq0 + q * colq_step) / 16) * 32 + (wave & 1) * 128;
+        if (lane < 8) dma16(sb, uint32_t(lane) * 16, st + uint32_t(GB_A + GB_B + wave * 128));
+      }
+    };
+    issue(0);
+    if (KS > 1) issue(1);
+
+    const auto tile_body = [&](auto nrb) {
+      constexpr int RB = decltype(nrb)::value;
+      v4f acc[RB][4];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int s = 0; s < KS; ++s) {
+        if (s + 1 < KS) wait_vm<7>();  // stage s has landed; stage s + 1 may still be in flight
+        else wait_vm<0>();
+        __syncthreads();  // every wave's part of stage s has landed; slot (s + 2) % 3 (stage s - 1) is free
+        if (s + 2 < KS) issue(s + 2);
+        const uint8_t* stb = smem + (s % GB_S) * GB_STAGE;
+        uint32_t bsc[4], bw[2][4];
+        bf16x8 af[2][RB];
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) bsc[cb] = *reinterpret_cast<const uint16_t*>(stb + s_lane + cb * 32);
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int cb = 0; cb < 4; ++cb)
+            bw[b][cb] = *reinterpret_cast<const uint32_t*>(stb + b_lane + (cb >> 1) * 1024 + b * 512 + (cb & 1) * 256);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) af[0][rb] = *reinterpret_cast<const bf16x8*>(stb + a_lane0 + rb * 2048);
+        __builtin_amdgcn_sched_barrier(0);  // the stage's first reads all issued before any use
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) af[1][rb] = *reinterpret_cast<const bf16x8*>(stb + a_lane1 + rb * 2048);
+        __builtin_amdgcn_sched_barrier(0);  // block 1's A reads issued ahead of block 0's MFMAs
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          bf16x8 bf[4];
+#pragma unroll
+          for (int cb = 0; cb < 4; ++cb)
+            bf[cb] = fp4x8_to_bf16(bw[b][cb], __uint_as_float(((bsc[cb] >> (8 * b)) & 0xffu) << 23));
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = mfma_bf16(af[b][rb], bf[cb], acc[rb][cb]);
+        }
+      }
+      gp_epilogue<NP>(a, smem, M, row0, bx, cq, tid, [&](const auto& f) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) f(rb * 16 + 4 * g + i, cb * 16 + m16, acc[rb][cb][i]);
+      });
+    };
+    {
+      const int rb16 = __builtin_amdgcn_readfirstlane((M + 15) / 16);
+      if (rb16 == 8) tile_body(std::integral_constant<int, 8>{});
+      else if (rb16 == 7) tile_body(std::integral_constant<int, 7>{});
+      else if (rb16 == 6) tile_body(std::integral_constant<int, 6>{});
+      else if (rb16 == 5) tile_body(std::integral_constant<int, 5>{});
+      else if (rb16 == 4) tile_body(std::integral_constant<int, 4>{});
+      else if (rb16 == 3) tile_body(std::integral_constant<int, 3>{});
+      else if (rb16 == 2) tile_body(std::integral_constant<int, 2>{});
+      else tile_body(std::integral_constant<int, 1>{});
+    }
+  }
+}
+
 template <int NP>
 void launch_pipe_t(const MxGemvArgs& a, int ntiles, hipStream_t st) {
   const size_t lds = std::max<size_t>(size_t(GP_RING) + size_t(128) * (a.K / 128), NP == 2 ? GP_C2 : GP_C1);
   auto* kern = mx_gemm_exact() ? &mx_gemm_pipe_kernel<NP, false> : &mx_gemm_pipe_kernel<NP, true>;
+  UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               int(lds)));
+  MxGemvArgs b = a;
+  b.ntiles = ntiles;
+  kern<<<tile_grid(a.N / (NP == 2 ? 128 : 256), ntiles), 256, lds, st>>>(b);
+  UH_CHECK_LAUNCH();
+}
+
+template <int NP>
+void launch_pipe_bf16_t(const MxGemvArgs& a, int ntiles, hipStream_t st) {
+  const size_t lds = GB_RING;
+  auto* kern = &mx_gemm_pipe_bf16_kernel<NP>;
   UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                int(lds)));
   MxGemvArgs b = a;
@@ -645,7 +831,13 @@ static bool pipe_disabled() {
 
 void launch_mx_gemm(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st) {
   if (ntiles <= 0) return;
-  if (a.K % GM_KS || a.N % 128 || a.K <= 0 || a.N <= 0) throw std::runtime_error("mx_grouped_gemm: K % 128 or N % 128");
+  // bf16 activation rows (amode 1) take the 64-input-stage pipelined kernel: K % 64 as the reference asks
+  // (mx_moe.hip:1045); the other kernels stage 128 inputs at a time.
+  const bool glu_ = a.hh || a.hq;  // (two projections without the epilogue run as two one-projection launches)
+  const bool pipe16 = amode == 1 && !pipe_disabled() && a.N % 128 == 0 && (glu_ || a.N % 256 == 0) &&
+                      a.K % GB_KS == 0;
+  if (a.K <= 0 || a.N <= 0 || a.N % 128 || (!pipe16 && a.K % GM_KS))
+    throw std::runtime_error("mx_grouped_gemm: K % 128 (K % 64 for bf16 rows) or N % 128");
   const bool np2 = a.w_tab[1] != nullptr, glu = a.hh || a.hq;
   if (np2 && !glu) {  // two projections without the epilogue: one launch each
     MxGemvArgs b = a;
@@ -674,7 +866,10 @@ void launch_mx_gemm(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st) 
   const bool pipe = amode == 0 && a.K / GM_KS <= GP_MAX_KS && !pipe_disabled();
   if (amode == 0 && a.x_rows && (!pipe || (!glu && a.N % 256)))
     throw std::runtime_error("mx_grouped_gemm_q: x_rows needs the pipelined kernel (K <= 14336, N % 256 without glu)");
-  if (glu) {
+  if (pipe16) {
+    if (glu) launch_pipe_bf16_t<2>(a, ntiles, st);
+    else launch_pipe_bf16_t<1>(a, ntiles, st);
+  } else if (glu) {
     if (pipe) launch_pipe_t<2>(a, ntiles, st);
     else UH_GM(2);
   } else {
@@ -779,6 +974,19 @@ void mx_grouped_gemm_x(const bf16* x, int ldx, const int32_t* x_rows, int K, con
   a.x_rows = x_rows;
   a.ldx = ldx;
   launch_mx_gemm(a, ntiles, 2, st);
+}
+
+void mx_grouped_gemm_rows(const bf16* xa, const int32_t* x_rows, int K, const Exl3Tile* tiles, int ntiles,
+                          const uint8_t* const* w_tab, const uint8_t* const* s_tab, bf16* out, int ldo, int N,
+                          hipStream_t st, const int* ntiles_dev, const uint8_t* const* w_tab2,
+                          const uint8_t* const* s_tab2, bf16* out2, const MxGlu& glu) {
+  MxGemvArgs a = gemm_args(xa, nullptr, nullptr, K, tiles, w_tab, s_tab, out, ldo, N, ntiles_dev, w_tab2, s_tab2, out2,
+                           glu);
+  a.x_rows = x_rows;
+  if (x_rows && (pipe_disabled() || K % GB_KS || N % 128 || (!(glu.hh || glu.hq) && N % 256)))
+    throw std::runtime_error("mx_grouped_gemm_rows: x_rows needs the pipelined kernel (K % 64, N % 128; N % 256 "
+                             "without the SwiGLU epilogue)");
+  launch_mx_gemm(a, ntiles, 1, st);
 }
 
 void mx_grouped_gemm_glu(const bf16* xa, int K, const Exl3Tile* tiles, int ntiles, const uint8_t* const* w1_tab,
