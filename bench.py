@@ -2,7 +2,7 @@
 """Benchmark of the MXFP4 routed-expert FFN on one MI355X (gfx950).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
-    python bench.py --only {decode,single,verify,prefill,fp8,grouped,producers,pack,remote,copy}   # one workload (for profilers), one JSON line
+    python bench.py --only {decode,single,verify,prefill,fp8,grouped,producers,dropin,pack,remote,copy}   # one workload (for profilers), one JSON line
 
 A step is one routed-expert FFN over one batch of synthetic tokens: softmax top-6 routing of [T, 256] logits,
 dispatch, fp8 input transform, w1/w3 grouped GEMV with the SwiGLU epilogue, w2 grouped GEMV, combine to bf16
@@ -70,14 +70,26 @@ class Weights:
         self.table = pointer_table([p for row in tab for p in row])
 
 
-def routing_sets(rng, T, R, bias_scale=0.0):
+def routing_sets(rng, T, R, bias_scale=0.0, disjoint=False):
+    """R (x, logits) sets for rotating steps. disjoint: consecutive sets (the last and the first included) route to
+    disjoint experts -- the logits of the experts the neighbouring sets pick are lowered below every other logit
+    -- so no step's weights can come from a cache the step before it filled (the 256 MB Infinity Cache holds part
+    of a ~595 MB decode step)."""
     sets = []
     bias = rng.standard_normal(E).astype(np.float32) * np.float32(bias_scale) if bias_scale else None
-    for _ in range(R):
+    picked = []
+    for i in range(R):
         x = to_bf16(rng.standard_normal((T, D), dtype=np.float32))
         logits = rng.standard_normal((T, E), dtype=np.float32)
         if bias is not None:
             logits = logits + bias
+        if disjoint:
+            avoid = set(picked[-1]) if picked else set()
+            if i == R - 1 and picked:
+                avoid |= set(picked[0])
+            if avoid:
+                logits[:, sorted(avoid)] -= np.float32(1000.0)
+            picked.append(set(distinct_experts(logits)[1].ravel().tolist()))
         sets.append((x, logits))
     return sets
 
@@ -150,13 +162,83 @@ def time_graph(fn, steps, warmup, per_graph=32):
 
 def bench_moe(w, T, steps, warmup, rng, R=8, bias=0.0, stage=False):
     from unholy_amd.device import synchronize
-    sets = routing_sets(rng, T, R, bias)
+    sets = routing_sets(rng, T, R, bias, disjoint=T <= 8)
     r = MoeRunner(w, sets)
     ms = time_steps(lambda i: r.step(i), steps, warmup, (lambda i: r.step(i, True)) if stage else None)
     synchronize()
     stage_ms = [(r.ev[i][0].elapsed_ms(r.ev[i][1]), r.U[i % R]) for i in range(steps)] if stage else []
     u_mean = float(np.mean([r.U[i % R] for i in range(steps)]))
     return dict(ms=ms / steps, U=u_mean, stage=stage_ms, runner=r)
+
+
+class DropinRunner:
+    """The reference's own call sequence for the native MXFP4 experts (src/model/forward_ref.hip:455-470) through the
+    drop-in entry points: routing (uh_route_softmax), dispatch (uh_moe_dispatch_small for T <= 32, else count / plan /
+    scatter), mx_xform_in (the pair rows gathered and fake-quantized to bf16), the w1 / w3 launch with the SwiGLU
+    epilogue writing hh (mx_grouped_gemv with MxGlu, or mx_grouped_gemm_glu for T > 64), the w2 launch on hh
+    (mx_grouped_gemv / mx_grouped_gemm), then moe_combine."""
+
+    def __init__(self, w, sets):
+        from unholy_amd import call
+        from unholy_amd.device import DeviceBuffer, pointer_table
+        self.call, self.w = call, w
+        T = self.T = sets[0][0].shape[0]
+        P = self.P = T * TOPK
+        self.gemv = T <= 64
+        self.tile_rows = 16 if self.gemv else 128
+        self.max_tiles = min(P, E + P // self.tile_rows + 1)
+        self.dev = [(DeviceBuffer.from_array(x), DeviceBuffer.from_array(l)) for x, l in sets]
+        self.U = [distinct_experts(l)[0] for _, l in sets]
+        B = DeviceBuffer
+        self.sel, self.wt = B(P * 4), B(P * 4)
+        self.plan, self.tiles = B(20), B(self.max_tiles * 12)
+        self.eidx, self.ewt, self.row_expert, self.pidx = B(P * 4), B(P * 4), B(P * 4), B(P * 4)
+        self.count, self.off, self.fill = B(E * 4), B(E * 4), B(E * 4)
+        self.xa, self.hh, self.pair = B(P * D * 2), B(P * I * 2), B(P * D * 2)
+        self.out = B(T * D * 2)
+        t = w.ptrs
+        self.tab = [pointer_table(t[i]) for i in range(6)]
+
+    def step(self, i, stream=None):
+        c, T, P, st = self.call, self.T, self.P, (stream.handle if stream is not None else None)
+        x, l = self.dev[i % len(self.dev)]
+        w1, s1, w3, s3, w2, s2 = self.tab
+        ntd = self.plan.ptr + 8  # MoePlan::n_local_tiles
+        c("uh_route_softmax", l, self.sel, self.wt, T, E, TOPK, st)
+        if T <= 32:
+            c("uh_moe_dispatch_small", self.sel, self.wt, T, TOPK, E, P, self.max_tiles, self.tile_rows, self.plan,
+              self.tiles, self.eidx, self.ewt, self.row_expert, self.pidx, None, None, None, 0.0, None, None, None,
+              None, None, 0, st)
+        else:
+            self.count.zero(st)
+            c("uh_moe_count", self.sel, T, TOPK, self.count, E, st, None)
+            c("uh_moe_plan", self.count, None, E, P, self.plan, self.tiles, None, self.off, self.fill, self.max_tiles,
+              st, self.tile_rows)
+            c("uh_moe_scatter", self.sel, self.wt, T, TOPK, self.off, self.fill, self.eidx, self.ewt, self.row_expert,
+              self.pidx, st)
+        c("uh_mx_xform_in", x, D, self.row_expert, s1, self.xa, P, D, st, self.eidx)
+        rows = min(T, self.tile_rows)
+        if self.gemv:
+            c("uh_mx_grouped_gemv", self.xa, D, self.tiles, self.max_tiles, w1, s1, None, I, I, st, ntd, w3, s3, None,
+              rows, self.ewt, self.row_expert, s2, self.hh, LIMIT, None)
+            c("uh_mx_grouped_gemv", self.hh, I, self.tiles, self.max_tiles, w2, s2, self.pair, D, D, st, ntd, None,
+              None, None, rows, None, None, None, None, 0.0, None)
+        else:
+            c("uh_mx_grouped_gemm_glu", self.xa, D, self.tiles, self.max_tiles, w1, s1, w3, s3, I, self.ewt,
+              self.row_expert, s2, self.hh, LIMIT, st, ntd)
+            c("uh_mx_grouped_gemm", self.hh, I, self.tiles, self.max_tiles, w2, s2, self.pair, D, D, st, ntd, None,
+              None, None, rows)
+        c("uh_moe_combine", self.pair, self.pidx, None, self.out, T, TOPK, D, st)
+
+
+def bench_dropin(w, T, steps, warmup, rng, R=8):
+    """ms per step of the reference's call sequence (DropinRunner); T <= 32 as HIP-graph replays (the GPU's time, not
+    the host's launch rate of seven ctypes calls), larger T eagerly (memsets are not captured)."""
+    sets = routing_sets(rng, T, R, disjoint=T <= 8)
+    r = DropinRunner(w, sets)
+    if T <= 32:
+        return dict(ms=time_graph(lambda i, st: r.step(i, st), steps, warmup, per_graph=R), U=float(np.mean(r.U)))
+    return dict(ms=time_steps(lambda i: r.step(i), steps, warmup) / steps, U=float(np.mean(r.U)))
 
 
 def bench_single_gemv(w, steps, warmup, rng):
@@ -352,14 +434,27 @@ def grouped_entry(M, ms):
 
 
 def cpu_model():
+    """The host CPU as /proc/cpuinfo names it: model name, family / model / stepping, logical CPUs, the clock the
+    kernel reports, and this process's CPU affinity."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                k, _, v = line.partition(":")
+                k = k.strip()
+                if k in ("model name", "cpu family", "model", "stepping", "cpu MHz") and k not in info:
+                    info[k] = v.strip()
+                if k == "processor":
+                    info["logical"] = info.get("logical", 0) + 1
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        aff = os.cpu_count() or 1
+    return (f"{info.get('model name', 'unknown')} (family {info.get('cpu family', '?')}, model "
+            f"{info.get('model', '?')}, stepping {info.get('stepping', '?')}; {info.get('logical', '?')} logical CPUs, "
+            f"{aff} in this process's affinity; {info.get('cpu MHz', '?')} MHz reported)")
 
 
 def cpu_threads():
@@ -499,6 +594,10 @@ def run_only(name, args, rng):
     if name == "decode":
         d = bench_moe(w, 8, args.steps, args.warmup, rng)
         return {"moe_decode_T8_ms": d["ms"], "distinct_experts": d["U"]}
+    if name == "dropin":
+        d8 = bench_dropin(w, 8, args.steps, args.warmup, rng)
+        d4 = bench_dropin(w, 4096, 5, 1, rng)
+        return {"dropin_T8_ms": d8["ms"], "dropin_T4096_ms": d4["ms"]}
     if name == "verify":
         d = bench_moe(w, 64, 50, 5, rng, bias=0.5)
         return {"moe_verify_T64_ms": d["ms"], "distinct_experts": d["U"]}
@@ -513,7 +612,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "single", "verify", "prefill", "fp8", "grouped", "producers",
+    ap.add_argument("--only", choices=["decode", "single", "verify", "prefill", "fp8", "grouped", "producers", "dropin",
                                        "pack", "remote", "copy"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -590,6 +689,13 @@ def main():
                 "mfma": "v_mfma_scale_f32_16x16x128_f8f6f4 (e4m3 x e2m1, e8m0 block scales); sums below fp32 "
                         "precision, outside the per-element tolerance",
                 "frac_fp8_mfma_peak": flops / (ps["ms"] * 1e-3) / 1e12 / FP8_PEAK_TFLOPS}}
+        for T, stp, wu in ((8, 200, 16), (4096, 5, 1)):
+            dr = bench_dropin(w, T, stp, wu, rng)
+            wl[f"dropin_sequence_T{T}"] = {
+                "ms": dr["ms"], "tokens_per_s": T / (dr["ms"] * 1e-3), "distinct_experts": dr["U"],
+                "sequence": "route_softmax, dispatch, mx_xform_in, " + (
+                    "mx_grouped_gemv (MxGlu hh), mx_grouped_gemv" if T <= 64 else
+                    "mx_grouped_gemm_glu, mx_grouped_gemm") + ", moe_combine (forward_ref.hip:455-470)"}
         for M, copies in ((1, 64), (64, 64), (4096, 4)):
             t = bench_fp8_dense(M, 100 if M < 4096 else 10, 10 if M < 4096 else 2, rng, copies)
             wl[f"fp8_dense_M{M} (configs[4])"] = {"ms": t, "tokens_per_s": M / (t * 1e-3),
