@@ -53,3 +53,15 @@ def test_shape_errors_are_reported(call):
     rc = f(*args)
     assert rc == -1
     assert msg in _lib.last_error()
+
+
+def test_cpp_dropin_caller_compiles_and_links(tmp_path):
+    """A C++ caller compiles against include/unholy/kernels/*.hpp and links every drop-in symbol it uses from
+    libunholy_amd.so (tests/cpp/build.sh into a temporary path; running it needs a GPU: tests/test_gpu_dropin.py)."""
+    import subprocess
+    root = pathlib.Path(__file__).resolve().parent.parent
+    out = tmp_path / "dropin_link"
+    r = subprocess.run([str(root / "tests" / "cpp" / "build.sh"), str(out)], capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert out.exists()
