@@ -88,10 +88,12 @@ void write_pack(const char* path, const Geometry& g, const uint8_t* const* parts
                 uint64_t source_hash);
 
 // The loader: slots [first, first + count) of an open pack into device memory at dst (slot i at dst + i * stride,
-// stride >= slot_bytes, 256-byte aligned). Eight reader threads, each with two pinned staging buffers taken from a
-// process-wide pool (kept and reused by later calls), read whole slots (or, unverified with fewer slots than threads,
-// 4 KiB-aligned chunks of them), so file reads, checksums and host-to-device copies overlap; with verify, each slot's xxh64 against the checksum table (throws on a mismatch or an absent
-// slot; the first error of any thread is the one thrown). Synchronous on `stream` at return.
+// stride >= slot_bytes, 256-byte aligned). Eight reader threads, each with two pinned staging buffers of one slot
+// taken from a process-wide pool (kept for later calls; at most 16 buffers of the largest slot size loaded), read
+// whole slots (or, unverified with fewer slots than threads, 4 KiB-aligned chunks of them), so file reads, checksums
+// and host-to-device copies overlap. The checksum table's present flags are always read: an absent slot throws,
+// verified or not. With verify, each slot's xxh64 is checked against the table (throws on a mismatch; the first error
+// of any thread is the one thrown). Synchronous on `stream` at return.
 void load_slots(int fd, const Header& h, size_t first, size_t count, void* dst, size_t stride, bool verify,
                 void* stream);
 

@@ -17,11 +17,11 @@ pytestmark = pytest.mark.gpu
 D, I = K13, G13  # w1 / w3 [I, D] = [256, 512], w2 [D, I] = [512, 256]
 
 
-def _load(path, first, count, verify=1, direct=0):
+def _load(path, first, count, verify=1, direct=0, pad=0):
     hb = (ctypes.c_uint8 * 264)()
     call("uh_pack_read_header", str(path).encode(), hb)
     h = parse_header(hb)
-    stride = h["slot_bytes"]
+    stride = h["slot_bytes"] + pad
     buf = DeviceBuffer(count * stride)
     call("uh_pack_load", str(path).encode(), first, count, buf.ptr, stride, verify, direct, None)
     return hb, h, buf, stride
@@ -81,14 +81,17 @@ def test_pack_verify_refuses_damage_and_absence(tmp_path):
     path.write_bytes(bytes(raw))
     with pytest.raises(UhError, match="checksum"):
         _load(path, 3, 1)
+    with pytest.raises(UhError, match="absent"):  # unverified loads refuse an absent slot too
+        _load(path, 1, 2, verify=0)
     _, _, buf, _ = _load(path, 3, 1, verify=0)  # unverified: the damaged bytes as they are
     got = buf.download((h["slot_bytes"],), np.uint8).tobytes()
     assert got == bytes(raw[h["slots_offset"] + 3 * h["slot_bytes"]:h["slots_offset"] + 4 * h["slot_bytes"]])
 
 
 def test_pack_load_o_direct(tmp_path):
-    """O_DIRECT reads (4 KiB-aligned slots straight into the pinned staging), in a directory of the repository's tree
-    when its file system takes O_DIRECT (the temporary directory is often tmpfs, which does not), else tmp_path."""
+    """O_DIRECT reads (4 KiB-aligned slots read into an aligned bounce buffer, then copied into the pinned staging:
+    pread into pinned memory fails with EFAULT under O_DIRECT), in a directory of the repository's tree when its file
+    system takes O_DIRECT (the temporary directory is often tmpfs, which does not), else tmp_path."""
     import pathlib
     import shutil
     import tempfile
@@ -112,3 +115,43 @@ def test_pack_load_o_direct(tmp_path):
         pytest.skip("O_DIRECT not available on these file systems")
     finally:
         shutil.rmtree(dirs[0], ignore_errors=True)
+
+
+def _odirect_dir():
+    """A directory of the repository's tree (its file system may take O_DIRECT; the temporary directory is often
+    tmpfs, which does not)."""
+    import pathlib
+    import tempfile
+    return pathlib.Path(tempfile.mkdtemp(prefix="odirect_", dir=pathlib.Path(__file__).resolve().parent))
+
+
+@pytest.mark.parametrize("count", [2, 3, 5, 7])
+@pytest.mark.parametrize("direct", [0, 1])
+def test_pack_load_unverified_chunks(tmp_path, count, direct):
+    """Unverified loads of fewer slots than reader threads read each slot as several 4 KiB-aligned chunks: every slot's
+    bytes in device memory equal the file's, with a destination stride larger than the slot (slot_bytes + 4096) and
+    with O_DIRECT (where the file system takes it)."""
+    import shutil
+    rng = np.random.default_rng(50 + count)
+    n = 8
+    experts = _experts(rng, n)
+    dr = _odirect_dir() if direct else tmp_path
+    try:
+        path = dr / "c.pack"
+        write_pack(path, 1, 0, n, experts)
+        first = n - count
+        try:
+            _, h, buf, stride = _load(path, first, count, verify=0, direct=direct, pad=4096)
+        except UhError as err:
+            if direct:
+                pytest.skip(f"O_DIRECT not available here: {err}")
+            raise
+        raw = path.read_bytes()
+        sb = h["slot_bytes"]
+        got = buf.download((count * stride,), np.uint8).tobytes()
+        for i in range(count):
+            want = raw[h["slots_offset"] + (first + i) * sb:h["slots_offset"] + (first + i + 1) * sb]
+            assert got[i * stride:i * stride + sb] == want, (count, direct, i)
+    finally:
+        if direct:
+            shutil.rmtree(dr, ignore_errors=True)

@@ -34,10 +34,14 @@ constexpr size_t kLoadThreads = 8;  // reader threads of load_slots
 
 // Pinned staging buffers of load_slots, kept for the life of the process and reused by later calls (allocating pinned
 // memory costs milliseconds per buffer, more than loading a few slots). Portable, so any device can copy from them.
-// A buffer is taken by one reader thread at a time and returned only after its last copy has completed.
+// A buffer is taken by one reader thread at a time and returned only after its last copy has completed. Callers
+// request whole-slot buffers (slot bytes + alignment) even for chunked reads, and a request that no free buffer can
+// serve first frees the free buffers that are too small: the pool holds at most 2 buffers per reader thread (16) of
+// the largest slot size loaded so far, plus any taken at that moment.
 class StagingPool {
  public:
   void* take(size_t bytes) {
+    std::vector<void*> drop;
     {
       const std::lock_guard<std::mutex> lock(mu_);
       for (size_t i = 0; i < free_.size(); ++i)
@@ -46,7 +50,13 @@ class StagingPool {
           free_.erase(free_.begin() + std::ptrdiff_t(i));
           return p;
         }
+      for (const auto& f : free_) {  // every free buffer is smaller than the request
+        drop.push_back(f.first);
+        size_.erase(f.first);
+      }
+      free_.clear();
     }
+    for (void* d : drop) UH_CHECK(hipHostFree(d));
     void* p = nullptr;
     UH_CHECK(hipHostMalloc(&p, bytes, hipHostMallocPortable));
     const std::lock_guard<std::mutex> lock(mu_);
@@ -303,8 +313,10 @@ void load_slots(int fd, const Header& h, size_t first, size_t count, void* dst, 
   if (!dst || stride < h.slot_bytes || stride % 256) throw std::runtime_error("expert pack: destination stride");
   if (count == 0) return;
   const hipStream_t st = static_cast<hipStream_t>(stream);
+  // The checksum table is read for every load (n_slots entries, a few KiB): its present flags refuse an absent slot
+  // whether or not the slots are verified (an absent slot's bytes are zeros, not an expert).
   std::vector<ChecksumEntry> table;
-  if (verify) {
+  {
     const size_t tb = h.n_slots * sizeof(ChecksumEntry);
     uint8_t* buf = alloc_aligned(aligned_buffer_bytes(tb));
     table.resize(h.n_slots);
@@ -316,6 +328,9 @@ void load_slots(int fd, const Header& h, size_t first, size_t count, void* dst, 
     }
     free_aligned(buf);
   }
+  for (size_t i = 0; i < count; ++i)
+    if (!table[first + i].present)
+      throw std::runtime_error("expert pack: slot " + std::to_string(first + i) + " is absent");
   // Reader threads, as the reference's stream test issues whole-slot reads from several threads: each thread claims
   // slots from a shared counter and owns two pinned staging buffers (4 KiB aligned for O_DIRECT; slots start on
   // 4 KiB boundaries and are whole 4 KiB multiples, so each read is exactly its slot). A thread's file read and
@@ -344,7 +359,7 @@ void load_slots(int fd, const Header& h, size_t first, size_t count, void* dst, 
       if (direct) bounce = alloc_aligned(aligned_buffer_bytes(cb));
       UH_CHECK(hipSetDevice(device));
       for (int b = 0; b < 2; ++b) {
-        stage[b] = staging_pool().take(cb + kAlign);
+        stage[b] = staging_pool().take(h.slot_bytes + kAlign);  // whole-slot size: chunked reads reuse them
         UH_CHECK(hipEventCreateWithFlags(&done[b], hipEventDisableTiming));
       }
       for (int n = 0; !failed.load(std::memory_order_relaxed); ++n) {
@@ -362,7 +377,6 @@ void load_slots(int fd, const Header& h, size_t first, size_t count, void* dst, 
           read_aligned(fd, off, len, a);
         if (verify) {  // nch == 1: the whole slot
           const ChecksumEntry& e = table[first + i];
-          if (!e.present) throw std::runtime_error("expert pack: slot " + std::to_string(first + i) + " is absent");
           if (xxh64(a, h.slot_bytes) != e.hash)
             throw std::runtime_error("expert pack: slot " + std::to_string(first + i) + " checksum mismatch");
         }
