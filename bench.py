@@ -146,6 +146,9 @@ def time_graph(fn, steps, warmup, per_graph=32):
     graphs) after `warmup` steps' worth of replays; events on the capture stream."""
     from unholy_amd.device import Event, Graph, Stream
     st = Stream()
+    for i in range(per_graph):  # one eager pass first: an entry point may allocate its workspace (not under capture)
+        fn(i, st)
+    st.synchronize()
     g = Graph(st, lambda: [fn(i, st) for i in range(per_graph)])
     reps = max(1, -(-steps // per_graph))
     for _ in range(max(1, -(-warmup // per_graph))):
