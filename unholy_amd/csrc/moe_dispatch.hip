@@ -163,74 +163,91 @@ __global__ __launch_bounds__(SC_NT) void moe_scatter_kernel(const int32_t* __res
 }
 
 // ---- routers: a wave per token ---------------------------------------------------------------------------------------
-// Top-K of key[] (E <= 64 * NV) with ties to the lower index, in selection order, into chosen[] (every lane): per
-// round the largest key (a DPP max of the order-preserving bits), then the lowest expert holding it (a DPP min).
-template <int NV>
-__device__ __forceinline__ void wave_topk(float key[NV], int E, int K, int* chosen) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int k = 0; k < kMaxK; ++k) {  // unrolled: chosen[] stays in registers (a runtime index would put it in scratch)
-    if (k >= K) break;
-    float bv = -INFINITY;
-    uint32_t bi = 0xffffffffu;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int e = lane + 64 * i;
-      if (e < E && (key[i] > bv || bi == 0xffffffffu)) bv = key[i], bi = uint32_t(e);
-    }
-    const uint32_t ob = bi == 0xffffffffu ? 0u : orderable(bv);
-    const uint32_t m = wave_reduce_u32<true>(ob);
-    const uint32_t idx = wave_reduce_u32<false>(ob == m ? bi : 0xffffffffu);
-    chosen[k] = int(idx);
-#pragma unroll
-    for (int i = 0; i < NV; ++i)
-      if (uint32_t(lane + 64 * i) == idx) key[i] = -INFINITY;
-  }
-}
-
 __device__ __forceinline__ float ds_score(float x) { return sqrtf(x > 20.0f ? x : log1pf(expf(x))); }
 __device__ __forceinline__ float sigmoid(float x) {
 #pragma clang fp contract(off)
   return 1.0f / (1.0f + uh::exp_f32(-x));
 }
+__device__ __forceinline__ float lane_f32(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
 
-// Lane 0's part of a router: GLM reports its picks in ascending id; weights in selection (or id) order:
-// mode 0 score / sum * scale, 1 sigmoid / (sum + 1e-20) * scale, 2 exp(l - l_first) / sum. Loops are unrolled
-// over kMaxK so that the picks stay in registers.
-__device__ __forceinline__ void route_weights(int mode, const float* lr, int* chosen, int K, float route_scale,
-                                              int32_t* sel_t, float* wt_t, int* ssel, float* swt) {
+// One token's routing by one wave (MODE 0: DSV4 sqrt-softplus + bias or the hash row, 1: GLM sigmoid + bias, 2:
+// softmax top-K; E <= 64 * NV). Lane l holds the keys of experts l + 64 i. Top-K with ties to the lower index, in
+// selection order: per round the largest key (a DPP max of the order-preserving bits), then the lowest expert holding
+// it (a DPP min); the pick's logit comes from the lane that holds it (readlane, no memory access). The picks are kept
+// spread over lanes (lane k holds pick k) and every loop over them is a rolled loop over K: this code runs once per
+// launch from a cold instruction cache, so its size sets its time more than its instruction count does.
+// Weights (lane 0's order of operations in the reference's routers): GLM reports its picks in ascending id, the
+// weights follow that order; mode 0 score / sum * scale, 1 sigmoid / (sum + 1e-20) * scale, 2 exp(l - l_first) / sum,
+// the sum taken pick by pick from zero. Lanes k < K write pick k to sel_t / wt_t (and ssel / swt when set).
+template <int MODE, int NV>
+__device__ __forceinline__ void route_wave(const float* lr, const float* bias, const int32_t* hash_row, int E, int K,
+                                           float route_scale, int32_t* sel_t, float* wt_t, int* ssel, float* swt) {
 #pragma clang fp contract(off)
-  if (mode == 1) {
-#pragma unroll
-    for (int x = 1; x < kMaxK; ++x)
-#pragma unroll
-      for (int y = x; y > 0; --y)
-        if (x < K && chosen[y - 1] > chosen[y]) {
-          const int c = chosen[y];
-          chosen[y] = chosen[y - 1];
-          chosen[y - 1] = c;
-        }
-  }
-  float w[kMaxK], sum = 0.0f;
-  const float l0 = lr[chosen[0]];
-#pragma unroll
-  for (int k = 0; k < kMaxK; ++k)
-    if (k < K) {
-      const float l = lr[chosen[k]];
-      w[k] = mode == 2 ? uh::exp_f32(l - l0) : mode == 1 ? sigmoid(l) : ds_score(l);
-      sum += w[k];
+  const int lane = threadIdx.x & 63;
+  int pick = 0;
+  float lgt = 0.0f;
+  if (MODE == 0 && hash_row) {
+    if (lane < K) {
+      pick = hash_row[lane];
+      lgt = lr[pick];
     }
+  } else {
+    float key[NV], raw[NV];
 #pragma unroll
-  for (int k = 0; k < kMaxK; ++k)
-    if (k < K) {
-      const float wk = mode == 2 ? w[k] / sum : mode == 1 ? w[k] / (sum + 1e-20f) * route_scale : (w[k] / sum) * route_scale;
-      sel_t[k] = chosen[k];
-      wt_t[k] = wk;
-      if (ssel) {
-        ssel[k] = chosen[k];
-        swt[k] = wk;
+    for (int i = 0; i < NV; ++i) {
+      const int e = lane + 64 * i;
+      raw[i] = e < E ? lr[e] : 0.0f;
+      float v = -INFINITY;
+      if (e < E) {
+        if constexpr (MODE == 2) v = raw[i];
+        else if constexpr (MODE == 1) v = sigmoid(raw[i]) + bias[e];
+        else v = ds_score(raw[i]) + bias[e];
       }
+      key[i] = v;
     }
+    for (int k = 0; k < K; ++k) {
+      float bv = -INFINITY;
+      uint32_t bi = 0xffffffffu;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int e = lane + 64 * i;
+        if (e < E && (key[i] > bv || bi == 0xffffffffu)) bv = key[i], bi = uint32_t(e);
+      }
+      const uint32_t ob = bi == 0xffffffffu ? 0u : orderable(bv);
+      const uint32_t m = wave_reduce_u32<true>(ob);
+      const uint32_t idx = wave_reduce_u32<false>(ob == m ? bi : 0xffffffffu);
+      float v = 0.0f;
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        if (int(idx >> 6) == i) v = raw[i];
+      const float l = lane_f32(v, int(idx & 63));
+      if (lane == k) pick = int(idx), lgt = l;
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        if (uint32_t(lane + 64 * i) == idx) key[i] = -INFINITY;
+    }
+  }
+  if constexpr (MODE == 1) {  // ascending id: lane k's pick moves to lane (number of smaller picks)
+    int r = lane;
+    if (lane < K) {
+      r = 0;
+      for (int q = 0; q < K; ++q) r += __builtin_amdgcn_readlane(pick, q) < pick;
+    }
+    pick = __builtin_amdgcn_ds_permute(r * 4, pick);
+    lgt = __int_as_float(__builtin_amdgcn_ds_permute(r * 4, __float_as_int(lgt)));
+  }
+  const float w = MODE == 2 ? uh::exp_f32(lgt - lane_f32(lgt, 0)) : MODE == 1 ? sigmoid(lgt) : ds_score(lgt);
+  float sum = 0.0f;
+  for (int k = 0; k < K; ++k) sum += lane_f32(w, k);
+  if (lane < K) {
+    const float wk = MODE == 2 ? w / sum : MODE == 1 ? w / (sum + 1e-20f) * route_scale : (w / sum) * route_scale;
+    sel_t[lane] = pick;
+    wt_t[lane] = wk;
+    if (ssel) {
+      ssel[lane] = pick;
+      swt[lane] = wk;
+    }
+  }
 }
 
 // mode 0: DSV4 (sqrt-softplus + bias, hash tid2eid, bias_vl for image ids), 1: GLM sigmoid, 2: softmax top-K.
@@ -239,35 +256,13 @@ __global__ __launch_bounds__(256) void route_wave_kernel(const float* __restrict
                                                          const int32_t* tid2eid0, const int32_t* ids, int32_t* sel,
                                                          float* weights, int T, int E, int K, float route_scale,
                                                          const float* bias_vl, int vocab) {
-  constexpr int NV = 16;  // E <= 1024
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  const float* lr = logits + size_t(t) * E;
   const bool image = MODE == 0 && bias_vl && ids[t] >= vocab;
   const float* bias = image ? bias_vl : bias0;
-  const int32_t* tid2eid = MODE == 0 && !image ? tid2eid0 : nullptr;
-  int chosen[kMaxK];
-  if (tid2eid) {
-#pragma unroll
-    for (int k = 0; k < kMaxK; ++k)
-      if (k < K) chosen[k] = tid2eid[size_t(ids[t]) * K + k];
-  } else {
-    float key[NV];
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int e = lane + 64 * i;
-      float v = -INFINITY;
-      if (e < E) {
-        if constexpr (MODE == 0) v = ds_score(lr[e]) + bias[e];
-        else if constexpr (MODE == 1) v = sigmoid(lr[e]) + bias[e];
-        else v = lr[e];
-      }
-      key[i] = v;
-    }
-    wave_topk<NV>(key, E, K, chosen);
-  }
-  if (lane != 0) return;
-  route_weights(MODE, lr, chosen, K, route_scale, sel + size_t(t) * K, weights + size_t(t) * K, nullptr, nullptr);
+  const int32_t* hash_row = MODE == 0 && !image && tid2eid0 ? tid2eid0 + size_t(ids[t]) * K : nullptr;
+  route_wave<MODE, 16>(logits + size_t(t) * E, bias, hash_row, E, K, route_scale, sel + size_t(t) * K,
+                       weights + size_t(t) * K, nullptr, nullptr);
 }
 
 // The reference's one-thread-per-token DSV4 router (ref_moe.hip:14-60): the same picks and weights as the wave
@@ -312,34 +307,12 @@ __global__ void route_thread_kernel(const float* logits, const float* bias0, con
 // One token's routing by one wave inside moe_dispatch_small (MODE 0 DSV4, 1 GLM, 2 softmax; E <= 64 * NV).
 template <int MODE, int NV>
 __device__ __forceinline__ void route_token(const MoeSmallArgs& a, int t, int* skey, float* swt) {
-  const int lane = threadIdx.x & 63, E = a.E, K = a.K;
-  const float* lr = (MODE == 2 ? a.softmax_logits : MODE == 1 ? a.route_logits : a.ds_logits) + size_t(t) * E;
+  const float* lr = (MODE == 2 ? a.softmax_logits : MODE == 1 ? a.route_logits : a.ds_logits) + size_t(t) * a.E;
   const bool image = MODE == 0 && a.ds_bias_vl && a.ids[t] >= a.vocab;
   const float* bias = MODE == 1 ? a.route_bias : image ? a.ds_bias_vl : a.ds_bias;
-  const int32_t* tid2eid = MODE == 0 && !image ? a.ds_tid2eid : nullptr;
-  int chosen[kMaxK];
-  if (tid2eid) {
-#pragma unroll
-    for (int k = 0; k < kMaxK; ++k)
-      if (k < K) chosen[k] = tid2eid[size_t(a.ids[t]) * K + k];
-  } else {
-    float key[NV];
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int e = lane + 64 * i;
-      float v = -INFINITY;
-      if (e < E) {
-        if constexpr (MODE == 2) v = lr[e];
-        else if constexpr (MODE == 1) v = sigmoid(lr[e]) + bias[e];
-        else v = ds_score(lr[e]) + bias[e];
-      }
-      key[i] = v;
-    }
-    wave_topk<NV>(key, E, K, chosen);
-  }
-  if (lane == 0)
-    route_weights(MODE, lr, chosen, K, a.route_scale, const_cast<int32_t*>(a.sel) + size_t(t) * K,
-                  const_cast<float*>(a.wt) + size_t(t) * K, skey + t * K, swt + t * K);
+  const int32_t* hash_row = MODE == 0 && !image && a.ds_tid2eid ? a.ds_tid2eid + size_t(a.ids[t]) * a.K : nullptr;
+  route_wave<MODE, NV>(lr, bias, hash_row, a.E, a.K, a.route_scale, const_cast<int32_t*>(a.sel) + size_t(t) * a.K,
+                       const_cast<float*>(a.wt) + size_t(t) * a.K, skey + t * a.K, swt + t * a.K);
 }
 
 // ---- single-block dispatch for small steps -------------------------------------------------------------------------
@@ -354,6 +327,11 @@ __global__ __launch_bounds__(SMALL_NT) void moe_dispatch_small_kernel(MoeSmallAr
   __shared__ float swt[SMALL_NT];
   __shared__ int lds[SMALL_NT / 64 + 1];
   const int T = a.T, K = a.K, E = a.E, n = T * K, tid = threadIdx.x, wave = tid >> 6;
+  // The arguments every launch uses, read into scalar registers here: one wait for all of them, instead of a
+  // scalar-cache miss at each first use further down (a kernel-argument line is not cached from the last launch).
+  asm volatile("" ::"s"(a.softmax_logits), "s"(a.route_logits), "s"(a.ds_logits), "s"(a.eidx), "s"(a.ewt),
+               "s"(a.row_expert), "s"(a.pidx), "s"(a.lt), "s"(a.plan), "s"(a.tile_rows), "s"(a.max_tiles),
+               "s"(a.resident), "s"(a.hist), "s"(a.P), "s"(a.sel), "s"(a.wt));
   const bool route = a.route_logits || a.ds_logits || a.softmax_logits;
   if (route) {
     const int mode = a.softmax_logits ? 2 : a.route_logits ? 1 : 0;
@@ -389,22 +367,64 @@ __global__ __launch_bounds__(SMALL_NT) void moe_dispatch_small_kernel(MoeSmallAr
   // Non-resident experts sort after every resident one: key class ek = e + E (resident first, then the others, each
   // in ascending id: the reference's plan order). Rows below remote0 = keys below E * T * K.
   const int ek = (a.resident && live && !a.resident[e]) ? e + E : e;
+  __shared__ int sexp[SMALL_NT], sek[SMALL_NT];  // pick i's expert id and key class
   __syncthreads();
-  if (live) skey[i] = (ek * T + t) * K + j;
+  if (live) {
+    skey[i] = (ek * T + t) * K + j;
+    sexp[i] = e;
+    sek[i] = ek;
+  }
   __syncthreads();
   const int mykey = (ek * T + t) * K + j, lo = ek * T * K, hi = (ek + 1) * T * K, lim = E * T * K;
   int rank = 0, off = 0, cnt = 0, nloc = 0;
-  if (live) {
-    int q = 0;
-    for (; q + 4 <= n; q += 4) {  // the same address in every lane: broadcast reads, four keys at a time
-      const int4 k4 = *reinterpret_cast<const int4*>(&skey[q]);
-      const int kk[4] = {k4.x, k4.y, k4.z, k4.w};
+  if (n <= 64) {
+    // All 8 waves count: wave w compares keys 8w .. 8w + 7 against pick l (lane l) and the partial counts are added
+    // through LDS (an eighth of the serial compares of one wave doing all of them).
+    __shared__ int4 spart[SMALL_NT / 64][64];
+    const int l = tid & 63;
+    int4 c = {0, 0, 0, 0};
+    if (l < n) {
+      const int mk = skey[l], lo_l = sek[l] * T * K, hi_l = lo_l + T * K;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        rank += kk[u] < mykey;
-        off += kk[u] < lo;
-        cnt += kk[u] >= lo && kk[u] < hi;
-        nloc += kk[u] < lim;
+      for (int u = 0; u < 8; ++u) {
+        const int q = wave * 8 + u;
+        if (q < n) {
+          const int kq = skey[q];
+          c.x += kq < mk;
+          c.y += kq < lo_l;
+          c.z += kq >= lo_l && kq < hi_l;
+          c.w += kq < lim;
+        }
+      }
+    }
+    spart[wave][l] = c;
+    __syncthreads();
+    if (live)
+#pragma unroll
+      for (int w = 0; w < SMALL_NT / 64; ++w) {
+        const int4 v = spart[w][tid];
+        rank += v.x;
+        off += v.y;
+        cnt += v.z;
+        nloc += v.w;
+      }
+  } else if (live) {
+    int q = 0;
+    // The same address in every lane: broadcast reads, sixteen keys (four 16-byte reads issued together) at a time.
+    for (; q + 16 <= n; q += 16) {
+      int4 k4[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) k4[v] = *reinterpret_cast<const int4*>(&skey[q + 4 * v]);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int kk[4] = {k4[v].x, k4[v].y, k4[v].z, k4[v].w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          rank += kk[u] < mykey;
+          off += kk[u] < lo;
+          cnt += kk[u] >= lo && kk[u] < hi;
+          nloc += kk[u] < lim;
+        }
       }
     }
     for (; q < n; ++q) {
@@ -417,11 +437,10 @@ __global__ __launch_bounds__(SMALL_NT) void moe_dispatch_small_kernel(MoeSmallAr
   }
   const int remote0 = live ? nloc : 0;  // the same in every live thread; thread 0 is live (n >= 1)
   // Token t's picks ordered before this one by expert id, then selection order (the reference's sorted picks):
-  // the expert id comes back from the key, whose class puts non-resident experts at e + E.
   int below = 0;
   if (live)
     for (int q = 0; q < K; ++q) {
-      const int cq = skey[t * K + q] / (T * K), eq = cq >= E ? cq - E : cq;
+      const int eq = sexp[t * K + q];
       below += eq < e || (eq == e && q < j);
     }
   const int p = rank;
@@ -553,23 +572,28 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const bf16* __restrict
   const int t = blockIdx.y, d = (blockIdx.x * 256 + threadIdx.x) * 8;
   if (d >= dim) return;
   float acc[8] = {};
-  for (int j = 0; j < K; ++j) {
-    const uint4 v = *reinterpret_cast<const uint4*>(pair_out + size_t(pidx[size_t(t) * K + j]) * dim + d);
+  const auto add = [&](const uint4 v) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       acc[2 * q] += __uint_as_float(w[q] << 16);
       acc[2 * q + 1] += __uint_as_float(w[q] & 0xffff0000u);
     }
-  }
+  };
+  // Up to kMaxK picks: every row load is issued before the first add (one memory latency, not one per pick); the
+  // adds stay in pick order.
+  const int kk = min(K, kMaxK);
+  uint4 v[kMaxK];
+#pragma unroll
+  for (int j = 0; j < kMaxK; ++j)
+    if (j < kk) v[j] = *reinterpret_cast<const uint4*>(pair_out + size_t(pidx[size_t(t) * K + j]) * dim + d);
+  const uint4 sv = shared ? *reinterpret_cast<const uint4*>(shared + size_t(t) * dim + d) : uint4{};
+#pragma unroll
+  for (int j = 0; j < kMaxK; ++j)
+    if (j < kk) add(v[j]);
+  for (int j = kMaxK; j < K; ++j) add(*reinterpret_cast<const uint4*>(pair_out + size_t(pidx[size_t(t) * K + j]) * dim + d));
   if (shared) {
-    const uint4 v = *reinterpret_cast<const uint4*>(shared + size_t(t) * dim + d);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      acc[2 * q] += __uint_as_float(w[q] << 16);
-      acc[2 * q + 1] += __uint_as_float(w[q] & 0xffff0000u);
-    }
+    add(sv);
   } else {
 #pragma unroll
     for (int q = 0; q < 8; ++q) acc[q] += 0.0f;
