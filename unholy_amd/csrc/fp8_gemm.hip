@@ -426,6 +426,213 @@ void launch_fp8_gemv_t(const Fp8GemmArgs& a, hipStream_t st, const Fp8Parts& pp)
   UH_CHECK_LAUNCH();
 }
 
+
+// ---- fp8 dense, 16 < M <= 64 with fp32 scales: wide column blocks, K split over workgroups ------------------------
+// The one-tile GEMV above reads all M activation rows once per 16 output columns: at M = 64 that is 4x the weight
+// bytes again from L2 (a load-only kernel of that pattern takes 12 us at 4096 x 4096 against 5 us for the weights
+// alone). Here a workgroup owns 64 columns x one K slice of KR inputs x all M rows:
+// - its activation slice (codes + fp32 row scales) is staged once into LDS, so A is read from L2 once per 64
+//   columns; the codes are held as their bf16 values (exact), converted once per workgroup rather than once per
+//   column tile;
+// - 4 KP waves = 4 column tiles x KP parts of the chunk; each wave's weights (16 columns x KR / KP inputs, 32 bytes
+//   per lane per 128-block) are all loaded before the staging starts;
+// - per 128-block: four bf16 16x16x32 MFMAs per row tile on exactly dequantized operands, the block sum folded as
+//   acc += raw * (sa * sw) (the reference's fp32-scale order);
+// - the KP parts are added in LDS in part order; S slices write fp32 partial tiles to
+//   part[s][M][N], which fp8_split_sum_kernel adds in slice order into bf16 C (S = 1: C directly).
+// Sums differ from the one-tile GEMV only in fp32 association (tolerance parity, not bit parity).
+constexpr int SK_COLS = 64, SK_PAD = 16, SK_MAXS = 16;
+
+struct Fp8SplitArgs {
+  const uint8_t* a;    // e4m3 codes [M, K]
+  const float* sa;     // fp32 row scales [M, K / 128]
+  const uint8_t* w;    // e4m3 [N, K]
+  const float* sw;     // fp32 [ceil(N / 128), K / 128]
+  uint16_t* c;         // bf16 [M, ldc] (S = 1)
+  float* part;         // fp32 [S, M, N] (S > 1)
+  int ldc, M, N, K, S;
+};
+
+template <int KP, int NB>
+__global__ __launch_bounds__(256 * KP) void fp8_split_kernel(Fp8SplitArgs a) {
+  constexpr int NT = 256 * KP, KR = KP * NB * 128, LDA = KR + SK_PAD / 2, KB = KR / 128;
+  extern __shared__ __align__(16) uint8_t smem[];
+  uint16_t* sA = reinterpret_cast<uint16_t*>(smem);            // the codes' values as bf16 [64][LDA]
+  float* sS = reinterpret_cast<float*>(smem + 64 * LDA * 2);  // row scales [64][KB]
+  const int M = a.M, K = a.K, N = a.N, KS = K / 128, slice = blockIdx.y, nch = K / (a.S * KR);
+  const int tid = threadIdx.x, lane = tid & 63, nl = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), ct = wave & 3, kh = wave >> 2;  // column tile, K part
+  const int n0 = blockIdx.x * SK_COLS + ct * 16, n = n0 + nl;
+  const int mlive = (M + 15) / 16;
+  const uint8_t* wrow = a.w + size_t(n) * K + g * 32;
+  v4f acc[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) acc[mt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  // The slice's K range in chunks of KR inputs (one chunk unless the slice is longer than the LDS holds).
+  for (int ch = 0; ch < nch; ++ch) {
+    const int chunk = slice * nch + ch;
+    const int kb0 = chunk * KB + kh * NB;  // this wave's first global 128-block in the chunk
+    // Weights first: every load of the wave's NB blocks in flight before the activation staging.
+    v4i b[NB][2];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      b[u][0] = *reinterpret_cast<gptr<v4i>>(as_global(wrow + (kb0 + u) * 128));
+      b[u][1] = *reinterpret_cast<gptr<v4i>>(as_global(wrow + (kb0 + u) * 128 + 16));
+    }
+    float swv[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) swv[u] = a.sw[size_t(n0 / 128) * KS + kb0 + u];
+    if (ch > 0) __syncthreads();  // every wave is past its reads of the previous chunk
+    // The chunk's activation rows into LDS.
+    const size_t col0 = size_t(chunk) * KR;
+    // Every load of the staging is issued before the first is used (one memory latency, not one per item).
+    constexpr int per_row = KR / 16, IT = 64 * per_row / NT;
+    const int items = M * per_row;
+    uint4 raw[IT];
+#pragma unroll
+    for (int j = 0; j < IT; ++j) {
+      const int it = min(j * NT + tid, items - 1), r = it / per_row, c16 = (it % per_row) * 16;
+      raw[j] = *reinterpret_cast<const uint4*>(a.a + size_t(r) * K + col0 + c16);
+    }
+    const float sv = tid < M * KB ? a.sa[size_t(tid / KB) * KS + chunk * KB + tid % KB] : 0.0f;  // M * KB <= NT
+#pragma unroll
+    for (int j = 0; j < IT; ++j) {
+      const int it = j * NT + tid, r = it / per_row, c16 = (it % per_row) * 16;
+      if (it < items) {
+        *reinterpret_cast<bf16x8*>(sA + r * LDA + c16) = fp8x8_to_bf16(raw[j].x, raw[j].y, 1.0f);
+        *reinterpret_cast<bf16x8*>(sA + r * LDA + c16 + 8) = fp8x8_to_bf16(raw[j].z, raw[j].w, 1.0f);
+      }
+    }
+    if (tid < M * KB) sS[tid] = sv;
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int lb = kh * NB + u;  // block within the chunk
+      bf16x8 bf[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        bf[t] = fp8x8_to_bf16(uint32_t(b[u][t / 2][2 * (t % 2)]), uint32_t(b[u][t / 2][2 * (t % 2) + 1]), 1.0f);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        if (mt >= mlive) break;
+        const int row = mt * 16 + nl;
+        bf16x8 af[4];
+        if (row < M) {
+          const uint16_t* ap = sA + row * LDA + lb * 128 + g * 32;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) af[t] = *reinterpret_cast<const bf16x8*>(ap + 8 * t);
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) af[t] = bf16x8{};
+        }
+        v4f raw = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) raw = mfma_bf16(af[t], bf[t], raw);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int rr = mt * 16 + 4 * g + i;  // C row of value i
+          const float sa = rr < M ? sS[rr * KB + lb] : 0.0f;
+          acc[mt][i] += raw[i] * (sa * swv[u]);
+        }
+      }
+    }
+  }
+  // The K parts added in order (part 0 + part 1 + ...), through LDS (the staged rows are no longer read).
+  __syncthreads();
+  v4f* red = reinterpret_cast<v4f*>(smem);
+  if (kh > 0)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) red[(((kh - 1) * 4 + ct) * 4 + mt) * 64 + lane] = acc[mt];
+  __syncthreads();
+  if (kh > 0) return;
+#pragma unroll
+  for (int q = 1; q < KP; ++q)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) acc[mt] += red[(((q - 1) * 4 + ct) * 4 + mt) * 64 + lane];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    if (mt >= mlive) break;
+    const v4f s = acc[mt];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = mt * 16 + 4 * g + i;
+      if (r >= M) continue;
+      if (a.S == 1) a.c[size_t(r) * a.ldc + n] = f32_to_bf16(s[i]);
+      else a.part[(size_t(slice) * M + r) * N + n] = s[i];
+    }
+  }
+}
+
+// C[m][n] = bf16(sum over slices s in order of part[s][m][n]): a thread per 4 columns.
+__global__ __launch_bounds__(256) void fp8_split_sum_kernel(const float* __restrict__ part, int S, int M, int N,
+                                                            uint16_t* __restrict__ c, int ldc) {
+  const size_t i = (size_t(blockIdx.x) * 256 + threadIdx.x) * 4, total = size_t(M) * N;
+  if (i >= total) return;
+  const int m = int(i / N), n = int(i % N);
+  float4 v[SK_MAXS];  // every slice's load issued before the first add
+#pragma unroll
+  for (int s = 0; s < SK_MAXS; ++s)
+    if (s < S) v[s] = *reinterpret_cast<const float4*>(part + size_t(s) * total + i);
+  float4 acc = v[0];
+#pragma unroll
+  for (int s = 1; s < SK_MAXS; ++s)
+    if (s < S) {
+      acc.x += v[s].x;
+      acc.y += v[s].y;
+      acc.z += v[s].z;
+      acc.w += v[s].w;
+    }
+  const uint32_t lo = uint32_t(f32_to_bf16(acc.x)) | uint32_t(f32_to_bf16(acc.y)) << 16;
+  const uint32_t hi = uint32_t(f32_to_bf16(acc.z)) | uint32_t(f32_to_bf16(acc.w)) << 16;
+  *reinterpret_cast<uint2*>(c + size_t(m) * ldc + n) = make_uint2(lo, hi);
+}
+
+// Slices for a shape (0: the split kernel does not take it): N % 64, K % 256; the fewest slices S (K a multiple of
+// 256 S) that give >= 256 workgroups, else as many as K allows. A slice is staged in chunks of split_chunk inputs.
+int split_slices(int M, int N, int K) {
+  if (M <= 16 || M > 64 || N % SK_COLS || K % 256 || N <= 0) return 0;
+  const int cols = N / SK_COLS;
+  int best = 0;
+  for (int S = 1; S * 256 <= K && S <= SK_MAXS; ++S) {
+    if (K % (256 * S)) continue;
+    best = S;
+    if (cols * S >= 256) break;
+  }
+  return best;
+}
+// Chunk of a slice held in LDS at once: the largest of 1024, 512, 256 inputs that divides the slice.
+int split_chunk(int K, int S) {
+  const int r = K / S;
+  return r % 1024 == 0 ? 1024 : r % 512 == 0 ? 512 : 256;
+}
+
+void launch_split(const Fp8SplitArgs& a0, void* ws, size_t ws_bytes, hipStream_t st) {
+  Fp8SplitArgs a = a0;
+  a.S = split_slices(a.M, a.N, a.K);
+  if (!a.S) throw std::runtime_error("fp8 split: shape");
+  if (a.S > 1) {
+    const size_t need = size_t(a.S) * a.M * a.N * 4;
+    if (!ws || ws_bytes < need) throw std::runtime_error("fp8 split: workspace too small");
+    if (reinterpret_cast<uintptr_t>(ws) % 16) throw std::runtime_error("fp8 split: workspace alignment");
+    a.part = static_cast<float*>(ws);
+  }
+  // 16 waves (4 K parts) when the chunk has 4 or more 128-blocks, else 8 waves (2 parts).
+  const int KR = split_chunk(a.K, a.S), KP = KR >= 512 ? 4 : 2, NB = KR / (128 * KP);
+  const size_t lds = size_t(64) * (KR + SK_PAD / 2) * 2 + size_t(64) * (KR / 128) * 4;
+  const dim3 grid(unsigned(a.N / SK_COLS), unsigned(a.S));
+  const auto go = [&](auto kern, int threads) {
+    UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+    kern<<<grid, threads, lds, st>>>(a);
+  };
+  if (KP == 2) go(&fp8_split_kernel<2, 1>, 512);
+  else if (NB == 1) go(&fp8_split_kernel<4, 1>, 1024);
+  else go(&fp8_split_kernel<4, 2>, 1024);
+  UH_CHECK_LAUNCH();
+  if (a.S > 1) {
+    fp8_split_sum_kernel<<<unsigned(cdiv(size_t(a.M) * a.N / 4, 256)), 256, 0, st>>>(a.part, a.S, a.M, a.N, a.c, a.ldc);
+    UH_CHECK_LAUNCH();
+  }
+}
 }  // namespace
 
 void launch_fp8_skinny(const Fp8GemmArgs& a0, hipStream_t st) {
@@ -568,6 +775,42 @@ void gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const fl
   g.N = N;
   g.K = K;
   launch_fp8_gemm(g, st);
+}
+
+
+size_t gemm_fp8_f32s_ws_size(int M, int N, int K) {
+  const int S = split_slices(M, N, K);
+  return S > 1 ? size_t(S) * M * N * 4 : 0;
+}
+namespace {
+void check_split(const char* name, int M, int N, int K, int ldc, const void* c, const void* w, const float* sw) {
+  if (!split_slices(M, N, K))
+    throw std::runtime_error(std::string(name) + ": 16 < M <= 64, N % 64, K % 256 (gemm_fp8_f32s_ws_size says 0 for "
+                             "other shapes only when they need no workspace)");
+  if (!c || !w || !sw) throw std::runtime_error(std::string(name) + ": null operand");
+  if (ldc < N || ldc % 4 || reinterpret_cast<uintptr_t>(c) % 8) throw std::runtime_error(std::string(name) + ": ldc");
+}
+}  // namespace
+void gemm_fp8_f32s_ws(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw, bf16* c, int ldc, int M,
+                      int N, int K, void* ws, size_t ws_bytes, hipStream_t st) {
+  if (M <= 0) return;
+  if (!split_slices(M, N, K)) {  // the workspace is not needed: the plain entry's kernels
+    gemm_fp8_f32s(a, sa, w, sw, c, ldc, M, N, K, st);
+    return;
+  }
+  check_split("gemm_fp8_f32s_ws", M, N, K, ldc, c, w, sw);
+  if (!a || !sa) throw std::runtime_error("gemm_fp8_f32s_ws: null operand");
+  Fp8SplitArgs g{};
+  g.a = a;
+  g.sa = sa;
+  g.w = w;
+  g.sw = sw;
+  g.c = c;
+  g.ldc = ldc;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  launch_split(g, ws, ws_bytes, st);
 }
 
 namespace {
