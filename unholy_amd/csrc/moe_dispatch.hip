@@ -353,6 +353,56 @@ __global__ __launch_bounds__(SMALL_NT) void moe_dispatch_small_kernel(MoeSmallAr
     }
   }
   __syncthreads();
+  if (n <= 64 && !a.remote && !a.resident && !a.hist) {
+    // The forward's decode case (all picks fit one wave, only the local plan is asked for): wave 0 alone finishes
+    // the dispatch with no further barrier. Lane l stands for pick l (token l / K, selection l % K). The expert's
+    // bits are walked from the top with ballots: `less` collects the picks whose expert is smaller, `peers` ends as
+    // the picks of the same expert. Within an expert the plan orders rows by (token, selection), which is the pick
+    // index order, so pair row p = |less| + (peers below this lane); token t's picks before this one by (expert,
+    // selection) are the same counts restricted to the token's K lanes.
+    if (wave != 0) return;
+    const int l = tid;
+    const bool live = l < n;
+    const int e = live ? skey[l] : 0;
+    const float w = live ? swt[l] : 0.0f;
+    const int t = live ? l / K : 0;
+    uint64_t peers = __ballot(live), less = 0;
+    for (int b = 31 - __builtin_clz(uint32_t(max(E - 1, 1))); b >= 0; --b) {
+      const uint64_t ones = __ballot(live && ((e >> b) & 1));
+      if ((e >> b) & 1) {
+        less |= peers & ~ones;
+        peers &= ones;
+      } else {
+        peers &= ~ones;
+      }
+    }
+    const auto below_me = [](uint64_t m) {
+      return int(__builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u)));
+    };
+    const uint64_t tok = ((K >= 64 ? ~0ull : (1ull << K) - 1)) << (t * K);
+    const int off = __popcll(less), cnt = __popcll(peers), p = off + below_me(peers);
+    const int below = __popcll(less & tok) + below_me(peers & tok);
+    __shared__ int sflag[64], srow_e1[64], sleft[64];  // per pair row
+    if (live) {
+      a.eidx[p] = t;
+      a.ewt[p] = w;
+      a.row_expert[p] = e;
+      a.pidx[size_t(t) * K + below] = p;
+      // rows of the expert's run from here when this row starts a tile (a multiple of tile_rows into the run)
+      sflag[p] = (p - off) % a.tile_rows == 0;
+      srow_e1[p] = e;
+      sleft[p] = cnt - (p - off);
+    }
+    __builtin_amdgcn_wave_barrier();  // one wave: its LDS accesses complete in order
+    // Lane r now stands for pair row r: tiles are numbered in row order (a ballot prefix count).
+    const int r = tid;
+    const bool start = r < n && sflag[r];
+    const uint64_t starts = __ballot(start);
+    const int tile = below_me(starts);
+    if (start && tile < a.max_tiles) a.lt[tile] = Exl3Tile{srow_e1[r], r, min(a.tile_rows, sleft[r])};
+    if (tid == 0) *a.plan = MoePlan{a.P, n, min(int(__popcll(starts)), a.max_tiles), 0, 0};
+    return;
+  }
   const int i = tid;
   const bool live = i < n;
   int e = 0, t = 0, j = 0;
