@@ -149,9 +149,13 @@ constexpr int GV_WAVES = 8, GV_PAD = 16, GV_MAXROWS = 16, GV_PF = 4;
 // W: waves per workgroup (16 outputs each).
 // KSPLIT (small launches, plain outputs): the workgroup is one 16-column tile whose W waves take K / W steps each, so
 // every wave's weight loads are in flight at once; the partial sums are added in LDS in wave order.
-template <int NP, int GM, int AM, int W, bool KSPLIT = false>
+// ABF: the staged rows are held as their bf16 values (the codes times their e8m0 scale, exact) instead of codes +
+// scales, so each step reads its activation operands without converting them; rows past the tile read a zero row.
+// Chosen when (rows_cap + 1) rows of bf16 fit the two-workgroups-per-CU LDS share.
+template <int NP, int GM, int AM, int W, bool KSPLIT = false, bool ABF = false>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void mx_gemv_kernel(MxGemvArgs a) {
   static_assert(!KSPLIT || GM == 0, "the K split has a plain epilogue");
+  static_assert(!(KSPLIT && ABF), "the K split stages codes");
   constexpr int NT = 64 * W;
   extern __shared__ __align__(16) uint8_t smem[];
   if (a.ntiles_dev && int(blockIdx.y) >= *a.ntiles_dev) return;
@@ -176,7 +180,12 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
   const int K = a.K, N = a.N, KS = K / 128, ldA = K + GV_PAD, ntn = N / 16;
   uint8_t* sA = smem;
   uint8_t* sS = smem + size_t(a.rows_cap) * ldA;
+  uint16_t* const sAb = reinterpret_cast<uint16_t*>(smem);  // ABF: [rows_cap + 1][ldAb] bf16, the last row zero
+  const int ldAb = K + 8;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nl = lane & 15, g = lane >> 4;
+  if constexpr (ABF)
+    for (int i = tid * 8; i < ldAb; i += NT * 8)
+      *reinterpret_cast<uint4*>(sAb + size_t(a.rows_cap) * ldAb + i) = uint4{0u, 0u, 0u, 0u};
   const int nt = KSPLIT ? int(blockIdx.x) : int(blockIdx.x) * W + wave;
   const bool active = nt < (a.split ? a.split : ntn);  // uniform per wave
   const int sb = KSPLIT ? wave * (KS / W) : 0, se = KSPLIT ? sb + KS / W : KS;  // this wave's K steps
@@ -252,17 +261,29 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
             se = blk.se;
             fp8_codes8(v, blk, lo, hi);
           }
-          *reinterpret_cast<uint2*>(sA + m * ldA + c) = make_uint2(lo, hi);
-          if ((c & 127) == 0) sS[m * KS + c / 128] = se;
+          if constexpr (ABF) {
+            *reinterpret_cast<bf16x8*>(sAb + m * ldAb + c) = fp8x8_to_bf16(lo, hi, e8m0_to_f32(se));
+          } else {
+            *reinterpret_cast<uint2*>(sA + m * ldA + c) = make_uint2(lo, hi);
+            if ((c & 127) == 0) sS[m * KS + c / 128] = se;
+          }
         }
       }
     } else {
       const int total = M * (K / 16);
       for (int i = tid; i < total; i += NT) {
         const int m = i / (K / 16), c = (i % (K / 16)) * 16;
-        *reinterpret_cast<uint4*>(sA + m * ldA + c) = *reinterpret_cast<const uint4*>(a.aq + (row0 + m) * K + c);
+        const uint4 q = *reinterpret_cast<const uint4*>(a.aq + (row0 + m) * K + c);
+        if constexpr (ABF) {
+          const float sc = e8m0_to_f32(a.as[(row0 + m) * KS + c / 128]);
+          *reinterpret_cast<bf16x8*>(sAb + m * ldAb + c) = fp8x8_to_bf16(q.x, q.y, sc);
+          *reinterpret_cast<bf16x8*>(sAb + m * ldAb + c + 8) = fp8x8_to_bf16(q.z, q.w, sc);
+        } else {
+          *reinterpret_cast<uint4*>(sA + m * ldA + c) = q;
+        }
       }
-      for (int i = tid; i < M * KS; i += NT) sS[i] = a.as[row0 * KS + i];
+      if constexpr (!ABF)
+        for (int i = tid; i < M * KS; i += NT) sS[i] = a.as[row0 * KS + i];
     }
     __syncthreads();
 
@@ -278,9 +299,13 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     // supplies inputs 8g .. 8g + 7 of block t on both sides. The weights arrive as block g of the step in lane group
     // g (16 bytes); a 4 x 4 transpose of dwords across the lane groups (two permlane32 and two permlane16 swaps)
     // hands each group its dword of every block.
+    const uint16_t* apb = sAb + size_t(arow ? nl : a.rows_cap) * ldAb + g * 8;
     const auto step = [&](int s, int i) {
       bf16x8 af[4];
-      if (arow) {
+      if constexpr (ABF) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) af[t] = *reinterpret_cast<const bf16x8*>(apb + s * 128 + 32 * t);
+      } else if (arow) {
         const float sc = e8m0_to_f32(asp[s]);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -560,9 +585,17 @@ void launch_gemv_w(const MxGemvArgs& a, int ntiles, hipStream_t st) {
       return;
     }
   }
+  const dim3 grid(cdiv(ntn, W), unsigned(ntiles), 1);
+  const size_t lds_bf = size_t(a.rows_cap + 1) * (a.K + 8) * 2;
+  if (lds_bf <= 80 * 1024) {  // bf16 rows, two workgroups per CU
+    auto* kern = &mx_gemv_kernel<NP, GM, AM, W, false, true>;
+    set_lds_limit(kern, lds_bf);
+    kern<<<grid, 64 * W, lds_bf, st>>>(a);
+    UH_CHECK_LAUNCH();
+    return;
+  }
   auto* kern = &mx_gemv_kernel<NP, GM, AM, W>;
   set_lds_limit(kern, lds);
-  const dim3 grid(cdiv(ntn, W), unsigned(ntiles), 1);
   kern<<<grid, 64 * W, lds, st>>>(a);
   UH_CHECK_LAUNCH();
 }
