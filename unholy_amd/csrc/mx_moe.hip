@@ -151,7 +151,7 @@ constexpr int GV_WAVES = 8, GV_PAD = 16, GV_MAXROWS = 16, GV_PF = 4;
 // every wave's weight loads are in flight at once; the partial sums are added in LDS in wave order.
 // ABF: the staged rows are held as their bf16 values (the codes times their e8m0 scale, exact) instead of codes +
 // scales, so each step reads its activation operands without converting them; rows past the tile read a zero row.
-// Chosen when (rows_cap + 1) rows of bf16 fit the two-workgroups-per-CU LDS share.
+// Chosen when (rows_cap + 1) rows of bf16 fit the LDS.
 template <int NP, int GM, int AM, int W, bool KSPLIT = false, bool ABF = false>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void mx_gemv_kernel(MxGemvArgs a) {
   static_assert(!KSPLIT || GM == 0, "the K split has a plain epilogue");
@@ -586,8 +586,10 @@ void launch_gemv_w(const MxGemvArgs& a, int ntiles, hipStream_t st) {
     }
   }
   const dim3 grid(cdiv(ntn, W), unsigned(ntiles), 1);
+  // bf16 rows when they fit the LDS next to the epilogue's static share (the kernel's registers already hold it to
+  // one 8-wave workgroup per CU)
   const size_t lds_bf = size_t(a.rows_cap + 1) * (a.K + 8) * 2;
-  if (lds_bf <= 80 * 1024) {  // bf16 rows, two workgroups per CU
+  if (lds_bf <= 156 * 1024) {
     auto* kern = &mx_gemv_kernel<NP, GM, AM, W, false, true>;
     set_lds_limit(kern, lds_bf);
     kern<<<grid, 64 * W, lds_bf, st>>>(a);
