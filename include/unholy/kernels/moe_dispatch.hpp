@@ -88,6 +88,10 @@ struct MoeSmallArgs {
   const float* softmax_logits = nullptr;
 };
 void moe_dispatch_small(const MoeSmallArgs& a, hipStream_t st);
+// No reference counterpart: the same single-block launch for local steps of up to kMoeMidMaxPicks picks (T * K; no
+// remote outputs, no resident mask), e.g. a 64-token verify step at top-6.
+constexpr int kMoeMidMaxPicks = 512;
+void moe_dispatch_mid(const MoeSmallArgs& a, hipStream_t st);
 
 // ---- remote experts (the compact transport of experts held elsewhere) -------------------------------------------------
 // Kernels with device-side extents (the plan); grids sized for max_rows / max_tokens. Each ends with a system-scope

@@ -190,6 +190,14 @@ int uh_moe_dispatch_small(const int32_t* sel, const float* wt, int T, int K, int
                           const float* route_bias, float route_scale, const float* ds_logits, const float* ds_bias,
                           const float* ds_bias_vl, const int32_t* ds_tid2eid, const int32_t* ids, int vocab,
                           void* stream);
+/* No reference counterpart: uh_moe_dispatch_small for local steps of up to 512 picks (T * K, e.g. T = 64 at top-6;
+ * no resident mask or remote outputs), softmax_logits (may be NULL): softmax top-K routing in the launch. */
+int uh_moe_dispatch_mid(const int32_t* sel, const float* wt, int T, int K, int E, int P, int max_tiles, int tile_rows,
+                        int32_t* plan, int32_t* tiles, int32_t* eidx, float* ewt, int32_t* row_expert, int32_t* pidx,
+                        uint32_t* hist, const float* route_logits, const float* route_bias, float route_scale,
+                        const float* ds_logits, const float* ds_bias, const float* ds_bias_vl,
+                        const int32_t* ds_tid2eid, const int32_t* ids, int vocab, const float* softmax_logits,
+                        void* stream);
 /* ref.hpp:251-252 */
 int uh_swiglu(const uint16_t* gate, const uint16_t* up, const float* w, uint16_t* h, int rows, int dim, float limit,
               void* stream);

@@ -76,6 +76,63 @@ def test_dispatch_small(T, E, K, tile_rows):
                     bufs["tiles"].download((max_tiles, 3), np.int32), plan, plan[2])
 
 
+@pytest.mark.parametrize("T,E,K,tile_rows,mode", [(64, 256, 6, 16, "softmax"), (64, 256, 8, 16, "sel"),
+                                                   (40, 1024, 6, 4, "glm"), (50, 256, 6, 16, "ds"),
+                                                   (64, 16, 8, 3, "sel"), (9, 256, 6, 16, "softmax")])
+def test_dispatch_mid(T, E, K, tile_rows, mode):
+    """moe_dispatch_mid (the single-block dispatch for local steps of up to 512 picks; past one wave of picks the
+    rows come from per-expert counts and a scan): the host plan order bit for bit, given picks or routing in the
+    launch (softmax, GLM sigmoid, DSV4 with hash rows for some tokens), and the histogram output."""
+    rng = np.random.default_rng(T * 7 + E + K)
+    P, max_tiles = T * K, T * K + E
+    logits = rng.standard_normal((T, E), dtype=np.float32) * 2
+    bias = rng.standard_normal(E, dtype=np.float32) * 0.3
+    ids = tid2eid = None
+    if mode == "softmax":
+        sel_ref, wt_ref = oracle.route_softmax(logits, K)
+    elif mode == "glm":
+        sel_ref, wt_ref = oracle.route_glm(logits, bias, K, 2.0)
+    elif mode == "ds":
+        vocab = 800  # ids >= vocab: image tokens, routed by score + bias_vl; the others take their hash row
+        ids = rng.integers(0, 1000, T).astype(np.int32)
+        tid2eid = np.stack([rng.permutation(E)[:K] for _ in range(1000)]).astype(np.int32)
+        bias_vl = rng.standard_normal(E, dtype=np.float32) * 0.3
+        sel_ref, wt_ref = oracle.route_ds(logits, bias, K, 2.0, tid2eid=tid2eid, ids=ids, bias_vl=bias_vl, vocab=vocab)
+    else:
+        sel_ref = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+        wt_ref = rng.random((T, K)).astype(np.float32)
+    ref = oracle.dispatch(sel_ref, wt_ref, E, tile_rows)
+    sel, wt = (dev(sel_ref), dev(wt_ref)) if mode == "sel" else (DeviceBuffer(P * 4), DeviceBuffer(P * 4))
+    hist = DeviceBuffer(E * 4)
+    hist.zero()
+    b = dict(plan=DeviceBuffer(20), tiles=DeviceBuffer(max_tiles * 12), eidx=DeviceBuffer(P * 4),
+             ewt=DeviceBuffer(P * 4), row_expert=DeviceBuffer(P * 4), pidx=DeviceBuffer(P * 4))
+    dl, db = dev(logits), dev(bias)
+    call("uh_moe_dispatch_mid", sel, wt, T, K, E, P, max_tiles, tile_rows, b["plan"], b["tiles"], b["eidx"], b["ewt"],
+         b["row_expert"], b["pidx"], hist if mode == "sel" else None, dl if mode == "glm" else None,
+         db if mode == "glm" else None, 2.0, dl if mode == "ds" else None, db if mode == "ds" else None,
+         dev(bias_vl) if mode == "ds" else None, dev(tid2eid) if mode == "ds" else None,
+         dev(ids) if mode == "ds" else None, vocab if mode == "ds" else 0,
+         dl if mode == "softmax" else None, None)
+    assert np.array_equal(sel.download((T, K), np.int32), sel_ref)
+    if mode == "sel":
+        assert np.array_equal(wt.download((T, K), np.float32), wt_ref)
+        assert np.array_equal(hist.download(E, np.int32), np.bincount(sel_ref.ravel(), minlength=E))
+    else:  # the device's weights (its transcendentals may differ from the host's by an ulp) carried exactly
+        wt_dev = wt.download((T, K), np.float32)
+        np.testing.assert_allclose(wt_dev, wt_ref, rtol=1e-5)
+        ref = oracle.dispatch(sel_ref, wt_dev, E, tile_rows)
+    plan = b["plan"].download(5, np.int32)
+    _check_dispatch(ref, b["eidx"].download(P, np.int32), b["ewt"].download(P, np.float32),
+                    b["row_expert"].download(P, np.int32), b["pidx"].download((T, K), np.int32),
+                    b["tiles"].download((max_tiles, 3), np.int32), plan, plan[2])
+    if mode != "sel":
+        return
+    with pytest.raises(Exception, match="512"):
+        call("uh_moe_dispatch_mid", sel, wt, 65, 8, E, 520, max_tiles, tile_rows, b["plan"], b["tiles"], b["eidx"],
+             b["ewt"], b["row_expert"], b["pidx"], None, None, None, 0.0, None, None, None, None, None, 0, None, None)
+
+
 @pytest.mark.parametrize("T,E,K,tile_rows", [(4096, 256, 6, 128), (100, 16, 4, 8), (33, 1024, 8, 128)])
 def test_dispatch_multi_kernel(T, E, K, tile_rows):
     rng = np.random.default_rng(T)

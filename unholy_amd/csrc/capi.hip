@@ -430,6 +430,40 @@ int uh_moe_scatter(const int32_t* sel, const float* wt, int T, int K, const int3
                    int32_t* eidx, float* ewt, int32_t* row_expert, int32_t* pidx, void* st) {
   return guard([&] { k::moe_scatter(sel, wt, T, K, off, fill, eidx, ewt, row_expert, pidx, S(st)); });
 }
+namespace {
+k::MoeSmallArgs small_args(const int32_t* sel, const float* wt, int T, int K, int E, int P, int max_tiles,
+                           int tile_rows, int32_t* plan, int32_t* tiles, int32_t* eidx, float* ewt,
+                           int32_t* row_expert, int32_t* pidx, uint32_t* hist, const float* route_logits,
+                           const float* route_bias, float route_scale, const float* ds_logits, const float* ds_bias,
+                           const float* ds_bias_vl, const int32_t* ds_tid2eid, const int32_t* ids, int vocab) {
+  k::MoeSmallArgs a{};
+  a.sel = sel;
+  a.wt = wt;
+  a.T = T;
+  a.K = K;
+  a.hist = hist;
+  a.E = E;
+  a.P = P;
+  a.max_tiles = max_tiles;
+  a.tile_rows = tile_rows;
+  a.plan = reinterpret_cast<k::MoePlan*>(plan);
+  a.lt = reinterpret_cast<k::Exl3Tile*>(tiles);
+  a.eidx = eidx;
+  a.ewt = ewt;
+  a.row_expert = row_expert;
+  a.pidx = pidx;
+  a.route_logits = route_logits;
+  a.route_bias = route_bias;
+  a.route_scale = route_scale;
+  a.ds_logits = ds_logits;
+  a.ds_bias = ds_bias;
+  a.ds_bias_vl = ds_bias_vl;
+  a.ds_tid2eid = ds_tid2eid;
+  a.ids = ids;
+  a.vocab = vocab;
+  return a;
+}
+}  // namespace
 int uh_moe_dispatch_small(const int32_t* sel, const float* wt, int T, int K, int E, int P, int max_tiles,
                           int tile_rows, int32_t* plan, int32_t* tiles, int32_t* eidx, float* ewt,
                           int32_t* row_expert, int32_t* pidx, uint32_t* hist, const float* route_logits,
@@ -437,32 +471,24 @@ int uh_moe_dispatch_small(const int32_t* sel, const float* wt, int T, int K, int
                           const float* ds_bias_vl, const int32_t* ds_tid2eid, const int32_t* ids, int vocab,
                           void* st) {
   return guard([&] {
-    k::MoeSmallArgs a{};
-    a.sel = sel;
-    a.wt = wt;
-    a.T = T;
-    a.K = K;
-    a.hist = hist;
-    a.E = E;
-    a.P = P;
-    a.max_tiles = max_tiles;
-    a.tile_rows = tile_rows;
-    a.plan = reinterpret_cast<k::MoePlan*>(plan);
-    a.lt = reinterpret_cast<k::Exl3Tile*>(tiles);
-    a.eidx = eidx;
-    a.ewt = ewt;
-    a.row_expert = row_expert;
-    a.pidx = pidx;
-    a.route_logits = route_logits;
-    a.route_bias = route_bias;
-    a.route_scale = route_scale;
-    a.ds_logits = ds_logits;
-    a.ds_bias = ds_bias;
-    a.ds_bias_vl = ds_bias_vl;
-    a.ds_tid2eid = ds_tid2eid;
-    a.ids = ids;
-    a.vocab = vocab;
-    k::moe_dispatch_small(a, S(st));
+    k::moe_dispatch_small(small_args(sel, wt, T, K, E, P, max_tiles, tile_rows, plan, tiles, eidx, ewt, row_expert,
+                                     pidx, hist, route_logits, route_bias, route_scale, ds_logits, ds_bias, ds_bias_vl,
+                                     ds_tid2eid, ids, vocab),
+                          S(st));
+  });
+}
+int uh_moe_dispatch_mid(const int32_t* sel, const float* wt, int T, int K, int E, int P, int max_tiles, int tile_rows,
+                        int32_t* plan, int32_t* tiles, int32_t* eidx, float* ewt, int32_t* row_expert, int32_t* pidx,
+                        uint32_t* hist, const float* route_logits, const float* route_bias, float route_scale,
+                        const float* ds_logits, const float* ds_bias, const float* ds_bias_vl,
+                        const int32_t* ds_tid2eid, const int32_t* ids, int vocab, const float* softmax_logits,
+                        void* st) {
+  return guard([&] {
+    k::MoeSmallArgs a = small_args(sel, wt, T, K, E, P, max_tiles, tile_rows, plan, tiles, eidx, ewt, row_expert,
+                                   pidx, hist, route_logits, route_bias, route_scale, ds_logits, ds_bias, ds_bias_vl,
+                                   ds_tid2eid, ids, vocab);
+    a.softmax_logits = softmax_logits;
+    k::moe_dispatch_mid(a, S(st));
   });
 }
 int uh_swiglu(const uint16_t* gate, const uint16_t* up, const float* w, uint16_t* h, int rows, int dim, float limit,
@@ -792,10 +818,13 @@ int uh_mx_moe_forward_ev(const uint16_t* x, const float* logits, int T, int K, i
     float* s_wt = wt ? wt : w.wt;
     const auto t = [&](int m, int f) { return tab + size_t(2 * m + f) * E; };
     mark(0);
-    if (T > k::kMoeSmallMaxTokens) k::route_softmax(logits, s_sel, s_wt, T, E, K, st);
+    // Dispatch in one single-block launch up to 512 picks; the routing in that launch too while every token has a
+    // wave of its own (T <= 8), else a wave per token over many workgroups first.
+    const bool one_block = P <= k::kMoeMidMaxPicks, route_in = one_block && T <= 8;
+    if (!route_in) k::route_softmax(logits, s_sel, s_wt, T, E, K, st);
     const int* ntd = &reinterpret_cast<const k::MoePlan*>(w.plan)->n_local_tiles;
     k::Exl3Tile* tiles = reinterpret_cast<k::Exl3Tile*>(w.tiles);
-    if (T <= k::kMoeSmallMaxTokens) {
+    if (one_block) {
       k::MoeSmallArgs a{};
       a.sel = s_sel;
       a.wt = s_wt;
@@ -811,8 +840,8 @@ int uh_mx_moe_forward_ev(const uint16_t* x, const float* logits, int T, int K, i
       a.ewt = w.ewt;
       a.row_expert = w.row_expert;
       a.pidx = w.pidx;
-      a.softmax_logits = logits;  // routing in the same launch
-      k::moe_dispatch_small(a, st);
+      a.softmax_logits = route_in ? logits : nullptr;
+      k::moe_dispatch_mid(a, st);
     } else {
       k::launch_zero_words(w.count, size_t(E), st);  // a kernel: no memset node if the caller captures a graph
       k::moe_count(s_sel, T, K, w.count, E, st);

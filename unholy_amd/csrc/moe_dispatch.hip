@@ -179,9 +179,11 @@ __device__ __forceinline__ float lane_f32(float v, int l) { return __int_as_floa
 // Weights (lane 0's order of operations in the reference's routers): GLM reports its picks in ascending id, the
 // weights follow that order; mode 0 score / sum * scale, 1 sigmoid / (sum + 1e-20) * scale, 2 exp(l - l_first) / sum,
 // the sum taken pick by pick from zero. Lanes k < K write pick k to sel_t / wt_t (and ssel / swt when set).
+// pre (may be null): the lane's logits already loaded (pre[i] = lr[lane + 64 i], 0 past E).
 template <int MODE, int NV>
 __device__ __forceinline__ void route_wave(const float* lr, const float* bias, const int32_t* hash_row, int E, int K,
-                                           float route_scale, int32_t* sel_t, float* wt_t, int* ssel, float* swt) {
+                                           float route_scale, int32_t* sel_t, float* wt_t, int* ssel, float* swt,
+                                           const float* pre = nullptr) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
   int pick = 0;
@@ -196,7 +198,7 @@ __device__ __forceinline__ void route_wave(const float* lr, const float* bias, c
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int e = lane + 64 * i;
-      raw[i] = e < E ? lr[e] : 0.0f;
+      raw[i] = pre ? pre[i] : e < E ? lr[e] : 0.0f;
       float v = -INFINITY;
       if (e < E) {
         if constexpr (MODE == 2) v = raw[i];
@@ -215,16 +217,22 @@ __device__ __forceinline__ void route_wave(const float* lr, const float* bias, c
       }
       const uint32_t ob = bi == 0xffffffffu ? 0u : orderable(bv);
       const uint32_t m = wave_reduce_u32<true>(ob);
-      const uint32_t idx = wave_reduce_u32<false>(ob == m ? bi : 0xffffffffu);
+      // The lowest expert holding the largest key: when one lane holds it (the usual case) that lane's candidate,
+      // else the DPP min over the lanes that do.
+      const uint64_t holders = __ballot(ob == m);
+      const uint32_t idx = __popcll(holders) == 1
+                               ? uint32_t(__builtin_amdgcn_readlane(int(bi), int(__builtin_ctzll(holders))))
+                               : wave_reduce_u32<false>(ob == m ? bi : 0xffffffffu);
+      const int slot = int(idx >> 6), owner = int(idx & 63);
       float v = 0.0f;
 #pragma unroll
       for (int i = 0; i < NV; ++i)
-        if (int(idx >> 6) == i) v = raw[i];
-      const float l = lane_f32(v, int(idx & 63));
+        if (slot == i) {
+          v = raw[i];
+          if (lane == owner) key[i] = -INFINITY;
+        }
+      const float l = lane_f32(v, owner);
       if (lane == k) pick = int(idx), lgt = l;
-#pragma unroll
-      for (int i = 0; i < NV; ++i)
-        if (uint32_t(lane + 64 * i) == idx) key[i] = -INFINITY;
     }
   }
   if constexpr (MODE == 1) {  // ascending id: lane k's pick moves to lane (number of smaller picks)
@@ -305,14 +313,38 @@ __global__ void route_thread_kernel(const float* logits, const float* bias0, con
 }
 
 // One token's routing by one wave inside moe_dispatch_small (MODE 0 DSV4, 1 GLM, 2 softmax; E <= 64 * NV).
+template <int MODE>
+__device__ __forceinline__ const float* route_row(const MoeSmallArgs& a, int t) {
+  return (MODE == 2 ? a.softmax_logits : MODE == 1 ? a.route_logits : a.ds_logits) + size_t(t) * a.E;
+}
 template <int MODE, int NV>
-__device__ __forceinline__ void route_token(const MoeSmallArgs& a, int t, int* skey, float* swt) {
-  const float* lr = (MODE == 2 ? a.softmax_logits : MODE == 1 ? a.route_logits : a.ds_logits) + size_t(t) * a.E;
+__device__ __forceinline__ void route_token(const MoeSmallArgs& a, int t, int* skey, float* swt,
+                                            const float* pre = nullptr) {
+  const float* lr = route_row<MODE>(a, t);
   const bool image = MODE == 0 && a.ds_bias_vl && a.ids[t] >= a.vocab;
   const float* bias = MODE == 1 ? a.route_bias : image ? a.ds_bias_vl : a.ds_bias;
   const int32_t* hash_row = MODE == 0 && !image && a.ds_tid2eid ? a.ds_tid2eid + size_t(a.ids[t]) * a.K : nullptr;
   route_wave<MODE, NV>(lr, bias, hash_row, a.E, a.K, a.route_scale, const_cast<int32_t*>(a.sel) + size_t(t) * a.K,
-                       const_cast<float*>(a.wt) + size_t(t) * a.K, skey + t * a.K, swt + t * a.K);
+                       const_cast<float*>(a.wt) + size_t(t) * a.K, skey + t * a.K, swt + t * a.K, pre);
+}
+// A wave's tokens t = first, first + stride, ...: the next token's logits are loaded before this one is routed.
+template <int MODE, int NV>
+__device__ __forceinline__ void route_tokens(const MoeSmallArgs& a, int first, int stride, int* skey, float* swt) {
+  const int lane = threadIdx.x & 63;
+  const auto load = [&](int t, float (&v)[NV]) {
+    const float* lr = route_row<MODE>(a, t);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] = lane + 64 * i < a.E ? lr[lane + 64 * i] : 0.0f;
+  };
+  float nxt[NV];
+  if (first < a.T) load(first, nxt);
+  for (int t = first; t < a.T; t += stride) {
+    float cur[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) cur[i] = nxt[i];
+    if (t + stride < a.T) load(t + stride, nxt);
+    route_token<MODE, NV>(a, t, skey, swt, cur);
+  }
 }
 
 // ---- single-block dispatch for small steps -------------------------------------------------------------------------
@@ -332,19 +364,27 @@ __global__ __launch_bounds__(SMALL_NT) void moe_dispatch_small_kernel(MoeSmallAr
   asm volatile("" ::"s"(a.softmax_logits), "s"(a.route_logits), "s"(a.ds_logits), "s"(a.eidx), "s"(a.ewt),
                "s"(a.row_expert), "s"(a.pidx), "s"(a.lt), "s"(a.plan), "s"(a.tile_rows), "s"(a.max_tiles),
                "s"(a.resident), "s"(a.hist), "s"(a.P), "s"(a.sel), "s"(a.wt));
+  // Steps with more picks than one wave and no resident mask rank their picks by expert counts (histogram +
+  // scan) instead of comparing every pair of keys; the counts are cleared here, while the routing loads are out.
+  const bool by_hist = n > 64 && !a.resident;
+  __shared__ int ehist[1024], wcnt[SMALL_NT / 64][1024];  // picks per expert; per wave
+  if (by_hist)
+    for (int q = tid; q < (SMALL_NT / 64 + 1) * E; q += SMALL_NT) {
+      if (q < E) ehist[q] = 0;
+      else wcnt[q / E - 1][q % E] = 0;
+    }
   const bool route = a.route_logits || a.ds_logits || a.softmax_logits;
   if (route) {
     const int mode = a.softmax_logits ? 2 : a.route_logits ? 1 : 0;
-    for (int t = wave; t < T; t += SMALL_NT / 64) {
-      if (E <= 256) {
-        if (mode == 2) route_token<2, 4>(a, t, skey, swt);
-        else if (mode == 1) route_token<1, 4>(a, t, skey, swt);
-        else route_token<0, 4>(a, t, skey, swt);
-      } else {
-        if (mode == 2) route_token<2, 16>(a, t, skey, swt);
-        else if (mode == 1) route_token<1, 16>(a, t, skey, swt);
-        else route_token<0, 16>(a, t, skey, swt);
-      }
+    constexpr int S = SMALL_NT / 64;
+    if (E <= 256) {
+      if (mode == 2) route_tokens<2, 4>(a, wave, S, skey, swt);
+      else if (mode == 1) route_tokens<1, 4>(a, wave, S, skey, swt);
+      else route_tokens<0, 4>(a, wave, S, skey, swt);
+    } else {
+      if (mode == 2) route_tokens<2, 16>(a, wave, S, skey, swt);
+      else if (mode == 1) route_tokens<1, 16>(a, wave, S, skey, swt);
+      else route_tokens<0, 16>(a, wave, S, skey, swt);
     }
   } else {
     for (int i = tid; i < n; i += SMALL_NT) {
@@ -427,7 +467,38 @@ __global__ __launch_bounds__(SMALL_NT) void moe_dispatch_small_kernel(MoeSmallAr
   __syncthreads();
   const int mykey = (ek * T + t) * K + j, lo = ek * T * K, hi = (ek + 1) * T * K, lim = E * T * K;
   int rank = 0, off = 0, cnt = 0, nloc = 0;
-  if (n <= 64) {
+  if (by_hist) {
+    // Each wave groups its lanes by expert with a ballot walk over the expert's bits; the lowest lane of a group
+    // records the group's size for its wave and adds it to the expert's count. An exclusive scan of the counts gives
+    // each expert's first row; a pick's row adds the same expert's picks in earlier waves and in lower lanes (the
+    // plan's order within an expert is the pick order). Every pick is resident: nloc = n.
+    uint64_t peers = __ballot(live);
+    for (int b = 31 - __builtin_clz(uint32_t(max(E - 1, 1))); b >= 0; --b) {
+      const uint64_t ones = __ballot(live && ((e >> b) & 1));
+      peers &= ((e >> b) & 1) ? ones : ~ones;
+    }
+    const int inwave = int(__builtin_amdgcn_mbcnt_hi(uint32_t(peers >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(peers), 0u)));
+    if (live && inwave == 0) {
+      wcnt[wave][e] = __popcll(peers);
+      atomicAdd(&ehist[e], __popcll(peers));
+    }
+    __syncthreads();
+    // exclusive scan over experts, two per thread (E <= 1024)
+    const int e0 = 2 * tid, c0 = e0 < E ? ehist[e0] : 0, c1 = e0 + 1 < E ? ehist[e0 + 1] : 0;
+    int total;
+    const int ex = block_exclusive_scan<SMALL_NT>(c0 + c1, &total, lds);
+    __shared__ int estart[1024];
+    if (e0 < E) estart[e0] = ex;
+    if (e0 + 1 < E) estart[e0 + 1] = ex + c0;
+    __syncthreads();
+    if (live) {
+      off = estart[e];
+      cnt = ehist[e];
+      rank = off + inwave;
+      for (int w = 0; w < wave; ++w) rank += wcnt[w][e];
+      nloc = n;
+    }
+  } else if (n <= 64) {
     // All 8 waves count: wave w compares keys 8w .. 8w + 7 against pick l (lane l) and the partial counts are added
     // through LDS (an eighth of the serial compares of one wave doing all of them).
     __shared__ int4 spart[SMALL_NT / 64][64];
@@ -936,6 +1007,20 @@ void moe_dispatch_small(const MoeSmallArgs& a, hipStream_t st) {
   }
   if (!a.sel || !a.wt || !a.plan || !a.lt || !a.eidx || !a.ewt || !a.row_expert || !a.pidx)
     throw std::runtime_error("moe_dispatch_small: null output");
+  moe_dispatch_small_kernel<<<1, SMALL_NT, 0, st>>>(a);
+  UH_CHECK_LAUNCH();
+}
+void moe_dispatch_mid(const MoeSmallArgs& a, hipStream_t st) {
+  static_assert(kMoeMidMaxPicks == SMALL_NT, "a thread per pick");
+  if (a.T <= 0) return;
+  if (a.K <= 0 || a.K > kMaxK || a.T * a.K > kMoeMidMaxPicks) throw std::runtime_error("moe_dispatch_mid: T * K <= 512, K <= 8");
+  if (a.E <= 0 || a.E > 1024) throw std::runtime_error("moe_dispatch_mid: E in [1, 1024]");
+  if (a.P != a.T * a.K) throw std::runtime_error("moe_dispatch_mid: P != T * K");
+  if (a.tile_rows <= 0) throw std::runtime_error("moe_dispatch_mid: tile_rows");
+  if (a.resident || a.remote || a.qin || a.x_dst || a.q_dst || a.req_flag || a.plan_dst)
+    throw std::runtime_error("moe_dispatch_mid: local steps only");
+  if (!a.sel || !a.wt || !a.plan || !a.lt || !a.eidx || !a.ewt || !a.row_expert || !a.pidx)
+    throw std::runtime_error("moe_dispatch_mid: null output");
   moe_dispatch_small_kernel<<<1, SMALL_NT, 0, st>>>(a);
   UH_CHECK_LAUNCH();
 }
