@@ -667,7 +667,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": GEMV_TRAFFIC_BYTES,
                      "traffic_source": "profiles/hbm_traffic_pmc.md (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)",
-                     "kernel": "mx_gemv_kernel<2, 2, 2, 8, false> (w1/w3 grouped GEMV, SwiGLU epilogue)", "avg_launch_ms": g_ms,
+                     "kernel": "mx_gemv_kernel<2, 2, 2, 8, false, true> (w1/w3 grouped GEMV, SwiGLU epilogue)", "avg_launch_ms": g_ms,
                      "algorithmic_bytes_per_launch": float(np.mean(gemv_bytes))},
     }
     if not args.no_sweep:
