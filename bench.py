@@ -595,6 +595,9 @@ def run_only(name, args, rng):
     if name == "grouped":
         return {f"grouped_fp8w_M{M}": bench_grouped_fp8w(M, 100 if M < 4096 else 10, 10 if M < 4096 else 2, rng, c)
                 for M, c in ((1, 16), (64, 16), (4096, 2))}
+    if name == "fp8_m64":  # configs[4] at M = 64: the split-K form with its workspace, then the reference's call
+        return {"fp8_dense_M64": bench_fp8_dense(64, 40, 5, rng, 16),
+                "fp8_dense_M64_no_workspace": bench_fp8_dense(64, 40, 5, rng, 16, form="plain")}
     if name == "fp8":
         return {f"fp8_dense_M{M}": bench_fp8_dense(M, 100 if M < 4096 else 10, 10 if M < 4096 else 2, rng, c)
                 for M, c in ((1, 64), (64, 64), (4096, 4))}
@@ -622,8 +625,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "single", "verify", "prefill", "fp8", "grouped", "producers", "dropin",
-                                       "pack", "remote", "copy"])
+    ap.add_argument("--only", choices=["decode", "single", "verify", "prefill", "fp8", "fp8_m64", "grouped", "producers",
+                                       "dropin", "pack", "remote", "copy"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the MoE expert path runs on a single MI355X in this build "
