@@ -301,7 +301,8 @@ def bench_fp8_dense(M, steps, warmup, rng, copies, form="fused"):
 def bench_grouped_fp8w(M, steps, warmup, rng, copies):
     """The reference's wo_a projection (forward_ref.hip:1012-1022), grouped "mgk,grk->mgr" at the DSV4 shape: a bf16
     [M, 8, 4096], w e4m3 [8 x 1024, 4096] (32 MiB) with 128 x 128 e8m0 scales, c bf16 [M, 8, 1024]; through
-    uh_gemm_grouped_fp8w_wmma (the GEMV for M <= 32, the tiled MFMA GEMM above), rotating over `copies` weight copies
+    uh_gemm_grouped_fp8w_wmma (the GEMV for M <= 16, the row-tile kernel for 16 < M <= 160, the tiled MFMA GEMM above),
+    rotating over `copies` weight copies
     so that they are read from HBM."""
     from unholy_amd import call
     from unholy_amd.device import DeviceBuffer

@@ -7,13 +7,16 @@
 // Three entry points, as the reference has them:
 //   gemm_grouped_fp8w       the reference order (ref_gemm.hip:116-125, :198-202 at G = K: one fp32 fmaf chain over k
 //                           in order), a thread per output: bit-exact against the CPU oracle, not a fast path;
-//   gemm_grouped_fp8w_wmma  the fast path: the GEMV below for M <= 160, else the tiled MFMA GEMM;
-//   gemv_grouped_fp8w       the GEMV (M <= 32), optionally followed by act_quant_fp8 of its outputs (GemvQuant).
+//   gemm_grouped_fp8w_wmma  the fast path: the GEMV below for M <= 16, the row-tile kernel for 16 < M <= 160
+//                           (R % 64 == 0, K <= 4096; else the GEMV), else the tiled MFMA GEMM;
+//   gemv_grouped_fp8w       M <= 32 as the fast path, optionally followed by act_quant_fp8 of its outputs (GemvQuant).
 //
 // GEMV (bound: HBM, 32 MB of weights at the DSV4 shape G = 8, R = 1024, K = 4096): a workgroup per 16-column tile,
 // its 8 waves splitting K in 128-input blocks, every load of a chunk issued before its first use; bf16 MFMA
 // 16x16x32 on the activations as they are and the weights dequantized with the block scale folded in; the 8
 // partial tiles added in LDS in wave order.
+// Row tiles (16 < M <= 160): a workgroup per 64 columns x 32 rows over the whole of K, the activation rows staged once
+// per workgroup in LDS (the GEMV reads them once per 16 columns), the weights held in registers four chunks ahead.
 // GEMM (bound: MFMA at M = 4096): 128-row tiles of one group, 4 waves, 64-input stages in an LDS ring filled by direct
 // global -> LDS loads (two workgroups per CU); bf16 MFMA 32x32x16. A wave's columns lie in one 128-row weight block
 // and a stage in one 128-input block, so the weight scale is one value per stage, folded into the dequantization.
@@ -122,6 +125,173 @@ __global__ __launch_bounds__(64 * GV_W) void grouped_fp8w_gemv_kernel(const bf16
       if (r < M) c[size_t(r) * N + n] = f32_to_bf16(s[i]);
     }
   }
+}
+
+// ---- row tiles, 16 < M <= 160 -----------------------------------------------------------------------------------------
+// A workgroup per 64 columns (one group: R % 64 == 0) x 32 rows, the whole of K (<= 4,096), bf16 C written directly:
+// - 16 waves = 2 column halves x 8 K parts, 32 x 32 output tiles (bf16 MFMA 32x32x16); part p takes block p of every
+//   1,024-input chunk;
+// - a wave's weights for all (<= 4) chunks are loaded into registers up front, interleaved with the first two
+//   activation chunks (issue order: scales, W0 A0 W1 A1 W2 W3, then A(c + 2) once chunk c is done), so chunk c starts
+//   while the later weights stream; loads retire in order and each chunk waits for exactly the loads before its own;
+// - the tile's activation rows go through a 2-slot LDS ring of chunks (32 rows x 1,024 bf16, 64 KB) by direct
+//   global -> LDS loads; piece p (16 bytes) of row r sits at p ^ (r & 15), so the 16 rows of an MFMA operand pass
+//   cover the 64 banks once;
+// - the weights dequantize with the block scale folded in (exact); the 8 parts are added in LDS in part order by all
+//   16 waves;
+// - work item wi = column block x row tiles + row tile; XCD x takes the x-th eighth of the items, so the row tiles of
+//   a column block share one L2 (the second reads the weights from it) and a group's activation rows sit in one L2.
+// Against the GEMV (one 16-column tile per workgroup, every workgroup reading its rows from L2): the activation rows
+// leave L2 once per 64 columns. DSV4 shape at M = 64: 17.8 us against 45 us.
+constexpr int GR_KR = 1024, GR_PPR = GR_KR / 8, GR_SLOT = 32 * GR_KR * 2, GR_MAXCH = 4;
+
+// Loads issued as plain instructions, outside the compiler's wait accounting: the kernel counts them itself (vmcnt,
+// in issue order) and marks the registers written after each wait (gr_landed), so that no use moves above it.
+__device__ __forceinline__ v4i gr_load16(const uint8_t* p) {
+  v4i v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t gr_load_u8(const uint8_t* p) {
+  uint32_t v;
+  asm volatile("global_load_ubyte %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+__device__ __forceinline__ void gr_landed(v4i (&b)[4]) {
+  asm volatile("" : "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
+}
+
+__global__ __launch_bounds__(1024) void grouped_fp8w_rows_kernel(const bf16* a, const uint8_t* w, const uint8_t* sw,
+                                                                 bf16* c, int M, int G, int R, int K) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int N = G * R, KS = K / 128, nch = (KS + 7) / 8;  // nch <= GR_MAXCH
+  const int nw = gridDim.x, lin = blockIdx.x;
+  const int wi = nw % 8 ? lin : (lin & 7) * (nw >> 3) + (lin >> 3);
+  const int RT = (M + 31) / 32, rt = wi % RT, bx = wi / RT, row0 = rt * 32;
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), chh = wave & 1, kh = wave >> 1;
+  const int col0 = bx * 64, grp = col0 / R, n = col0 + chh * 32 + l32;
+  // Weight load x (0..3) of a block: lane l reads 16 bytes of column row 16 (x >> 1) + l % 16 at byte 64 (x & 1) +
+  // 16 (l >> 4), so a load covers 64 contiguous bytes of each of 16 rows (32 bytes of 32 rows in the MFMA's own
+  // layout measured 2.6 us slower at the DSV4 shape). One lane-row swap per dword pair (loads 0 <-> 2, 1 <-> 3) then
+  // leaves lane l with column l % 32: load x holds piece (16 bytes) 2 h + (x >> 1) + 4 (x & 1) of the block.
+  const uint8_t* wld = w + size_t(col0 + chh * 32 + (lane & 15)) * K + (lane >> 4) * 16;
+  const uint8_t* swrow = sw + size_t((col0 + chh * 32) / 128) * KS;  // 32 columns lie in one 128-row block
+  const uint32_t lds0 = lds_addr(smem);
+  // This wave's 4 direct loads of a chunk: 1 KB pieces q = 4 wave + i of the 64 KB slot (rows past M repeat row M - 1,
+  // inputs past K repeat the row's last 8; neither is used).
+  uint32_t rowoff[4];
+  int pin[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int slot = (wave * 4 + i) * 64 + lane, r = slot / GR_PPR;
+    rowoff[i] = uint32_t(min(row0 + r, M - 1) * G + grp) * uint32_t(K) * 2u;
+    pin[i] = ((slot % GR_PPR) ^ (r & 15)) * 8;
+  }
+  const auto issue_a = [&](int ch) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dma16(a, rowoff[i] + uint32_t(min(ch * GR_KR + pin[i], K - 8)) * 2u,
+            lds0 + uint32_t((ch & 1) * GR_SLOT + (wave * 4 + i) * 1024));
+  };
+  v4i b[GR_MAXCH][4];
+  const auto load_w = [&](int u) {
+    const uint8_t* p = wld + min(u * 8 + kh, KS - 1) * 128;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) b[u][x] = gr_load16(p + (x >> 1) * 16 * K + (x & 1) * 64);
+  };
+  // Issue order: the wave's block scales (lane u: chunk u), W0 A0 W1 A1 W2 W3, then A(c + 2) once chunk c is done.
+  // Loads retire in order, so chunk c starts while the later chunks stream.
+  uint32_t sv = gr_load_u8(swrow + min(min(lane, GR_MAXCH - 1) * 8 + kh, KS - 1));
+  load_w(0);
+  issue_a(0);
+  if (nch > 1) {
+    load_w(1);
+    issue_a(1);
+  }
+  if (nch > 2) load_w(2);
+  if (nch > 3) load_w(3);
+  const int r = l32;
+  v16f_t acc = v16f_t{};
+#pragma unroll
+  for (int ch = 0; ch < GR_MAXCH; ++ch) {
+    if (ch >= nch) break;
+    // Chunk ch, its weights and the scales have landed when only the loads issued after A(ch) are pending (4 per
+    // group): ch = 0: W1 A1 W2 W3; ch = 1: W2 W3 A2; ch = 2: A3; each where it exists.
+    const int later = ch == 0 ? (1 < nch) * 2 + (2 < nch) + (3 < nch)
+                      : ch == 1 ? (2 < nch) * 2 + (3 < nch)
+                      : ch == 2 ? (3 < nch)
+                                : 0;
+    switch (later) {
+      case 4: wait_vm<16>(); break;
+      case 3: wait_vm<12>(); break;
+      case 2: wait_vm<8>(); break;
+      case 1: wait_vm<4>(); break;
+      default: wait_vm<0>();
+    }
+    gr_landed(b[ch]);
+    asm volatile("" : "+v"(sv));
+    __syncthreads();  // every wave's part of chunk ch has landed
+    if (ch * 8 + kh < KS) {
+      const uint8_t* sl = smem + (ch & 1) * GR_SLOT;
+      const float swc = __uint_as_float(uint32_t(__builtin_amdgcn_readlane(int(sv), ch)) << 23);
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          // Lanes 16-31 (48-63) of load x trade with lanes 0-15 (32-47) of load x + 2.
+          const auto t = __builtin_amdgcn_permlane16_swap(uint32_t(b[ch][x][d]), uint32_t(b[ch][x + 2][d]), false,
+                                                          false);
+          b[ch][x][d] = int(t[0]);
+          b[ch][x + 2][d] = int(t[1]);
+        }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int x = j >> 1;
+        const bf16x8 bf = fp8x8_to_bf16(uint32_t(b[ch][x][2 * (j & 1)]), uint32_t(b[ch][x][2 * (j & 1) + 1]), swc);
+        const int pc = (kh * 16 + 2 * (2 * h + (x >> 1) + 4 * (x & 1)) + (j & 1)) ^ (r & 15);
+        const bf16x8 af = __builtin_bit_cast(bf16x8, *reinterpret_cast<const v4i*>(sl + (r * GR_PPR + pc) * 16));
+        acc = mfma32_bf16(af, bf, acc);
+      }
+    }
+    if (ch + 2 < nch) {
+      __syncthreads();  // every wave is done with slot ch & 1
+      issue_a(ch + 2);
+    }
+  }
+  // The 8 parts added in part order through LDS, shared by all waves: wave (chh, kh) adds elements 2 kh, 2 kh + 1 of
+  // its column half's lanes. 72-byte lane stride: a half-wave's 8-byte reads cover the 64 banks once.
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(smem);
+  constexpr int LS = 18;
+#pragma unroll
+  for (int i = 0; i < 16; i += 2)
+    *reinterpret_cast<float2*>(red + ((kh * 2 + chh) * 64 + lane) * LS + i) = make_float2(acc[i], acc[i + 1]);
+  __syncthreads();
+  float2 sum = *reinterpret_cast<const float2*>(red + (chh * 64 + lane) * LS + 2 * kh);
+#pragma unroll
+  for (int q = 1; q < 8; ++q) {
+    const float2 v = *reinterpret_cast<const float2*>(red + ((q * 2 + chh) * 64 + lane) * LS + 2 * kh);
+    sum.x += v.x;
+    sum.y += v.y;
+  }
+  // Element i of lane (l32, h) is row 8 (i / 4) + 4 h + i % 4 of the tile, column l32 of the half.
+  const int rr = row0 + 8 * (kh >> 1) + 4 * h + 2 * (kh & 1);
+  if (rr < M) c[size_t(rr) * N + n] = f32_to_bf16(sum.x);
+  if (rr + 1 < M) c[size_t(rr + 1) * N + n] = f32_to_bf16(sum.y);
+}
+
+bool rows_fits(int M, int G, int R, int K) {
+  return M > 16 && M <= 160 && R % 64 == 0 && K <= GR_MAXCH * GR_KR && size_t(M) * G * K * 2 < (size_t(1) << 32);
+}
+void launch_rows(const bf16* a, const uint8_t* w, const uint8_t* sw, bf16* c, int M, int G, int R, int K,
+                 hipStream_t st) {
+  const size_t lds = 2 * size_t(GR_SLOT);
+  auto* kern = &grouped_fp8w_rows_kernel;
+  UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               int(lds)));
+  kern<<<dim3(unsigned(G * R / 64 * ((M + 31) / 32))), 1024, lds, st>>>(a, w, sw, c, M, G, R, K);
+  UH_CHECK_LAUNCH();
 }
 
 // ---- tiled GEMM ------------------------------------------------------------------------------------------------------
@@ -255,8 +425,8 @@ void launch_ref(const bf16* a, const uint8_t* w, const uint8_t* sw, bf16* c, int
   UH_CHECK_LAUNCH();
 }
 
-// The GEMV for up to 160 rows (32-row chunks side by side), the tiled GEMM above: at the DSV4 shape M = 64 ran
-// 69 us tiled (64 workgroups) and 46 us as two chunks; the tiled kernel's workgroup count grows with M.
+// The GEMV for up to 160 rows (32-row chunks side by side) where the row-tile kernel does not take the shape, the tiled
+// GEMM above: at the DSV4 shape M = 64 the GEMV ran 46 us as two chunks, the tiled kernel 69 us (64 workgroups).
 constexpr int GV_MAX_ROWS = 160;
 bool gemv_fits(int M, int R) { return M <= GV_MAX_ROWS && R % 16 == 0; }
 void launch_gemv(const bf16* a, const uint8_t* w, const uint8_t* sw, bf16* c, int M, int G, int R, int K,
@@ -298,7 +468,8 @@ void gemm_grouped_fp8w_wmma(const bf16* a, const uint8_t* w, const uint8_t* sw, 
                             hipStream_t st) {
   check_args("gemm_grouped_fp8w_wmma", a, w, sw, c, M, G, R, K);
   if (M == 0) return;
-  if (gemv_fits(M, R)) launch_gemv(a, w, sw, c, M, G, R, K, st);
+  if (rows_fits(M, G, R, K)) launch_rows(a, w, sw, c, M, G, R, K, st);
+  else if (gemv_fits(M, R)) launch_gemv(a, w, sw, c, M, G, R, K, st);
   else if (tiled_fits(G, R, K)) launch_tiled(a, w, sw, c, M, G, R, K, st);
   else launch_ref(a, w, sw, c, M, G, R, K, st);  // shapes the fast kernels do not tile (R % 128 != 0)
 }
@@ -309,7 +480,8 @@ void gemv_grouped_fp8w(const bf16* a, const uint8_t* w, const uint8_t* sw, bf16*
   if (M > 32) throw std::runtime_error("gemv_grouped_fp8w: M > 32");  // the reference's bound (gemv.hip:653)
   if (gq.q && (!gq.qs || (size_t(G) * R) % 128)) throw std::runtime_error("gemv_grouped_fp8w: quantization shape");
   if (M == 0) return;
-  if (gemv_fits(M, R)) launch_gemv(a, w, sw, c, M, G, R, K, st);
+  if (rows_fits(M, G, R, K)) launch_rows(a, w, sw, c, M, G, R, K, st);
+  else if (gemv_fits(M, R)) launch_gemv(a, w, sw, c, M, G, R, K, st);
   else launch_ref(a, w, sw, c, M, G, R, K, st);
   // act_quant_fp8 (block 128) of the bf16 outputs, the values the reference's last blocks quantize (a second launch
   // here instead of its per-segment counters, which stay zero).
