@@ -267,9 +267,8 @@ def bench_single_gemv(w, steps, warmup, rng):
 def bench_fp8_dense(M, steps, warmup, rng, copies, form="fused"):
     """A bf16 [M, 4096] -> e4m3 per 1x128 with fp32 scales (in the step); W e4m3 [4096, 4096]
     with fp32 128x128 scales (quantized once from N(0, 0.02)); rotating over `copies` weight copies. form "fused":
-    for M <= 16 the quantization inside the GEMV launch (uh_gemm_fp8_f32s_x), otherwise act_quant_fp8_f32s then
-    uh_gemm_fp8_f32s_ws (with its workspace: the split-K kernel for 16 < M <= 64); "two": act_quant_fp8_f32s then
-    uh_gemm_fp8_f32s_ws; "plain": act_quant_fp8_f32s then uh_gemm_fp8_f32s (the reference's call, no workspace)."""
+    for M <= 16 the quantization inside the GEMV launch (uh_gemm_fp8_f32s_x), otherwise as "two"; "two":
+    act_quant_fp8_f32s then uh_gemm_fp8_f32s (the reference's call sequence)."""
     from unholy_amd import call
     from unholy_amd.device import DeviceBuffer
     N = K = 4096
@@ -282,18 +281,13 @@ def bench_fp8_dense(M, steps, warmup, rng, copies, form="fused"):
     x = DeviceBuffer.from_array(to_bf16(rng.standard_normal((M, K), dtype=np.float32)))
     q, sa = DeviceBuffer(M * K), DeviceBuffer(M * (K // 128) * 4)
     c = DeviceBuffer(M * N * 2)
-    wsb = call("uh_gemm_fp8_f32s_ws_size", M, N, K)
-    work = DeviceBuffer(max(wsb, 16))
 
     def fn(i, stream):
         if form == "fused" and M <= 16:
             call("uh_gemm_fp8_f32s_x", x, K, wq[i % copies], ws, c, N, M, N, K, stream.handle)
             return
         call("uh_act_quant_fp8_f32s", x, K, q, sa, M, K, 128, stream.handle)
-        if form == "plain":
-            call("uh_gemm_fp8_f32s", q, sa, wq[i % copies], ws, c, N, M, N, K, stream.handle)
-        else:
-            call("uh_gemm_fp8_f32s_ws", q, sa, wq[i % copies], ws, c, N, M, N, K, work, wsb, stream.handle)
+        call("uh_gemm_fp8_f32s", q, sa, wq[i % copies], ws, c, N, M, N, K, stream.handle)
 
     return time_graph(fn, steps, warmup, per_graph=copies)
 
@@ -596,9 +590,8 @@ def run_only(name, args, rng):
     if name == "grouped":
         return {f"grouped_fp8w_M{M}": bench_grouped_fp8w(M, 100 if M < 4096 else 10, 10 if M < 4096 else 2, rng, c)
                 for M, c in ((1, 16), (64, 16), (4096, 2))}
-    if name == "fp8_m64":  # configs[4] at M = 64: the split-K form with its workspace, then the reference's call
-        return {"fp8_dense_M64": bench_fp8_dense(64, 40, 5, rng, 16),
-                "fp8_dense_M64_no_workspace": bench_fp8_dense(64, 40, 5, rng, 16, form="plain")}
+    if name == "fp8_m64":  # configs[4] at M = 64
+        return {"fp8_dense_M64": bench_fp8_dense(64, 40, 5, rng, 16)}
     if name == "fp8":
         return {f"fp8_dense_M{M}": bench_fp8_dense(M, 100 if M < 4096 else 10, 10 if M < 4096 else 2, rng, c)
                 for M, c in ((1, 64), (64, 64), (4096, 4))}
@@ -718,8 +711,6 @@ def main():
             e = wl[f"fp8_dense_M{M} (configs[4])"]
             if M <= 16:  # the two-call form beside the fused one
                 e["ms_act_quant_then_gemm"] = bench_fp8_dense(M, 100, 10, rng, copies, form="two")
-            elif M <= 64:  # the reference's call (no workspace) beside the split-K form
-                e["ms_no_workspace"] = bench_fp8_dense(M, 100, 10, rng, copies, form="plain")
         for M, copies in ((1, 16), (64, 16), (4096, 2)):
             t = bench_grouped_fp8w(M, 100 if M < 4096 else 10, 10 if M < 4096 else 2, rng, copies)
             wl[f"grouped_fp8w_wo_a_M{M}"] = grouped_entry(M, t)

@@ -30,14 +30,6 @@ void gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const fl
 // the same results bit for bit in one launch (for decode rows). ldx % 8 == 0, x 16-byte aligned.
 void gemm_fp8_f32s_x(const bf16* x, int ldx, const uint8_t* w, const float* sw, bf16* c, int ldc, int M, int N,
                      int K, hipStream_t st);
-// No reference counterpart: gemm_fp8_f32s with a caller's workspace, for 16 < M <= 64: 64-column workgroups over K
-// slices, fp32 partial tiles in ws added in slice order (the activation rows are read once per 64 columns instead of
-// once per 16). gemm_fp8_f32s_ws_size gives the bytes (0: the shape needs none and the call is gemm_fp8_f32s's); the
-// split form needs N % 64, K % 256, ldc % 4 and 8-byte aligned C. Sums differ from gemm_fp8_f32s only in fp32
-// association.
-size_t gemm_fp8_f32s_ws_size(int M, int N, int K);
-void gemm_fp8_f32s_ws(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw, bf16* c, int ldc, int M,
-                      int N, int K, void* ws, size_t ws_bytes, hipStream_t st);
 // Grouped "mgk,grk->mgr" with fp8 weights dequantized by 128x128 e8m0 block scales, in the reference's order (one
 // fp32 fmaf chain over k per output). Ref ref.hpp:42-45. K % 128 == 0.
 void gemm_grouped_fp8w(const bf16* a, const uint8_t* w, const uint8_t* sw, bf16* c, int M, int G, int R, int K,

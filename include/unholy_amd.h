@@ -319,12 +319,6 @@ int uh_gemv_grouped_fp8w(const uint16_t* a, const uint8_t* w, const uint8_t* sw,
  * M <= 16 (decode rows): the same results bit for bit, one launch. */
 int uh_gemm_fp8_f32s_x(const uint16_t* x, int ldx, const uint8_t* w, const float* sw, uint16_t* c, int ldc, int M,
                        int N, int K, void* stream);
-/* No reference counterpart: uh_gemm_fp8_f32s with a workspace ws of uh_gemm_fp8_f32s_ws_size(M, N, K) bytes (0: none
- * needed, the call is uh_gemm_fp8_f32s's), for 16 < M <= 64: 64-column workgroups over K slices whose fp32 partial
- * tiles are added in slice order; the split form needs N % 64, K % 256, ldc % 4, C 8-byte aligned. */
-size_t uh_gemm_fp8_f32s_ws_size(int M, int N, int K);
-int uh_gemm_fp8_f32s_ws(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw, uint16_t* c, int ldc,
-                        int M, int N, int K, void* ws, size_t ws_bytes, void* stream);
 /* ref.hpp:139-140 and :142-143: the reference-order (bit-exact) a8w4 GEMMs */
 int uh_gemm_a8w4(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, uint16_t* c, int ldc,
                  int M, int N, int K, void* stream);

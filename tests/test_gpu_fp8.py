@@ -22,7 +22,11 @@ def _weights_f32s(rng, N, K):
     return q.download((N, K), np.uint8), s.download(((N + 127) // 128, K // 128), np.float32), w
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (5, 384, 1024), (64, 512, 1024), (300, 256, 512), (3, 136, 384), (1000, 768, 1024), (129, 200, 256)])
+# 16 < M <= 256 with N % 32 == 0 takes the row-tile kernel: one to four 2,048-input chunks, ragged last chunks (K = 640,
+# 2,176), one 32-column block (N = 32), a weight-scale row shared by fewer than 128 columns (N = 96), 1 to 8 row tiles.
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (5, 384, 1024), (64, 512, 1024), (300, 256, 512), (3, 136, 384),
+                                   (1000, 768, 1024), (129, 200, 256), (17, 32, 640), (33, 1024, 8192), (64, 96, 6144),
+                                   (48, 256, 2176), (40, 200, 512), (200, 128, 1024), (256, 96, 2176), (129, 64, 384)])
 def test_fp8_f32_scales(M, N, K):
     """BASELINE config 4 form: A bf16 -> e4m3 per 1x128 with fp32 scales; W e4m3 with fp32 128x128 scales."""
     rng = np.random.default_rng(M + N)
@@ -73,32 +77,24 @@ def test_fp8_f32s_fused_quant_is_bit_identical(M, N, K, pad):
 
 @pytest.mark.parametrize("M,N,K,pad", [(17, 512, 1024, 0), (64, 1024, 2048, 8), (40, 4096, 1024, 0), (64, 128, 256, 0),
                                        (33, 640, 4096, 64), (40, 16384, 2048, 0)])
-def test_fp8_f32s_split_k(M, N, K, pad):
-    """gemm_fp8_f32s_ws (16 < M <= 64: 64-column workgroups over K slices, fp32 partials added in slice order; one
-    slice writes C directly): against the oracle within the bf16 bar, a too-small workspace refused, and C columns
-    past N untouched."""
+def test_fp8_f32s_row_tiles_ldc(M, N, K, pad):
+    """gemm_fp8_f32s at 16 < M <= 64 (the row-tile kernel) with a C row stride wider than N: against the oracle within
+    the bf16 bar, and C columns past N untouched."""
     rng = np.random.default_rng(5 * M + K)
     ldx, ldc = K + pad, N + 8
     x = randn_bf16(rng, (M, ldx))
     wq, ws, _ = _weights_f32s(rng, N, K)
-    dx, dwq, dws = dev(x), dev(wq), dev(ws)
     q, sa = DeviceBuffer(M * K), DeviceBuffer(M * (K // 128) * 4)
-    call("uh_act_quant_fp8_f32s", dx, ldx, q, sa, M, K, 128, None)
+    call("uh_act_quant_fp8_f32s", dev(x), ldx, q, sa, M, K, 128, None)
     q_ref, sa_ref = oracle.act_quant_fp8_f32s(x[:, :K])
-    wsb = call("uh_gemm_fp8_f32s_ws_size", M, N, K)
-    wsp = DeviceBuffer(max(wsb, 16))
-    sentinel = np.full((M, ldc), 0x7FC1, np.uint16)
-    c = dev(sentinel)
-    call("uh_gemm_fp8_f32s_ws", q, sa, dwq, dws, c, ldc, M, N, K, wsp, wsb, None)
+    c = dev(np.full((M, ldc), 0x7FC1, np.uint16))
+    call("uh_gemm_fp8_f32s", q, sa, dev(wq), dev(ws), c, ldc, M, N, K, None)
     g = c.download((M, ldc), np.uint16)
     assert np.all(g[:, N:] == 0x7FC1)
     ref16, _ = oracle.gemm_w8a8(q_ref, sa_ref, wq, ws)
     mr = max_rel(from_bf16(g[:, :N]), from_bf16(ref16))
-    print(f"fp8 f32s split-K M={M} N={N} K={K}: workspace {wsb} B, max_rel {mr:.3e}")
+    print(f"fp8 f32s row tiles M={M} N={N} K={K} ldc={ldc}: max_rel {mr:.3e}")
     assert mr <= 1e-2
-    if wsb:
-        with pytest.raises(Exception, match="workspace too small"):
-            call("uh_gemm_fp8_f32s_ws", q, sa, dwq, dws, c, ldc, M, N, K, wsp, wsb - 4, None)
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (8, 1024, 512), (33, 256, 1024), (200, 512, 512), (17, 200, 640), (1000, 768, 1024)])

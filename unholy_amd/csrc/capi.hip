@@ -764,11 +764,6 @@ int uh_gemm_fp8_f32s_x(const uint16_t* x, int ldx, const uint8_t* w, const float
                        int N, int K, void* st) {
   return guard([&] { k::gemm_fp8_f32s_x(x, ldx, w, sw, c, ldc, M, N, K, S(st)); });
 }
-size_t uh_gemm_fp8_f32s_ws_size(int M, int N, int K) { return k::gemm_fp8_f32s_ws_size(M, N, K); }
-int uh_gemm_fp8_f32s_ws(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw, uint16_t* c, int ldc,
-                        int M, int N, int K, void* ws, size_t ws_bytes, void* st) {
-  return guard([&] { k::gemm_fp8_f32s_ws(a, sa, w, sw, c, ldc, M, N, K, ws, ws_bytes, S(st)); });
-}
 int uh_gemm_a8w4(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, uint16_t* c, int ldc,
                  int M, int N, int K, void* st) {
   return guard([&] { k::gemm_a8w4(a, sa, w, sw, c, ldc, M, N, K, S(st)); });

@@ -9,6 +9,7 @@
 
 #include "common.hpp"
 #include "numerics.hpp"
+#include "pipe.hpp"
 #include "unholy/kernels/gemm_wmma.hpp"
 #include "unholy/kernels/gemv.hpp"
 #include "unholy/kernels/ref.hpp"
@@ -427,213 +428,174 @@ void launch_fp8_gemv_t(const Fp8GemmArgs& a, hipStream_t st, const Fp8Parts& pp)
 }
 
 
-// ---- fp8 dense, 16 < M <= 64 with fp32 scales: wide column blocks, K split over workgroups ------------------------
-// The one-tile GEMV above reads all M activation rows once per 16 output columns: at M = 64 that is 4x the weight
-// bytes again from L2 (a load-only kernel of that pattern takes 12 us at 4096 x 4096 against 5 us for the weights
-// alone). Here a workgroup owns 64 columns x one K slice of KR inputs x all M rows:
-// - its activation slice (codes + fp32 row scales) is staged once into LDS, so A is read from L2 once per 64
-//   columns; the codes are held as their bf16 values (exact), converted once per workgroup rather than once per
-//   column tile;
-// - 4 KP waves = 4 column tiles x KP parts of the chunk; each wave's weights (16 columns x KR / KP inputs, 32 bytes
-//   per lane per 128-block) are all loaded before the staging starts;
-// - per 128-block: four bf16 16x16x32 MFMAs per row tile on exactly dequantized operands, the block sum folded as
-//   acc += raw * (sa * sw) (the reference's fp32-scale order);
-// - the KP parts are added in LDS in part order; S slices write fp32 partial tiles to
-//   part[s][M][N], which fp8_split_sum_kernel adds in slice order into bf16 C (S = 1: C directly).
-// Sums differ from the one-tile GEMV only in fp32 association (tolerance parity, not bit parity).
-constexpr int SK_COLS = 64, SK_PAD = 16, SK_MAXS = 16;
+// ---- fp8 dense, 16 < M <= 256 with fp32 scales: row tiles ------------------------------------------------------------
+// A workgroup per 32 columns x 32 rows over the whole of K (<= 8,192), bf16 C written directly, one launch:
+// - 16 waves = 16 K parts of one 32 x 32 output tile (bf16 MFMA 32x32x16); part p takes block p of every 2,048-input
+//   chunk;
+// - the tile's activation codes go through a 2-slot LDS ring of chunks (32 rows x 2,048 codes, 64 KB) by direct
+//   global -> LDS loads; piece p (16 bytes) of row r sits at p ^ (r & 15), so a 16-lane pass of 16-byte reads covers
+//   the 64 banks once; the fp32 row scales of the tile are staged beside them;
+// - a wave's weights for all (<= 4) chunks are loaded into registers up front, interleaved with the first two
+//   activation chunks (issue order: scales, W0 A0 W1 A1 W2 W3, then A(c + 2) once chunk c is done); loads retire in
+//   order and each chunk waits for exactly the loads before its own. Weight load x (0..3) of a block: lane l reads
+//   16 bytes of column 16 (x >> 1) + l % 16 at byte 64 (x & 1) + 16 (l >> 4) (64 contiguous bytes of each of 16
+//   rows); one lane-row swap per dword pair then leaves lane l with column l % 32, load x holding piece
+//   2 h + (x >> 1) + 4 (x & 1) of the block, and the activation reads take the same pieces;
+// - per block: the raw chain of 8 MFMAs on exactly converted codes, folded as acc += raw * (sa * sw) (the reference's
+//   fp32-scale order); the 16 parts are added in LDS in part order, wave p adding accumulator element p;
+// - work item wi = column block x row tiles + row tile; XCD x takes the x-th eighth of the items, so the row tiles of
+//   a column block share one L2.
+// Against the one-tile GEMV (every 16-column workgroup reading all M rows from L2): the rows leave L2 once per 32
+// columns. A K split over workgroups (fp32 partial tiles in a workspace, added in slice order by a second launch) ran
+// 17.9 us per step at 64 x 4096 x 4096 against 14.0 here: the second launch and the partial round trip cost more
+// than the split gains.
+// Up to FR_MAXM rows (8 row tiles): at 4096 x 4096 the row tiles ran 22-43 us per step for 65 <= M <= 256 against
+// 47-53 us for the 128 x 128 tiled GEMM (too few workgroups there), which wins from M = 384 on (53 against 62 us).
+constexpr int FR_KR = 2048, FR_SLOT = 32 * FR_KR, FR_MAXCH = 4, FR_LS = 17, FR_MAXM = 256;
 
-struct Fp8SplitArgs {
-  const uint8_t* a;    // e4m3 codes [M, K]
-  const float* sa;     // fp32 row scales [M, K / 128]
-  const uint8_t* w;    // e4m3 [N, K]
-  const float* sw;     // fp32 [ceil(N / 128), K / 128]
-  uint16_t* c;         // bf16 [M, ldc] (S = 1)
-  float* part;         // fp32 [S, M, N] (S > 1)
-  int ldc, M, N, K, S;
-};
-
-template <int KP, int NB>
-__global__ __launch_bounds__(256 * KP) void fp8_split_kernel(Fp8SplitArgs a) {
-  constexpr int NT = 256 * KP, KR = KP * NB * 128, LDA = KR + SK_PAD / 2, KB = KR / 128;
+__global__ __launch_bounds__(1024) void fp8_rows_kernel(Fp8GemmArgs p) {
+  using namespace pipe;
   extern __shared__ __align__(16) uint8_t smem[];
-  uint16_t* sA = reinterpret_cast<uint16_t*>(smem);            // the codes' values as bf16 [64][LDA]
-  float* sS = reinterpret_cast<float*>(smem + 64 * LDA * 2);  // row scales [64][KB]
-  const int M = a.M, K = a.K, N = a.N, KS = K / 128, slice = blockIdx.y, nch = K / (a.S * KR);
-  const int tid = threadIdx.x, lane = tid & 63, nl = lane & 15, g = lane >> 4;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), ct = wave & 3, kh = wave >> 2;  // column tile, K part
-  const int n0 = blockIdx.x * SK_COLS + ct * 16, n = n0 + nl;
-  const int mlive = (M + 15) / 16;
-  const uint8_t* wrow = a.w + size_t(n) * K + g * 32;
-  v4f acc[4];
+  const int M = p.M, N = p.N, K = p.K, KS = K / 128, nch = (KS + 15) / 16;  // nch <= FR_MAXCH
+  const int nw = gridDim.x, lin = blockIdx.x;
+  const int wi = nw % 8 ? lin : (lin & 7) * (nw >> 3) + (lin >> 3);
+  const int RT = (M + 31) / 32, rt = wi % RT, bx = wi / RT, row0 = rt * 32;
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+  const int kh = __builtin_amdgcn_readfirstlane(tid >> 6);  // K part = wave
+  const int col0 = bx * 32, n = col0 + l32;
+  float* const ssa = reinterpret_cast<float*>(smem + 2 * FR_SLOT);  // row scales [32][KS]
+  const uint8_t* wld = p.w + size_t(col0 + (lane & 15)) * K + (lane >> 4) * 16;
+  const float* swrow = p.sw32 + size_t(col0 / 128) * KS;  // 32 columns lie in one 128-row block
+  const uint32_t lds0 = lds_addr(smem);
+  uint32_t rowoff[4];
+  int pin[4];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) acc[mt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  // The slice's K range in chunks of KR inputs (one chunk unless the slice is longer than the LDS holds).
-  for (int ch = 0; ch < nch; ++ch) {
-    const int chunk = slice * nch + ch;
-    const int kb0 = chunk * KB + kh * NB;  // this wave's first global 128-block in the chunk
-    // Weights first: every load of the wave's NB blocks in flight before the activation staging.
-    v4i b[NB][2];
-#pragma unroll
-    for (int u = 0; u < NB; ++u) {
-      b[u][0] = *reinterpret_cast<gptr<v4i>>(as_global(wrow + (kb0 + u) * 128));
-      b[u][1] = *reinterpret_cast<gptr<v4i>>(as_global(wrow + (kb0 + u) * 128 + 16));
-    }
-    float swv[NB];
-#pragma unroll
-    for (int u = 0; u < NB; ++u) swv[u] = a.sw[size_t(n0 / 128) * KS + kb0 + u];
-    if (ch > 0) __syncthreads();  // every wave is past its reads of the previous chunk
-    // The chunk's activation rows into LDS.
-    const size_t col0 = size_t(chunk) * KR;
-    // Every load of the staging is issued before the first is used (one memory latency, not one per item).
-    constexpr int per_row = KR / 16, IT = 64 * per_row / NT;
-    const int items = M * per_row;
-    uint4 raw[IT];
-#pragma unroll
-    for (int j = 0; j < IT; ++j) {
-      const int it = min(j * NT + tid, items - 1), r = it / per_row, c16 = (it % per_row) * 16;
-      raw[j] = *reinterpret_cast<const uint4*>(a.a + size_t(r) * K + col0 + c16);
-    }
-    const float sv = tid < M * KB ? a.sa[size_t(tid / KB) * KS + chunk * KB + tid % KB] : 0.0f;  // M * KB <= NT
-#pragma unroll
-    for (int j = 0; j < IT; ++j) {
-      const int it = j * NT + tid, r = it / per_row, c16 = (it % per_row) * 16;
-      if (it < items) {
-        *reinterpret_cast<bf16x8*>(sA + r * LDA + c16) = fp8x8_to_bf16(raw[j].x, raw[j].y, 1.0f);
-        *reinterpret_cast<bf16x8*>(sA + r * LDA + c16 + 8) = fp8x8_to_bf16(raw[j].z, raw[j].w, 1.0f);
-      }
-    }
-    if (tid < M * KB) sS[tid] = sv;
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < NB; ++u) {
-      const int lb = kh * NB + u;  // block within the chunk
-      bf16x8 bf[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-        bf[t] = fp8x8_to_bf16(uint32_t(b[u][t / 2][2 * (t % 2)]), uint32_t(b[u][t / 2][2 * (t % 2) + 1]), 1.0f);
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        if (mt >= mlive) break;
-        const int row = mt * 16 + nl;
-        bf16x8 af[4];
-        if (row < M) {
-          const uint16_t* ap = sA + row * LDA + lb * 128 + g * 32;
-#pragma unroll
-          for (int t = 0; t < 4; ++t) af[t] = *reinterpret_cast<const bf16x8*>(ap + 8 * t);
-        } else {
-#pragma unroll
-          for (int t = 0; t < 4; ++t) af[t] = bf16x8{};
-        }
-        v4f raw = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int t = 0; t < 4; ++t) raw = mfma_bf16(af[t], bf[t], raw);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int rr = mt * 16 + 4 * g + i;  // C row of value i
-          const float sa = rr < M ? sS[rr * KB + lb] : 0.0f;
-          acc[mt][i] += raw[i] * (sa * swv[u]);
-        }
-      }
-    }
+  for (int i = 0; i < 4; ++i) {
+    const int slot = (kh * 4 + i) * 64 + lane, r = slot / (FR_KR / 16);
+    rowoff[i] = uint32_t(min(row0 + r, M - 1)) * uint32_t(K);
+    pin[i] = ((slot % (FR_KR / 16)) ^ (r & 15)) * 16;
   }
-  // The K parts added in order (part 0 + part 1 + ...), through LDS (the staged rows are no longer read).
-  __syncthreads();
-  v4f* red = reinterpret_cast<v4f*>(smem);
-  if (kh > 0)
+  const auto issue_a = [&](int ch) {
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) red[(((kh - 1) * 4 + ct) * 4 + mt) * 64 + lane] = acc[mt];
-  __syncthreads();
-  if (kh > 0) return;
-#pragma unroll
-  for (int q = 1; q < KP; ++q)
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) acc[mt] += red[(((q - 1) * 4 + ct) * 4 + mt) * 64 + lane];
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    if (mt >= mlive) break;
-    const v4f s = acc[mt];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = mt * 16 + 4 * g + i;
-      if (r >= M) continue;
-      if (a.S == 1) a.c[size_t(r) * a.ldc + n] = f32_to_bf16(s[i]);
-      else a.part[(size_t(slice) * M + r) * N + n] = s[i];
-    }
-  }
-}
-
-// C[m][n] = bf16(sum over slices s in order of part[s][m][n]): a thread per 4 columns.
-__global__ __launch_bounds__(256) void fp8_split_sum_kernel(const float* __restrict__ part, int S, int M, int N,
-                                                            uint16_t* __restrict__ c, int ldc) {
-  const size_t i = (size_t(blockIdx.x) * 256 + threadIdx.x) * 4, total = size_t(M) * N;
-  if (i >= total) return;
-  const int m = int(i / N), n = int(i % N);
-  float4 v[SK_MAXS];  // every slice's load issued before the first add
-#pragma unroll
-  for (int s = 0; s < SK_MAXS; ++s)
-    if (s < S) v[s] = *reinterpret_cast<const float4*>(part + size_t(s) * total + i);
-  float4 acc = v[0];
-#pragma unroll
-  for (int s = 1; s < SK_MAXS; ++s)
-    if (s < S) {
-      acc.x += v[s].x;
-      acc.y += v[s].y;
-      acc.z += v[s].z;
-      acc.w += v[s].w;
-    }
-  const uint32_t lo = uint32_t(f32_to_bf16(acc.x)) | uint32_t(f32_to_bf16(acc.y)) << 16;
-  const uint32_t hi = uint32_t(f32_to_bf16(acc.z)) | uint32_t(f32_to_bf16(acc.w)) << 16;
-  *reinterpret_cast<uint2*>(c + size_t(m) * ldc + n) = make_uint2(lo, hi);
-}
-
-// Slices for a shape (0: the split kernel does not take it): N % 64, K % 256; the fewest slices S (K a multiple of
-// 256 S) that give >= 256 workgroups, else as many as K allows. A slice is staged in chunks of split_chunk inputs.
-int split_slices(int M, int N, int K) {
-  if (M <= 16 || M > 64 || N % SK_COLS || K % 256 || N <= 0) return 0;
-  const int cols = N / SK_COLS;
-  int best = 0;
-  for (int S = 1; S * 256 <= K && S <= SK_MAXS; ++S) {
-    if (K % (256 * S)) continue;
-    best = S;
-    if (cols * S >= 256) break;
-  }
-  return best;
-}
-// Chunk of a slice held in LDS at once: the largest of 1024, 512, 256 inputs that divides the slice.
-int split_chunk(int K, int S) {
-  const int r = K / S;
-  return r % 1024 == 0 ? 1024 : r % 512 == 0 ? 512 : 256;
-}
-
-void launch_split(const Fp8SplitArgs& a0, void* ws, size_t ws_bytes, hipStream_t st) {
-  Fp8SplitArgs a = a0;
-  a.S = split_slices(a.M, a.N, a.K);
-  if (!a.S) throw std::runtime_error("fp8 split: shape");
-  if (a.S > 1) {
-    const size_t need = size_t(a.S) * a.M * a.N * 4;
-    if (!ws || ws_bytes < need) throw std::runtime_error("fp8 split: workspace too small");
-    if (reinterpret_cast<uintptr_t>(ws) % 16) throw std::runtime_error("fp8 split: workspace alignment");
-    a.part = static_cast<float*>(ws);
-  }
-  // 16 waves (4 K parts) when the chunk has 4 or more 128-blocks, else 8 waves (2 parts).
-  const int KR = split_chunk(a.K, a.S), KP = KR >= 512 ? 4 : 2, NB = KR / (128 * KP);
-  const size_t lds = size_t(64) * (KR + SK_PAD / 2) * 2 + size_t(64) * (KR / 128) * 4;
-  const dim3 grid(unsigned(a.N / SK_COLS), unsigned(a.S));
-  const auto go = [&](auto kern, int threads) {
-    UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
-    kern<<<grid, threads, lds, st>>>(a);
+    for (int i = 0; i < 4; ++i)
+      dma16(p.a, rowoff[i] + uint32_t(min(ch * FR_KR + pin[i], K - 16)),
+            lds0 + uint32_t((ch & 1) * FR_SLOT + (kh * 4 + i) * 1024));
   };
-  if (KP == 2) go(&fp8_split_kernel<2, 1>, 512);
-  else if (NB == 1) go(&fp8_split_kernel<4, 1>, 1024);
-  else go(&fp8_split_kernel<4, 2>, 1024);
-  UH_CHECK_LAUNCH();
-  if (a.S > 1) {
-    fp8_split_sum_kernel<<<unsigned(cdiv(size_t(a.M) * a.N / 4, 256)), 256, 0, st>>>(a.part, a.S, a.M, a.N, a.c, a.ldc);
-    UH_CHECK_LAUNCH();
+  v4i b[FR_MAXCH][4];
+  const auto load_w = [&](int u) {
+    const uint8_t* q = wld + min(u * 16 + kh, KS - 1) * 128;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) b[u][x] = vload16(q + (x >> 1) * 16 * K + (x & 1) * 64);
+  };
+  // Issue order: the scales (lane u < nch: the wave's weight scale of chunk u; thread t: row scales t, t + 1024 of
+  // the tile), W0 A0 W1 A1 W2 W3, then A(c + 2).
+  uint32_t swv = vload_u32(swrow + min(min(lane, FR_MAXCH - 1) * 16 + kh, KS - 1));
+  uint32_t sav[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int e = min(tid + 1024 * j, 32 * KS - 1);
+    sav[j] = vload_u32(p.sa32 + size_t(min(row0 + e / KS, M - 1)) * KS + e % KS);
   }
+  load_w(0);
+  issue_a(0);
+  if (nch > 1) {
+    load_w(1);
+    issue_a(1);
+  }
+  if (nch > 2) load_w(2);
+  if (nch > 3) load_w(3);
+  const int r = l32;
+  v16f_t acc = v16f_t{};
+#pragma unroll
+  for (int ch = 0; ch < FR_MAXCH; ++ch) {
+    if (ch >= nch) break;
+    // Chunk ch, its weights and the scales have landed when only the loads issued after A(ch) are pending (4 per
+    // group): ch = 0: W1 A1 W2 W3; ch = 1: W2 W3 A2; ch = 2: A3; each where it exists.
+    const int later = ch == 0 ? (1 < nch) * 2 + (2 < nch) + (3 < nch)
+                      : ch == 1 ? (2 < nch) * 2 + (3 < nch)
+                      : ch == 2 ? (3 < nch)
+                                : 0;
+    switch (later) {
+      case 4: wait_vm<16>(); break;
+      case 3: wait_vm<12>(); break;
+      case 2: wait_vm<8>(); break;
+      case 1: wait_vm<4>(); break;
+      default: wait_vm<0>();
+    }
+    vlanded(b[ch]);
+    if (ch == 0) {
+      vlanded(swv);
+      vlanded(sav[0]);
+      vlanded(sav[1]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        if (tid + 1024 * j < 32 * KS) ssa[tid + 1024 * j] = __uint_as_float(sav[j]);
+    }
+    __syncthreads();  // every wave's part of chunk ch (and the row scales) has landed
+    const int kb = ch * 16 + kh;
+    if (kb < KS) {
+      const uint8_t* sl = smem + (ch & 1) * FR_SLOT;
+      const float sw = __uint_as_float(uint32_t(__builtin_amdgcn_readlane(int(swv), ch)));
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          // Lanes 16-31 (48-63) of load x trade with lanes 0-15 (32-47) of load x + 2.
+          const auto t = __builtin_amdgcn_permlane16_swap(uint32_t(b[ch][x][d]), uint32_t(b[ch][x + 2][d]), false,
+                                                          false);
+          b[ch][x][d] = int(t[0]);
+          b[ch][x + 2][d] = int(t[1]);
+        }
+      v16f_t raw = v16f_t{};
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        const int pc = (kh * 8 + 2 * h + (x >> 1) + 4 * (x & 1)) ^ (r & 15);
+        const v4i av = *reinterpret_cast<const v4i*>(sl + r * FR_KR + pc * 16);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const bf16x8 af = fp8x8_to_bf16(uint32_t(av[2 * e]), uint32_t(av[2 * e + 1]), 1.0f);
+          const bf16x8 bf = fp8x8_to_bf16(uint32_t(b[ch][x][2 * e]), uint32_t(b[ch][x][2 * e + 1]), 1.0f);
+          raw = mfma32_bf16(af, bf, raw);
+        }
+      }
+      // Element i of lane (l32, h) is row 8 (i / 4) + 4 h + i % 4 of the tile.
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[i] += raw[i] * (ssa[(8 * (i / 4) + 4 * h + (i % 4)) * KS + kb] * sw);
+    }
+    if (ch + 2 < nch) {
+      __syncthreads();  // every wave is done with slot ch & 1
+      issue_a(ch + 2);
+    }
+  }
+  // The 16 parts added in part order through LDS: wave p adds element p of every lane (17-float lane stride: the
+  // reads of a wave cover the 64 banks once).
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) red[(kh * 64 + lane) * FR_LS + i] = acc[i];
+  __syncthreads();
+  float sum = red[lane * FR_LS + kh];
+#pragma unroll
+  for (int q = 1; q < 16; ++q) sum += red[(q * 64 + lane) * FR_LS + kh];
+  const int row = row0 + 8 * (kh / 4) + 4 * h + (kh % 4);
+  if (row < M) p.c[size_t(row) * p.ldc + n] = f32_to_bf16(sum);
 }
 }  // namespace
+
+bool fp8_rows_fits(const Fp8GemmArgs& a) {
+  return a.sa32 && a.sw32 && a.M > 16 && a.M <= FR_MAXM && a.N % 32 == 0 && a.K % 128 == 0 && a.K >= 128 &&
+         a.K <= FR_MAXCH * FR_KR && size_t(a.M) * a.K < (size_t(1) << 32);
+}
+void launch_fp8_rows(const Fp8GemmArgs& a, hipStream_t st) {
+  if (!fp8_rows_fits(a)) throw std::runtime_error("fp8 rows: shape");
+  if (!a.a || !a.w || !a.c) throw std::runtime_error("fp8 gemm: null operand");
+  const size_t lds = 2 * size_t(FR_SLOT) + size_t(32) * (a.K / 128) * 4;
+  auto* kern = &fp8_rows_kernel;
+  UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               int(lds)));
+  kern<<<dim3(unsigned(a.N / 32 * ((a.M + 31) / 32))), 1024, lds, st>>>(a);
+  UH_CHECK_LAUNCH();
+}
 
 void launch_fp8_skinny(const Fp8GemmArgs& a0, hipStream_t st) {
   Fp8GemmArgs a = a0;
@@ -777,41 +739,6 @@ void gemm_fp8_f32s(const uint8_t* a, const float* sa, const uint8_t* w, const fl
   launch_fp8_gemm(g, st);
 }
 
-
-size_t gemm_fp8_f32s_ws_size(int M, int N, int K) {
-  const int S = split_slices(M, N, K);
-  return S > 1 ? size_t(S) * M * N * 4 : 0;
-}
-namespace {
-void check_split(const char* name, int M, int N, int K, int ldc, const void* c, const void* w, const float* sw) {
-  if (!split_slices(M, N, K))
-    throw std::runtime_error(std::string(name) + ": 16 < M <= 64, N % 64, K % 256 (gemm_fp8_f32s_ws_size says 0 for "
-                             "other shapes only when they need no workspace)");
-  if (!c || !w || !sw) throw std::runtime_error(std::string(name) + ": null operand");
-  if (ldc < N || ldc % 4 || reinterpret_cast<uintptr_t>(c) % 8) throw std::runtime_error(std::string(name) + ": ldc");
-}
-}  // namespace
-void gemm_fp8_f32s_ws(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw, bf16* c, int ldc, int M,
-                      int N, int K, void* ws, size_t ws_bytes, hipStream_t st) {
-  if (M <= 0) return;
-  if (!split_slices(M, N, K)) {  // the workspace is not needed: the plain entry's kernels
-    gemm_fp8_f32s(a, sa, w, sw, c, ldc, M, N, K, st);
-    return;
-  }
-  check_split("gemm_fp8_f32s_ws", M, N, K, ldc, c, w, sw);
-  if (!a || !sa) throw std::runtime_error("gemm_fp8_f32s_ws: null operand");
-  Fp8SplitArgs g{};
-  g.a = a;
-  g.sa = sa;
-  g.w = w;
-  g.sw = sw;
-  g.c = c;
-  g.ldc = ldc;
-  g.M = M;
-  g.N = N;
-  g.K = K;
-  launch_split(g, ws, ws_bytes, st);
-}
 
 namespace {
 Fp8Parts to_parts(const GemvPart* parts, int nparts) {

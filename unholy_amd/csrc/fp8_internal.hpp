@@ -36,10 +36,14 @@ struct Fp8Parts {
 void launch_fp8_skinny(const Fp8GemmArgs& a, hipStream_t st);
 // M <= 64: one workgroup per 16-column tile, K split over its 8 waves (bandwidth-shaped).
 void launch_fp8_gemv(const Fp8GemmArgs& a, hipStream_t st, const Fp8Parts* parts = nullptr);
+// 16 < M <= 256 with fp32 scales: one workgroup per 32 x 32 output tile over the whole of K (N % 32, K <= 8192).
+bool fp8_rows_fits(const Fp8GemmArgs& a);
+void launch_fp8_rows(const Fp8GemmArgs& a, hipStream_t st);
 // M > 64: the LDS-ring MFMA GEMM (N % 256, K % 128, ldc % 8; fp8_tiled_fits says whether a shape qualifies).
 bool fp8_tiled_fits(const Fp8GemmArgs& a);
 void launch_fp8_tiled(const Fp8GemmArgs& a, hipStream_t st);
-// Picks the small-M kernel (M <= 64), the tiled GEMM, or the row-group kernel for shapes the tiled one does not take.
+// Picks the row-tile kernel (fp32 scales, 16 < M <= 256, where it fits), the small-M kernel (M <= 64), the tiled GEMM,
+// or the row-group kernel for shapes the tiled one does not take.
 void launch_fp8_gemm(const Fp8GemmArgs& a, hipStream_t st);
 
 }  // namespace unholy::kernels

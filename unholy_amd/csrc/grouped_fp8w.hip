@@ -145,22 +145,6 @@ __global__ __launch_bounds__(64 * GV_W) void grouped_fp8w_gemv_kernel(const bf16
 // leave L2 once per 64 columns. DSV4 shape at M = 64: 17.8 us against 45 us.
 constexpr int GR_KR = 1024, GR_PPR = GR_KR / 8, GR_SLOT = 32 * GR_KR * 2, GR_MAXCH = 4;
 
-// Loads issued as plain instructions, outside the compiler's wait accounting: the kernel counts them itself (vmcnt,
-// in issue order) and marks the registers written after each wait (gr_landed), so that no use moves above it.
-__device__ __forceinline__ v4i gr_load16(const uint8_t* p) {
-  v4i v;
-  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
-  return v;
-}
-__device__ __forceinline__ uint32_t gr_load_u8(const uint8_t* p) {
-  uint32_t v;
-  asm volatile("global_load_ubyte %0, %1, off" : "=v"(v) : "v"(p) : "memory");
-  return v;
-}
-__device__ __forceinline__ void gr_landed(v4i (&b)[4]) {
-  asm volatile("" : "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
-}
-
 __global__ __launch_bounds__(1024) void grouped_fp8w_rows_kernel(const bf16* a, const uint8_t* w, const uint8_t* sw,
                                                                  bf16* c, int M, int G, int R, int K) {
   extern __shared__ __align__(16) uint8_t smem[];
@@ -198,11 +182,11 @@ __global__ __launch_bounds__(1024) void grouped_fp8w_rows_kernel(const bf16* a, 
   const auto load_w = [&](int u) {
     const uint8_t* p = wld + min(u * 8 + kh, KS - 1) * 128;
 #pragma unroll
-    for (int x = 0; x < 4; ++x) b[u][x] = gr_load16(p + (x >> 1) * 16 * K + (x & 1) * 64);
+    for (int x = 0; x < 4; ++x) b[u][x] = vload16(p + (x >> 1) * 16 * K + (x & 1) * 64);
   };
   // Issue order: the wave's block scales (lane u: chunk u), W0 A0 W1 A1 W2 W3, then A(c + 2) once chunk c is done.
   // Loads retire in order, so chunk c starts while the later chunks stream.
-  uint32_t sv = gr_load_u8(swrow + min(min(lane, GR_MAXCH - 1) * 8 + kh, KS - 1));
+  uint32_t sv = vload_u8(swrow + min(min(lane, GR_MAXCH - 1) * 8 + kh, KS - 1));
   load_w(0);
   issue_a(0);
   if (nch > 1) {
@@ -229,8 +213,8 @@ __global__ __launch_bounds__(1024) void grouped_fp8w_rows_kernel(const bf16* a, 
       case 1: wait_vm<4>(); break;
       default: wait_vm<0>();
     }
-    gr_landed(b[ch]);
-    asm volatile("" : "+v"(sv));
+    vlanded(b[ch]);
+    vlanded(sv);
     __syncthreads();  // every wave's part of chunk ch has landed
     if (ch * 8 + kh < KS) {
       const uint8_t* sl = smem + (ch & 1) * GR_SLOT;

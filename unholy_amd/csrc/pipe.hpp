@@ -55,6 +55,32 @@ __device__ __forceinline__ void dma4(const void* base, uint32_t voff, uint32_t l
                : "memory", "m0");
 }
 
+// Global loads issued as plain instructions, outside the compiler's wait accounting: the kernel counts them itself
+// (vmcnt, in issue order, with the direct loads above) and marks the registers written after its wait (vlanded), so
+// that no use moves above that wait. Only for registers the compiler has no reason to copy before the wait (no loop-
+// carried values, no spills).
+__device__ __forceinline__ uh::v4i vload16(const void* p) {
+  uh::v4i v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t vload_u8(const void* p) {
+  uint32_t v;
+  asm volatile("global_load_ubyte %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t vload_u32(const void* p) {
+  uint32_t v;
+  asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void vlanded(uh::v4i (&b)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(b[i]));
+}
+__device__ __forceinline__ void vlanded(uint32_t& x) { asm volatile("" : "+v"(x)); }
+
 template <int N>
 __device__ __forceinline__ void wait_vm() {
   static_assert(N < 64);
