@@ -15,9 +15,11 @@ def dev(a):
     return DeviceBuffer.from_array(np.ascontiguousarray(a))
 
 
-def test_graph_replays_fp8_dense_step():
-    rng = np.random.default_rng(3)
-    M, N, K = 4, 1024, 1024
+# M = 4: the GEMV; 64 and 200: the row-tile kernel (asm-issued loads, counted waits).
+@pytest.mark.parametrize("M", [4, 64, 200])
+def test_graph_replays_fp8_dense_step(M):
+    rng = np.random.default_rng(3 + M)
+    N, K = 1024, 4096
     x = dev(randn_bf16(rng, (M, K)))
     wq = rng.integers(0, 256, (N, K), dtype=np.uint8)
     wq[(wq & 0x7F) == 0x7F] = 0
@@ -40,6 +42,35 @@ def test_graph_replays_fp8_dense_step():
         st.synchronize()
         assert np.array_equal(c.download((M, N), np.uint16), eager), rep
         step()  # eager work between replays
+        st.synchronize()
+
+
+@pytest.mark.parametrize("M", [1, 64])
+def test_graph_replays_grouped_fp8w(M):
+    """The grouped fp8-weight GEMM (M = 1: the GEMV; 64: the row-tile kernel) replayed: every replay equals eager."""
+    rng = np.random.default_rng(11 + M)
+    G, R, K = 4, 512, 4096
+    a = dev(randn_bf16(rng, (M, G, K)))
+    wq = rng.integers(0, 256, (G * R, K), dtype=np.uint8)
+    wq[(wq & 0x7F) == 0x7F] = 0
+    w, sw = dev(wq), dev(rng.integers(118, 126, (G * R // 128, K // 128), dtype=np.uint8))
+    c = DeviceBuffer(M * G * R * 2)
+    st = Stream()
+
+    def step():
+        call("uh_gemm_grouped_fp8w_wmma", a, w, sw, c, M, G, R, K, st.handle)
+
+    step()
+    st.synchronize()
+    eager = c.download((M, G * R), np.uint16)
+    g = Graph(st, step)
+    for rep in range(3):
+        c.zero()
+        synchronize()
+        g.launch()
+        st.synchronize()
+        assert np.array_equal(c.download((M, G * R), np.uint16), eager), rep
+        step()
         st.synchronize()
 
 
