@@ -191,3 +191,13 @@ def test_gemv_w8a8_glu(M):
     assert np.array_equal(hq.download((M, I), np.uint8), q_ref)
     assert np.array_equal(hs.download((M, I // 128), np.uint8), s_ref)
     assert not counters.download(I // 128, np.uint32).any()
+
+
+def test_fp8_gemm_refuses_narrow_ldc():
+    """A C row stride below N is refused before any launch (every kernel of the dense dispatch would write past it)."""
+    M, N, K = 40, 256, 512
+    q, sa = DeviceBuffer(M * K), DeviceBuffer(M * (K // 128) * 4)
+    w, sw = DeviceBuffer(N * K), DeviceBuffer((N // 128) * (K // 128) * 4)
+    c = DeviceBuffer(M * N * 2)
+    with pytest.raises(Exception, match="ldc < N"):
+        call("uh_gemm_fp8_f32s", q, sa, w, sw, c, N - 32, M, N, K, None)

@@ -880,6 +880,7 @@ void launch_mx_gemm(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st) 
 }
 
 void launch_fp8_gemm(const Fp8GemmArgs& a, hipStream_t st) {
+  if (a.M > 0 && a.ldc < a.N) throw std::runtime_error("fp8 gemm: ldc < N");
   if (fp8_rows_fits(a)) launch_fp8_rows(a, st);
   else if (a.M <= 64) launch_fp8_gemv(a, st);
   else if (fp8_tiled_fits(a)) launch_fp8_tiled(a, st);
