@@ -7,16 +7,18 @@
 // Three entry points, as the reference has them:
 //   gemm_grouped_fp8w       the reference order (ref_gemm.hip:116-125, :198-202 at G = K: one fp32 fmaf chain over k
 //                           in order), a thread per output: bit-exact against the CPU oracle, not a fast path;
-//   gemm_grouped_fp8w_wmma  the fast path: the GEMV below for M <= 16, the row-tile kernel for 16 < M <= 160
-//                           (R % 64 == 0, K <= 4096; else the GEMV), else the tiled MFMA GEMM;
+//   gemm_grouped_fp8w_wmma  the fast path: the row-tile kernel for M <= 160 (M <= 16: R % 32 == 0, K <= 8192;
+//                           else R % 64 == 0, K <= 4096), the GEMV for other shapes up to M = 160, else the tiled
+//                           MFMA GEMM;
 //   gemv_grouped_fp8w       M <= 32 as the fast path, optionally followed by act_quant_fp8 of its outputs (GemvQuant).
 //
 // GEMV (bound: HBM, 32 MB of weights at the DSV4 shape G = 8, R = 1024, K = 4096): a workgroup per 16-column tile,
 // its 8 waves splitting K in 128-input blocks, every load of a chunk issued before its first use; bf16 MFMA
 // 16x16x32 on the activations as they are and the weights dequantized with the block scale folded in; the 8
 // partial tiles added in LDS in wave order.
-// Row tiles (16 < M <= 160): a workgroup per 64 columns x 32 rows over the whole of K, the activation rows staged once
-// per workgroup in LDS (the GEMV reads them once per 16 columns), the weights held in registers four chunks ahead.
+// Row tiles (M <= 160): a workgroup per 64 columns x 32 rows (M <= 16: 32 columns x 16 rows) over the whole of K, the
+// activation rows staged once per workgroup in LDS (the GEMV reads them once per 16 columns), the weights held in
+// registers up to four chunks ahead.
 // GEMM (bound: MFMA at M = 4096): 128-row tiles of one group, 4 waves, 64-input stages in an LDS ring filled by direct
 // global -> LDS loads (two workgroups per CU); bf16 MFMA 32x32x16. A wave's columns lie in one 128-row weight block
 // and a stage in one 128-input block, so the weight scale is one value per stage, folded into the dequantization.
@@ -127,8 +129,9 @@ __global__ __launch_bounds__(64 * GV_W) void grouped_fp8w_gemv_kernel(const bf16
   }
 }
 
-// ---- row tiles, 16 < M <= 160 -----------------------------------------------------------------------------------------
-// A workgroup per 64 columns (one group: R % 64 == 0) x 32 rows, the whole of K (<= 4,096), bf16 C written directly:
+// ---- row tiles, M <= 160 -----------------------------------------------------------------------------------------
+// A workgroup per 64 columns (one group: R % 64 == 0) x 32 rows, the whole of K (<= 4,096), bf16 C written directly
+// (M <= 16: 32 columns x 16 rows, K <= 8,192, 16 K parts of 2,048-input chunks; the parameters below):
 // - 16 waves = 2 column halves x 8 K parts, 32 x 32 output tiles (bf16 MFMA 32x32x16); part p takes block p of every
 //   1,024-input chunk;
 // - a wave's weights for all (<= 4) chunks are loaded into registers up front, interleaved with the first two
@@ -142,19 +145,31 @@ __global__ __launch_bounds__(64 * GV_W) void grouped_fp8w_gemv_kernel(const bf16
 // - work item wi = column block x row tiles + row tile; XCD x takes the x-th eighth of the items, so the row tiles of
 //   a column block share one L2 (the second reads the weights from it) and a group's activation rows sit in one L2.
 // Against the GEMV (one 16-column tile per workgroup, every workgroup reading its rows from L2): the activation rows
-// leave L2 once per 64 columns. DSV4 shape at M = 64: 17.8 us against 45 us.
-constexpr int GR_KR = 1024, GR_PPR = GR_KR / 8, GR_SLOT = 32 * GR_KR * 2, GR_MAXCH = 4;
+// leave L2 once per 64 columns. DSV4 shape: 17.6 us against 45 us at M = 64; 10.0 / 11.5 / 12.0 us against 10.8 / 13.4 /
+// 14.9 us at M = 1 / 8 / 16 (the 32-column form: 256 workgroups, each wave's weights in flight at once).
+constexpr int GR_SLOT = 64 * 1024, GR_MAXCH = 4;
 
+// CH column halves of 32 (workgroup width 32 CH), TR staged rows (32, or 16 for M <= 16: the MFMA's rows 16-31 then
+// read rows 0-15 again and are not stored); KP = 16 / CH K parts, chunks of KR = 128 KP inputs, a 64 KB slot either way.
+template <int CH, int TR>
+struct GroupedRows {
+  static constexpr int KP = 16 / CH, KR = 128 * KP, PPR = KR / 8, W = 32 * CH;
+  static_assert(TR * KR * 2 == GR_SLOT, "one chunk fills a slot");
+};
+
+template <int CH, int TR>
 __global__ __launch_bounds__(1024) void grouped_fp8w_rows_kernel(const bf16* a, const uint8_t* w, const uint8_t* sw,
                                                                  bf16* c, int M, int G, int R, int K) {
+  using T = GroupedRows<CH, TR>;
+  constexpr int KP = T::KP, KR = T::KR, PPR = T::PPR;
   extern __shared__ __align__(16) uint8_t smem[];
-  const int N = G * R, KS = K / 128, nch = (KS + 7) / 8;  // nch <= GR_MAXCH
+  const int N = G * R, KS = K / 128, nch = (KS + KP - 1) / KP;  // nch <= GR_MAXCH
   const int nw = gridDim.x, lin = blockIdx.x;
   const int wi = nw % 8 ? lin : (lin & 7) * (nw >> 3) + (lin >> 3);
-  const int RT = (M + 31) / 32, rt = wi % RT, bx = wi / RT, row0 = rt * 32;
+  const int RT = (M + TR - 1) / TR, rt = wi % RT, bx = wi / RT, row0 = rt * TR;
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), chh = wave & 1, kh = wave >> 1;
-  const int col0 = bx * 64, grp = col0 / R, n = col0 + chh * 32 + l32;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), chh = wave % CH, kh = wave / CH;
+  const int col0 = bx * T::W, grp = col0 / R, n = col0 + chh * 32 + l32;
   // Weight load x (0..3) of a block: lane l reads 16 bytes of column row 16 (x >> 1) + l % 16 at byte 64 (x & 1) +
   // 16 (l >> 4), so a load covers 64 contiguous bytes of each of 16 rows (32 bytes of 32 rows in the MFMA's own
   // layout measured 2.6 us slower at the DSV4 shape). One lane-row swap per dword pair (loads 0 <-> 2, 1 <-> 3) then
@@ -168,25 +183,25 @@ __global__ __launch_bounds__(1024) void grouped_fp8w_rows_kernel(const bf16* a, 
   int pin[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int slot = (wave * 4 + i) * 64 + lane, r = slot / GR_PPR;
+    const int slot = (wave * 4 + i) * 64 + lane, r = slot / PPR;
     rowoff[i] = uint32_t(min(row0 + r, M - 1) * G + grp) * uint32_t(K) * 2u;
-    pin[i] = ((slot % GR_PPR) ^ (r & 15)) * 8;
+    pin[i] = ((slot % PPR) ^ (r & 15)) * 8;
   }
   const auto issue_a = [&](int ch) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      dma16(a, rowoff[i] + uint32_t(min(ch * GR_KR + pin[i], K - 8)) * 2u,
+      dma16(a, rowoff[i] + uint32_t(min(ch * KR + pin[i], K - 8)) * 2u,
             lds0 + uint32_t((ch & 1) * GR_SLOT + (wave * 4 + i) * 1024));
   };
   v4i b[GR_MAXCH][4];
   const auto load_w = [&](int u) {
-    const uint8_t* p = wld + min(u * 8 + kh, KS - 1) * 128;
+    const uint8_t* p = wld + min(u * KP + kh, KS - 1) * 128;
 #pragma unroll
     for (int x = 0; x < 4; ++x) b[u][x] = vload16(p + (x >> 1) * 16 * K + (x & 1) * 64);
   };
   // Issue order: the wave's block scales (lane u: chunk u), W0 A0 W1 A1 W2 W3, then A(c + 2) once chunk c is done.
   // Loads retire in order, so chunk c starts while the later chunks stream.
-  uint32_t sv = vload_u8(swrow + min(min(lane, GR_MAXCH - 1) * 8 + kh, KS - 1));
+  uint32_t sv = vload_u8(swrow + min(min(lane, GR_MAXCH - 1) * KP + kh, KS - 1));
   load_w(0);
   issue_a(0);
   if (nch > 1) {
@@ -195,7 +210,7 @@ __global__ __launch_bounds__(1024) void grouped_fp8w_rows_kernel(const bf16* a, 
   }
   if (nch > 2) load_w(2);
   if (nch > 3) load_w(3);
-  const int r = l32;
+  const int r = l32 & (TR - 1);
   v16f_t acc = v16f_t{};
 #pragma unroll
   for (int ch = 0; ch < GR_MAXCH; ++ch) {
@@ -216,7 +231,7 @@ __global__ __launch_bounds__(1024) void grouped_fp8w_rows_kernel(const bf16* a, 
     vlanded(b[ch]);
     vlanded(sv);
     __syncthreads();  // every wave's part of chunk ch has landed
-    if (ch * 8 + kh < KS) {
+    if (ch * KP + kh < KS) {
       const uint8_t* sl = smem + (ch & 1) * GR_SLOT;
       const float swc = __uint_as_float(uint32_t(__builtin_amdgcn_readlane(int(sv), ch)) << 23);
 #pragma unroll
@@ -234,7 +249,7 @@ __global__ __launch_bounds__(1024) void grouped_fp8w_rows_kernel(const bf16* a, 
         const int x = j >> 1;
         const bf16x8 bf = fp8x8_to_bf16(uint32_t(b[ch][x][2 * (j & 1)]), uint32_t(b[ch][x][2 * (j & 1) + 1]), swc);
         const int pc = (kh * 16 + 2 * (2 * h + (x >> 1) + 4 * (x & 1)) + (j & 1)) ^ (r & 15);
-        const bf16x8 af = __builtin_bit_cast(bf16x8, *reinterpret_cast<const v4i*>(sl + (r * GR_PPR + pc) * 16));
+        const bf16x8 af = __builtin_bit_cast(bf16x8, *reinterpret_cast<const v4i*>(sl + (r * PPR + pc) * 16));
         acc = mfma32_bf16(af, bf, acc);
       }
     }
@@ -243,39 +258,58 @@ __global__ __launch_bounds__(1024) void grouped_fp8w_rows_kernel(const bf16* a, 
       issue_a(ch + 2);
     }
   }
-  // The 8 parts added in part order through LDS, shared by all waves: wave (chh, kh) adds elements 2 kh, 2 kh + 1 of
-  // its column half's lanes. 72-byte lane stride: a half-wave's 8-byte reads cover the 64 banks once.
+  // The KP parts added in part order through LDS, shared by all waves: wave (chh, kh) adds elements CH kh ..
+  // CH kh + CH - 1 of its column half's lanes. Lane stride 18 floats for 8-byte reads (CH 2), 17 for 4-byte ones
+  // (CH 1): a half-wave's reads cover the 64 banks once.
   __syncthreads();
   float* red = reinterpret_cast<float*>(smem);
-  constexpr int LS = 18;
+  constexpr int LS = CH == 2 ? 18 : 17;
+  float* mine = red + ((kh * CH + chh) * 64 + lane) * LS;
+  if constexpr (CH == 2) {
 #pragma unroll
-  for (int i = 0; i < 16; i += 2)
-    *reinterpret_cast<float2*>(red + ((kh * 2 + chh) * 64 + lane) * LS + i) = make_float2(acc[i], acc[i + 1]);
-  __syncthreads();
-  float2 sum = *reinterpret_cast<const float2*>(red + (chh * 64 + lane) * LS + 2 * kh);
+    for (int i = 0; i < 16; i += 2) *reinterpret_cast<float2*>(mine + i) = make_float2(acc[i], acc[i + 1]);
+  } else {
 #pragma unroll
-  for (int q = 1; q < 8; ++q) {
-    const float2 v = *reinterpret_cast<const float2*>(red + ((q * 2 + chh) * 64 + lane) * LS + 2 * kh);
-    sum.x += v.x;
-    sum.y += v.y;
+    for (int i = 0; i < 16; ++i) mine[i] = acc[i];
   }
+  __syncthreads();
+  float sum[CH];
+#pragma unroll
+  for (int e = 0; e < CH; ++e) sum[e] = red[(chh * 64 + lane) * LS + CH * kh + e];
+#pragma unroll
+  for (int q = 1; q < KP; ++q)
+#pragma unroll
+    for (int e = 0; e < CH; ++e) sum[e] += red[((q * CH + chh) * 64 + lane) * LS + CH * kh + e];
   // Element i of lane (l32, h) is row 8 (i / 4) + 4 h + i % 4 of the tile, column l32 of the half.
-  const int rr = row0 + 8 * (kh >> 1) + 4 * h + 2 * (kh & 1);
-  if (rr < M) c[size_t(rr) * N + n] = f32_to_bf16(sum.x);
-  if (rr + 1 < M) c[size_t(rr + 1) * N + n] = f32_to_bf16(sum.y);
+#pragma unroll
+  for (int e = 0; e < CH; ++e) {
+    const int i = CH * kh + e, rr = 8 * (i / 4) + 4 * h + (i % 4);
+    if (rr < TR && row0 + rr < M) c[size_t(row0 + rr) * N + n] = f32_to_bf16(sum[e]);
+  }
 }
 
+// M <= 16: 32-column workgroups of 16 staged rows (256 workgroups at the DSV4 shape, every wave's weights in flight at
+// once); 16 < M <= 160: 64-column workgroups of 32-row tiles.
 bool rows_fits(int M, int G, int R, int K) {
-  return M > 16 && M <= 160 && R % 64 == 0 && K <= GR_MAXCH * GR_KR && size_t(M) * G * K * 2 < (size_t(1) << 32);
+  if (M < 1 || M > 160 || size_t(M) * G * K * 2 >= (size_t(1) << 32)) return false;
+  return M <= 16 ? R % 32 == 0 && K <= GR_MAXCH * GroupedRows<1, 16>::KR
+                 : R % 64 == 0 && K <= GR_MAXCH * GroupedRows<2, 32>::KR;
+}
+template <int CH, int TR>
+void launch_rows_t(const bf16* a, const uint8_t* w, const uint8_t* sw, bf16* c, int M, int G, int R, int K,
+                   hipStream_t st) {
+  const size_t lds = 2 * size_t(GR_SLOT);
+  auto* kern = &grouped_fp8w_rows_kernel<CH, TR>;
+  UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               int(lds)));
+  kern<<<dim3(unsigned(G * R / GroupedRows<CH, TR>::W * ((M + TR - 1) / TR))), 1024, lds, st>>>(a, w, sw, c, M, G, R,
+                                                                                                 K);
+  UH_CHECK_LAUNCH();
 }
 void launch_rows(const bf16* a, const uint8_t* w, const uint8_t* sw, bf16* c, int M, int G, int R, int K,
                  hipStream_t st) {
-  const size_t lds = 2 * size_t(GR_SLOT);
-  auto* kern = &grouped_fp8w_rows_kernel;
-  UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                               int(lds)));
-  kern<<<dim3(unsigned(G * R / 64 * ((M + 31) / 32))), 1024, lds, st>>>(a, w, sw, c, M, G, R, K);
-  UH_CHECK_LAUNCH();
+  if (M <= 16) launch_rows_t<1, 16>(a, w, sw, c, M, G, R, K, st);
+  else launch_rows_t<2, 32>(a, w, sw, c, M, G, R, K, st);
 }
 
 // ---- tiled GEMM ------------------------------------------------------------------------------------------------------
