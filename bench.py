@@ -431,7 +431,8 @@ def grouped_entry(M, ms):
     wbytes = G * R * K + (G * R // 128) * (K // 128)
     e = {"ms": ms, "tokens_per_s": M / (ms * 1e-3), "TFLOPs": 2 * M * G * R * K / (ms * 1e-3) / 1e12,
          "GBps_weights": wbytes / (ms * 1e-3) / 1e9}
-    if M <= 32:
+    # 2 M flop per weight byte: below the bf16 ridge (~312 flop/B) the weight stream bounds the call
+    if 2 * M * G * R * K / wbytes < BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):
         e["frac_hbm_peak"] = e["GBps_weights"] / HBM_PEAK_GBS
     else:
         e["frac_bf16_mfma_peak"] = e["TFLOPs"] / BF16_PEAK_TFLOPS
@@ -709,6 +710,11 @@ def main():
                                                   "TFLOPs": 2 * M * D * D / (t * 1e-3) / 1e12,
                                                   "GBps_weights": D * D / (t * 1e-3) / 1e9}
             e = wl[f"fp8_dense_M{M} (configs[4])"]
+            # 2 M flop per weight byte against the bf16 ridge (the operands are dequantized to bf16)
+            if 2 * M < BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):
+                e["frac_hbm_peak"] = e["GBps_weights"] / HBM_PEAK_GBS
+            else:
+                e["frac_bf16_mfma_peak"] = e["TFLOPs"] / BF16_PEAK_TFLOPS
             if M <= 16:  # the two-call form beside the fused one
                 e["ms_act_quant_then_gemm"] = bench_fp8_dense(M, 100, 10, rng, copies, form="two")
         for M, copies in ((1, 16), (64, 16), (4096, 2)):
