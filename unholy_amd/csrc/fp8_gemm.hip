@@ -457,6 +457,7 @@ __global__ __launch_bounds__(1024) void fp8_rows_kernel(Fp8GemmArgs p) {
   using namespace pipe;
   extern __shared__ __align__(16) uint8_t smem[];
   const int M = p.M, N = p.N, K = p.K, KS = K / 128, nch = (KS + 15) / 16;  // nch <= FR_MAXCH
+  if (nch < 1) return;  // (the host requires K >= 128) no load is ever left pending past the chunk loop
   const int nw = gridDim.x, lin = blockIdx.x;
   const int wi = nw % 8 ? lin : (lin & 7) * (nw >> 3) + (lin >> 3);
   const int RT = (M + 31) / 32, rt = wi % RT, bx = wi / RT, row0 = rt * 32;

@@ -164,6 +164,7 @@ __global__ __launch_bounds__(1024) void grouped_fp8w_rows_kernel(const bf16* a, 
   constexpr int KP = T::KP, KR = T::KR, PPR = T::PPR;
   extern __shared__ __align__(16) uint8_t smem[];
   const int N = G * R, KS = K / 128, nch = (KS + KP - 1) / KP;  // nch <= GR_MAXCH
+  if (nch < 1) return;  // (K % 128 == 0, K > 0 on the host) no load is ever left pending past the chunk loop
   const int nw = gridDim.x, lin = blockIdx.x;
   const int wi = nw % 8 ? lin : (lin & 7) * (nw >> 3) + (lin >> 3);
   const int RT = (M + TR - 1) / TR, rt = wi % RT, bx = wi / RT, row0 = rt * TR;
