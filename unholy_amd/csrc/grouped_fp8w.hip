@@ -140,8 +140,8 @@ __global__ __launch_bounds__(64 * GV_W) void grouped_fp8w_gemv_kernel(const bf16
 // - the tile's activation rows go through a 2-slot LDS ring of chunks (32 rows x 1,024 bf16, 64 KB) by direct
 //   global -> LDS loads; piece p (16 bytes) of row r sits at p ^ (r & 15), so the 16 rows of an MFMA operand pass
 //   cover the 64 banks once;
-// - the weights dequantize with the block scale folded in (exact); the 8 parts are added in LDS in part order by all
-//   16 waves;
+// - the weights dequantize with the block scale folded in (exact); the 8 parts (16 in the 32-column form) are added
+//   in LDS in part order by all 16 waves;
 // - work item wi = column block x row tiles + row tile; XCD x takes the x-th eighth of the items, so the row tiles of
 //   a column block share one L2 (the second reads the weights from it) and a group's activation rows sit in one L2.
 // Against the GEMV (one 16-column tile per workgroup, every workgroup reading its rows from L2): the activation rows
