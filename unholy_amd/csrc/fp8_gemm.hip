@@ -286,12 +286,27 @@ __global__ __launch_bounds__(64 * FV_WAVES) void fp8_gemv_kernel(Fp8GemmArgs a, 
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   const int mlive = (M + 15) / 16;  // row tiles with rows (uniform)
+  // The chunk's weights and their scales (every load issued before the first use; steps past the range clamped).
+  v4i b[FV_CHUNK][2];
+  float swv[FV_CHUNK];
+  const auto load_weights = [&](int kc) {
+#pragma unroll
+    for (int u = 0; u < FV_CHUNK; ++u) {
+      const int kb = min(kc + u, b1 - 1);
+      b[u][0] = *reinterpret_cast<gptr<v4i>>(as_global(wrow + kb * 128));
+      b[u][1] = *reinterpret_cast<gptr<v4i>>(as_global(wrow + kb * 128 + 16));
+      swv[u] = F32S ? a.sw32[size_t(nb) * KS + kb] : e8m0_to_f32(a.sw8[size_t(nb) * KS + kb]);
+    }
+  };
   if constexpr (XQ) {  // every wave: quantize the M rows into LDS before any wave reads them
     const int nbk = KS * 16, items = M * nbk;  // 8 values per item
     float* const sl = reinterpret_cast<float*>(xq_lds + size_t(M) * K);
-    for (int base = 0; base < items; base += 64 * FV_WAVES) {  // uniform bound: 16-thread groups stay whole
+    const auto load_item = [&](int base) {
       const int it = min(base + tid, items - 1), r = it / nbk, rem = it % nbk, bk = rem >> 4, l = rem & 15;
-      const uint4 raw = *reinterpret_cast<const uint4*>(a.xa + size_t(r) * a.ldx + bk * 128 + 8 * l);
+      return *reinterpret_cast<const uint4*>(a.xa + size_t(r) * a.ldx + bk * 128 + 8 * l);
+    };
+    const auto quant_item = [&](int base, const uint4 raw) {
+      const int it = min(base + tid, items - 1), r = it / nbk, rem = it % nbk, bk = rem >> 4, l = rem & 15;
       const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
       float v[8], am = 0.0f;
 #pragma unroll
@@ -302,29 +317,35 @@ __global__ __launch_bounds__(64 * FV_WAVES) void fp8_gemv_kernel(Fp8GemmArgs a, 
 #pragma unroll
       for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
       am = row16_max(am);
-      if (base + tid >= items) continue;
+      if (base + tid >= items) return;
       const float sc = fmaxf(am, 1e-4f) * (1.0f / 448.0f);
       uint32_t c0, c1;
       fp8_codes8(v, sc, c0, c1);
       *reinterpret_cast<uint2*>(xq_lds + size_t(r) * K + bk * 128 + 8 * l) = make_uint2(c0, c1);
       if (l == 0) sl[r * KS + bk] = sc;
-    }
+    };
+    // The first pass's row loads, then the first chunk's weights, then the quantization: it waits for the row loads
+    // only, and the weights' latency runs under it.
+    // (A wave with no K blocks loads block KS - 1 and never uses it: an unconditional load keeps the wait exact.)
+    const uint4 raw0 = load_item(0);
+    load_weights(b0);
+    quant_item(0, raw0);
+    for (int base = 64 * FV_WAVES; base < items; base += 64 * FV_WAVES)  // uniform bound: 16-thread groups stay whole
+      quant_item(base, load_item(base));
     __syncthreads();
   }
   for (int kc = b0; kc < b1; kc += FV_CHUNK) {
     // Every load of the chunk is issued before the first use, unconditionally (steps past the range and rows past M
     // are clamped, their products discarded): the weights, the activation rows and the scales, so the chunk waits
     // for one memory latency, not one per step.
-    v4i b[FV_CHUNK][2], aq[FV_CHUNK][MT][2];
-    float swv[FV_CHUNK], sav[FV_CHUNK][MT];
+    v4i aq[FV_CHUNK][MT][2];
+    float sav[FV_CHUNK][MT];
     constexpr bool kRowScales = F32S && MT == 1;  // the fp32 row scales of C's rows too (registers permitting)
     float sa32v[FV_CHUNK][4];
+    if (!XQ || kc != b0) load_weights(kc);
 #pragma unroll
     for (int u = 0; u < FV_CHUNK; ++u) {
       const int kb = min(kc + u, b1 - 1);
-      b[u][0] = *reinterpret_cast<gptr<v4i>>(as_global(wrow + kb * 128));
-      b[u][1] = *reinterpret_cast<gptr<v4i>>(as_global(wrow + kb * 128 + 16));
-      swv[u] = F32S ? a.sw32[size_t(nb) * KS + kb] : e8m0_to_f32(a.sw8[size_t(nb) * KS + kb]);
       if constexpr (XQ) {
         sav[u][0] = 1.0f;
       } else {
