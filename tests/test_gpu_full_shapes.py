@@ -10,6 +10,8 @@ the sizes the reference's own kernel tests run at (tools/kernel_test/mx_moe.hip:
 - configs[4] fp8 dense 4096 x 4096 at M = 64 and M = 4096 (fp32 scales), against the oracle (M = 4096: a sample of
   512 rows, the first and last included).
 - The DSV4 W8A8 projection shapes (e8m0 scales) at M = 1 / 8 / 64 through every W8A8 entry point.
+- DSV4 projection shapes with fp32 scales through the row-tile kernel (M = 64, and 200 for wo_b): the widest N, the
+  longest K, K = 1,024.
 Weights are made on the device (splitmix64 bytes, e8m0 scales in [119, 125]) and the touched experts copied back for
 the oracle."""
 import numpy as np
@@ -280,3 +282,33 @@ def test_dsv4_w8a8_shapes(name, N, Kd):
             assert mr <= 1e-2, fn
         for o in outs[1:]:
             assert np.array_equal(o, outs[0])
+
+
+# fp32-scale fp8 dense at DSV4 projection shapes through the row-tile kernel (16 < M <= 256): the widest N (head_fp8,
+# 4,040 column blocks), the longest K (wo_b, four 2,048-input chunks; also at M = 200, seven row tiles) and K = 1,024
+# (wq_b: one chunk with 8 of the 16 K parts busy).
+@pytest.mark.parametrize("name,N,Kd,M", [("wq_b", 32768, 1024, 64), ("wo_b", 4096, 8192, 64), ("wo_b", 4096, 8192, 200),
+                                         ("sw2", 4096, 2048, 64), ("head_fp8", 129280, 4096, 64)],
+                         ids=["wq_b-64", "wo_b-64", "wo_b-200", "sw2-64", "head_fp8-64"])
+def test_dsv4_fp8_f32s_row_tiles(name, N, Kd, M):
+    rng = np.random.default_rng(N + Kd + M)
+    x = randn_bf16(rng, (M, Kd))
+    q, sa = DeviceBuffer(M * Kd), DeviceBuffer(M * (Kd // 128) * 4)
+    call("uh_act_quant_fp8_f32s", dev(x), Kd, q, sa, M, Kd, 128, None)
+    # codes filled on the device (finite e4m3 only), fp32 block scales of the size act_quant would give them
+    wq = DeviceBuffer(N * Kd)
+    fill_random_bytes(wq, N * Kd, N * 5 + Kd, 0, 255)
+    wh = wq.download((N, Kd), np.uint8)
+    wh[(wh & 0x7F) == 0x7F] &= 0xFE
+    wq.upload(wh)
+    sw = (rng.random(((N + 127) // 128, Kd // 128), dtype=np.float32) * np.float32(1e-4) + np.float32(2e-5))
+    ws = dev(sw)
+    c = DeviceBuffer(M * N * 2)
+    call("uh_gemm_fp8_f32s", q, sa, wq, ws, c, N, M, N, Kd, None)
+    rows = np.arange(M) if N * Kd <= (1 << 26) else np.unique(np.concatenate([[0, M - 1], rng.choice(M, 14, replace=False)]))
+    qh, sah = q.download((M, Kd), np.uint8)[rows], sa.download((M, Kd // 128), np.float32)[rows]
+    ref16, _ = oracle.gemm_w8a8(qh, sah, wh, sw, threads=16)
+    got = from_bf16(c.download((M, N), np.uint16)[rows])
+    mr = max_rel(got, from_bf16(ref16))
+    print(f"{name} fp8 f32s M={M} ({len(rows)} rows checked): max_rel {mr:.3e}")
+    assert mr <= 1e-2
