@@ -77,7 +77,7 @@ def test_hazard_model_catches_an_early_read():
 
 
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not available")
-@pytest.mark.parametrize("src,name,count", [("fp8_gemm.hip", "fp8_rows_kernel", 1),
+@pytest.mark.parametrize("src,name,count", [("fp8_gemm.hip", "fp8_rows_kernel", 2),
                                             ("grouped_fp8w.hip", "grouped_fp8w_rows_kernel", 2)])
 def test_counted_loads_have_no_early_use(src, name, count, tmp_path):
     kernels = _kernel_asm(src, name, tmp_path)

@@ -23,10 +23,12 @@ def _weights_f32s(rng, N, K):
 
 
 # 16 < M <= 256 with N % 32 == 0 takes the row-tile kernel: one to four 2,048-input chunks, ragged last chunks (K = 640,
-# 2,176), one 32-column block (N = 32), a weight-scale row shared by fewer than 128 columns (N = 96), 1 to 8 row tiles.
+# 2,176), one 32-column block (N = 32), a weight-scale row shared by fewer than 128 columns (N = 96), 1 to 8 row tiles;
+# (200, 4096, 1024): the 64-column form over 7 row tiles.
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (5, 384, 1024), (64, 512, 1024), (300, 256, 512), (3, 136, 384),
                                    (1000, 768, 1024), (129, 200, 256), (17, 32, 640), (33, 1024, 8192), (64, 96, 6144),
-                                   (48, 256, 2176), (40, 200, 512), (200, 128, 1024), (256, 96, 2176), (129, 64, 384)])
+                                   (48, 256, 2176), (40, 200, 512), (200, 128, 1024), (256, 96, 2176), (129, 64, 384),
+                                   (200, 4096, 1024)])
 def test_fp8_f32_scales(M, N, K):
     """BASELINE config 4 form: A bf16 -> e4m3 per 1x128 with fp32 scales; W e4m3 with fp32 128x128 scales."""
     rng = np.random.default_rng(M + N)
@@ -75,8 +77,10 @@ def test_fp8_f32s_fused_quant_is_bit_identical(M, N, K, pad):
         call("uh_gemm_fp8_f32s_x", dx, ldx, dwq, dws, c, N, 17, N, K, None)
 
 
+# (40, 16384, 2048) and (48, 20480, 1152) leave >= 512 workgroups of 64 columns: the wide form (two chunks, the second
+# ragged at K = 1152).
 @pytest.mark.parametrize("M,N,K,pad", [(17, 512, 1024, 0), (64, 1024, 2048, 8), (40, 4096, 1024, 0), (64, 128, 256, 0),
-                                       (33, 640, 4096, 64), (40, 16384, 2048, 0)])
+                                       (33, 640, 4096, 64), (40, 16384, 2048, 0), (48, 20480, 1152, 0)])
 def test_fp8_f32s_row_tiles_ldc(M, N, K, pad):
     """gemm_fp8_f32s at 16 < M <= 64 (the row-tile kernel) with a C row stride wider than N: against the oracle within
     the bf16 bar, and C columns past N untouched."""

@@ -472,46 +472,61 @@ void launch_fp8_gemv_t(const Fp8GemmArgs& a, hipStream_t st, const Fp8Parts& pp)
 // than the split gains.
 // Up to FR_MAXM rows (8 row tiles): at 4096 x 4096 the row tiles ran 22-43 us per step for 65 <= M <= 256 against
 // 47-53 us for the 128 x 128 tiled GEMM (too few workgroups there), which wins from M = 384 on (53 against 62 us).
-constexpr int FR_KR = 2048, FR_SLOT = 32 * FR_KR, FR_MAXCH = 4, FR_LS = 17, FR_MAXM = 256;
+constexpr int FR_MAXCH = 4, FR_MAXM = 256;
 
+// CH column halves of 32 (workgroup width 32 CH); KP = 16 / CH K parts; chunks of KR = 128 KP inputs; NA direct loads
+// per wave per chunk (32 rows x KR codes in 1 KB loads over 16 waves). CH = 2 halves the workgroups of a wide, short
+// matrix (N / 64 column blocks), each wave then adding two accumulator elements in the reduction.
+template <int CH>
+struct Fp8Rows {
+  static constexpr int KP = 16 / CH, KR = 128 * KP, SLOT = 32 * KR, NA = SLOT / 1024 / 16, W = 32 * CH;
+  static constexpr int LS = CH == 2 ? 18 : 17;  // reduction lane stride (floats)
+  static size_t lds(int K) {
+    return std::max(2 * size_t(SLOT) + size_t(32) * (K / 128) * 4, size_t(16) * 64 * LS * 4);
+  }
+};
+
+template <int CH>
 __global__ __launch_bounds__(1024) void fp8_rows_kernel(Fp8GemmArgs p) {
   using namespace pipe;
+  using T = Fp8Rows<CH>;
+  constexpr int KP = T::KP, KR = T::KR, SLOT = T::SLOT, NA = T::NA;
   extern __shared__ __align__(16) uint8_t smem[];
-  const int M = p.M, N = p.N, K = p.K, KS = K / 128, nch = (KS + 15) / 16;  // nch <= FR_MAXCH
+  const int M = p.M, N = p.N, K = p.K, KS = K / 128, nch = (KS + KP - 1) / KP;  // nch <= FR_MAXCH
   if (nch < 1) return;  // (the host requires K >= 128) no load is ever left pending past the chunk loop
   const int nw = gridDim.x, lin = blockIdx.x;
   const int wi = nw % 8 ? lin : (lin & 7) * (nw >> 3) + (lin >> 3);
   const int RT = (M + 31) / 32, rt = wi % RT, bx = wi / RT, row0 = rt * 32;
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
-  const int kh = __builtin_amdgcn_readfirstlane(tid >> 6);  // K part = wave
-  const int col0 = bx * 32, n = col0 + l32;
-  float* const ssa = reinterpret_cast<float*>(smem + 2 * FR_SLOT);  // row scales [32][KS]
-  const uint8_t* wld = p.w + size_t(col0 + (lane & 15)) * K + (lane >> 4) * 16;
-  const float* swrow = p.sw32 + size_t(col0 / 128) * KS;  // 32 columns lie in one 128-row block
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), chh = wave % CH, kh = wave / CH;  // column half, K part
+  const int col0 = bx * T::W, n = col0 + chh * 32 + l32;
+  float* const ssa = reinterpret_cast<float*>(smem + 2 * SLOT);  // row scales [32][KS]
+  const uint8_t* wld = p.w + size_t(col0 + chh * 32 + (lane & 15)) * K + (lane >> 4) * 16;
+  const float* swrow = p.sw32 + size_t((col0 + chh * 32) / 128) * KS;  // 32 columns lie in one 128-row block
   const uint32_t lds0 = lds_addr(smem);
-  uint32_t rowoff[4];
-  int pin[4];
+  uint32_t rowoff[NA];
+  int pin[NA];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int slot = (kh * 4 + i) * 64 + lane, r = slot / (FR_KR / 16);
+  for (int i = 0; i < NA; ++i) {
+    const int slot = (wave * NA + i) * 64 + lane, r = slot / (KR / 16);
     rowoff[i] = uint32_t(min(row0 + r, M - 1)) * uint32_t(K);
-    pin[i] = ((slot % (FR_KR / 16)) ^ (r & 15)) * 16;
+    pin[i] = ((slot % (KR / 16)) ^ (r & 15)) * 16;
   }
   const auto issue_a = [&](int ch) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dma16(p.a, rowoff[i] + uint32_t(min(ch * FR_KR + pin[i], K - 16)),
-            lds0 + uint32_t((ch & 1) * FR_SLOT + (kh * 4 + i) * 1024));
+    for (int i = 0; i < NA; ++i)
+      dma16(p.a, rowoff[i] + uint32_t(min(ch * KR + pin[i], K - 16)),
+            lds0 + uint32_t((ch & 1) * SLOT + (wave * NA + i) * 1024));
   };
   v4i b[FR_MAXCH][4];
   const auto load_w = [&](int u) {
-    const uint8_t* q = wld + min(u * 16 + kh, KS - 1) * 128;
+    const uint8_t* q = wld + min(u * KP + kh, KS - 1) * 128;
 #pragma unroll
     for (int x = 0; x < 4; ++x) b[u][x] = vload16(q + (x >> 1) * 16 * K + (x & 1) * 64);
   };
   // Issue order: the scales (lane u < nch: the wave's weight scale of chunk u; thread t: row scales t, t + 1024 of
   // the tile), W0 A0 W1 A1 W2 W3, then A(c + 2).
-  uint32_t swv = vload_u32(swrow + min(min(lane, FR_MAXCH - 1) * 16 + kh, KS - 1));
+  uint32_t swv = vload_u32(swrow + min(min(lane, FR_MAXCH - 1) * KP + kh, KS - 1));
   uint32_t sav[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -532,16 +547,21 @@ __global__ __launch_bounds__(1024) void fp8_rows_kernel(Fp8GemmArgs p) {
   for (int ch = 0; ch < FR_MAXCH; ++ch) {
     if (ch >= nch) break;
     // Chunk ch, its weights and the scales have landed when only the loads issued after A(ch) are pending (4 per
-    // group): ch = 0: W1 A1 W2 W3; ch = 1: W2 W3 A2; ch = 2: A3; each where it exists.
-    const int later = ch == 0 ? (1 < nch) * 2 + (2 < nch) + (3 < nch)
-                      : ch == 1 ? (2 < nch) * 2 + (3 < nch)
-                      : ch == 2 ? (3 < nch)
+    // weight group, NA per activation group): ch = 0: W1 A1 W2 W3; ch = 1: W2 W3 A2; ch = 2: A3; each where it
+    // exists.
+    const int later = ch == 0   ? 4 * ((1 < nch) + (2 < nch) + (3 < nch)) + NA * (1 < nch)
+                      : ch == 1 ? 4 * ((2 < nch) + (3 < nch)) + NA * (2 < nch)
+                      : ch == 2 ? NA * (3 < nch)
                                 : 0;
     switch (later) {
-      case 4: wait_vm<16>(); break;
-      case 3: wait_vm<12>(); break;
-      case 2: wait_vm<8>(); break;
-      case 1: wait_vm<4>(); break;
+      case 16: wait_vm<16>(); break;
+      case 14: wait_vm<14>(); break;
+      case 12: wait_vm<12>(); break;
+      case 10: wait_vm<10>(); break;
+      case 8: wait_vm<8>(); break;
+      case 6: wait_vm<6>(); break;
+      case 4: wait_vm<4>(); break;
+      case 2: wait_vm<2>(); break;
       default: wait_vm<0>();
     }
     vlanded(b[ch]);
@@ -554,9 +574,9 @@ __global__ __launch_bounds__(1024) void fp8_rows_kernel(Fp8GemmArgs p) {
         if (tid + 1024 * j < 32 * KS) ssa[tid + 1024 * j] = __uint_as_float(sav[j]);
     }
     __syncthreads();  // every wave's part of chunk ch (and the row scales) has landed
-    const int kb = ch * 16 + kh;
+    const int kb = ch * KP + kh;
     if (kb < KS) {
-      const uint8_t* sl = smem + (ch & 1) * FR_SLOT;
+      const uint8_t* sl = smem + (ch & 1) * SLOT;
       const float sw = __uint_as_float(uint32_t(__builtin_amdgcn_readlane(int(swv), ch)));
 #pragma unroll
       for (int x = 0; x < 2; ++x)
@@ -572,7 +592,7 @@ __global__ __launch_bounds__(1024) void fp8_rows_kernel(Fp8GemmArgs p) {
 #pragma unroll
       for (int x = 0; x < 4; ++x) {
         const int pc = (kh * 8 + 2 * h + (x >> 1) + 4 * (x & 1)) ^ (r & 15);
-        const v4i av = *reinterpret_cast<const v4i*>(sl + r * FR_KR + pc * 16);
+        const v4i av = *reinterpret_cast<const v4i*>(sl + r * KR + pc * 16);
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const bf16x8 af = fp8x8_to_bf16(uint32_t(av[2 * e]), uint32_t(av[2 * e + 1]), 1.0f);
@@ -589,34 +609,61 @@ __global__ __launch_bounds__(1024) void fp8_rows_kernel(Fp8GemmArgs p) {
       issue_a(ch + 2);
     }
   }
-  // The 16 parts added in part order through LDS: wave p adds element p of every lane (17-float lane stride: the
-  // reads of a wave cover the 64 banks once).
+  // The KP parts added in part order through LDS: wave (chh, kh) adds elements CH kh .. CH kh + CH - 1 of its column
+  // half's lanes (lane stride 17 floats for 4-byte reads, 18 for 8-byte ones: a half-wave's reads cover the 64 banks
+  // once).
   __syncthreads();
   float* red = reinterpret_cast<float*>(smem);
+  float* mine = red + ((kh * CH + chh) * 64 + lane) * T::LS;
+  if constexpr (CH == 2) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) red[(kh * 64 + lane) * FR_LS + i] = acc[i];
+    for (int i = 0; i < 16; i += 2) *reinterpret_cast<float2*>(mine + i) = make_float2(acc[i], acc[i + 1]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mine[i] = acc[i];
+  }
   __syncthreads();
-  float sum = red[lane * FR_LS + kh];
+  float sum[CH];
 #pragma unroll
-  for (int q = 1; q < 16; ++q) sum += red[(q * 64 + lane) * FR_LS + kh];
-  const int row = row0 + 8 * (kh / 4) + 4 * h + (kh % 4);
-  if (row < M) p.c[size_t(row) * p.ldc + n] = f32_to_bf16(sum);
+  for (int e = 0; e < CH; ++e) sum[e] = red[(chh * 64 + lane) * T::LS + CH * kh + e];
+#pragma unroll
+  for (int q = 1; q < KP; ++q)
+#pragma unroll
+    for (int e = 0; e < CH; ++e) sum[e] += red[((q * CH + chh) * 64 + lane) * T::LS + CH * kh + e];
+  // Element i of lane (l32, h) is row 8 (i / 4) + 4 h + i % 4 of the tile.
+#pragma unroll
+  for (int e = 0; e < CH; ++e) {
+    const int i = CH * kh + e, row = row0 + 8 * (i / 4) + 4 * h + (i % 4);
+    if (row < M) p.c[size_t(row) * p.ldc + n] = f32_to_bf16(sum[e]);
+  }
 }
 }  // namespace
 
+// The wide form (CH = 2) where it still gives every CU a workgroup (N / 64 column blocks x row tiles >= 256) and K fits
+// its four 1,024-input chunks; else 32-column workgroups. Measured (us per call, wide / narrow): 32768 x 1024 M = 64
+// 26.8 / 43.1, 8192 x 1024 M = 64 7.4 / 11.6, 4096 x 4096 M = 128 17.2 / 20.3, 129280 x 4096 M = 32 150 / 174; with
+// 128 workgroups the wide form loses (4096 x 4096 M = 64: 16.9 / 11.8).
+static bool fp8_rows_wide(const Fp8GemmArgs& a) {
+  return a.N % 64 == 0 && a.K <= FR_MAXCH * Fp8Rows<2>::KR && size_t(a.N / 64) * ((a.M + 31) / 32) >= 256;
+}
 bool fp8_rows_fits(const Fp8GemmArgs& a) {
   return a.sa32 && a.sw32 && a.M > 16 && a.M <= FR_MAXM && a.N % 32 == 0 && a.K % 128 == 0 && a.K >= 128 &&
-         a.K <= FR_MAXCH * FR_KR && size_t(a.M) * a.K < (size_t(1) << 32);
+         a.K <= FR_MAXCH * Fp8Rows<1>::KR && size_t(a.M) * a.K < (size_t(1) << 32);
+}
+template <int CH>
+static void launch_fp8_rows_t(const Fp8GemmArgs& a, hipStream_t st) {
+  const size_t lds = Fp8Rows<CH>::lds(a.K);
+  auto* kern = &fp8_rows_kernel<CH>;
+  UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               int(lds)));
+  kern<<<dim3(unsigned(a.N / Fp8Rows<CH>::W * ((a.M + 31) / 32))), 1024, lds, st>>>(a);
+  UH_CHECK_LAUNCH();
 }
 void launch_fp8_rows(const Fp8GemmArgs& a, hipStream_t st) {
   if (!fp8_rows_fits(a)) throw std::runtime_error("fp8 rows: shape");
   if (!a.a || !a.w || !a.c) throw std::runtime_error("fp8 gemm: null operand");
-  const size_t lds = 2 * size_t(FR_SLOT) + size_t(32) * (a.K / 128) * 4;
-  auto* kern = &fp8_rows_kernel;
-  UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                               int(lds)));
-  kern<<<dim3(unsigned(a.N / 32 * ((a.M + 31) / 32))), 1024, lds, st>>>(a);
-  UH_CHECK_LAUNCH();
+  if (fp8_rows_wide(a)) launch_fp8_rows_t<2>(a, st);
+  else launch_fp8_rows_t<1>(a, st);
 }
 
 void launch_fp8_skinny(const Fp8GemmArgs& a0, hipStream_t st) {
