@@ -639,12 +639,16 @@ __global__ __launch_bounds__(1024) void fp8_rows_kernel(Fp8GemmArgs p) {
 }
 }  // namespace
 
-// The wide form (CH = 2) where it still gives every CU a workgroup (N / 64 column blocks x row tiles >= 256) and K fits
-// its four 1,024-input chunks; else 32-column workgroups. Measured (us per call, wide / narrow): 32768 x 1024 M = 64
-// 26.8 / 43.1, 8192 x 1024 M = 64 7.4 / 11.6, 4096 x 4096 M = 128 17.2 / 20.3, 129280 x 4096 M = 32 150 / 174; with
-// 128 workgroups the wide form loses (4096 x 4096 M = 64: 16.9 / 11.8).
+// The wide form (CH = 2, K <= 4096) where its rounds of workgroups (256 CUs, one workgroup each) cost less: a wide
+// workgroup runs ~1.7x as long as a narrow one (~1.25x at K <= 1024, where half the narrow form's K parts idle).
+// Measured (us per call, wide / narrow): 32768 x 1024 M = 64 26.8 / 43.1, 8192 x 1024 M = 64 7.4 / 11.6, 4096 x 4096
+// M = 128 17.2 / 20.3, 129280 x 4096 M = 32 150 / 174; M = 64 at 4096 x 4096 (128 wide workgroups) 16.9 / 11.8, and
+// M = 160 (320 against 640 workgroups) 34.6 / 31.8 per step.
 static bool fp8_rows_wide(const Fp8GemmArgs& a) {
-  return a.N % 64 == 0 && a.K <= FR_MAXCH * Fp8Rows<2>::KR && size_t(a.N / 64) * ((a.M + 31) / 32) >= 256;
+  if (a.N % 64 || a.K > FR_MAXCH * Fp8Rows<2>::KR) return false;
+  const size_t rt = size_t(a.M + 31) / 32, nn = size_t(a.N / 32) * rt, nw = size_t(a.N / 64) * rt;
+  const double f = a.K <= 1024 ? 1.25 : 1.7;
+  return double((nw + 255) / 256) * f < double((nn + 255) / 256);
 }
 bool fp8_rows_fits(const Fp8GemmArgs& a) {
   return a.sa32 && a.sw32 && a.M > 16 && a.M <= FR_MAXM && a.N % 32 == 0 && a.K % 128 == 0 && a.K >= 128 &&
