@@ -15,9 +15,9 @@ void gemm_w8a8_wmma(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const
                     int M, int N, int K, hipStream_t st);
 void gemm_force_skinny(int on);  // the reference's test override; kernel choice here is by shape only (no-op)
 // Ref gemm_wmma.hpp:24-26: grouped "mgk,grk->mgr" with fp8 weights x 128x128 e8m0 scales (dequantized to bf16,
-// exact): a bf16 [M, G, K], w e4m3 [G R, K], sw [ceil(G R / 128), K / 128], c bf16 [M, G, R]; K % 128 == 0. M <= 160
-// takes the row-tile kernel (M <= 16: R % 32 == 0, K <= 8192; else R % 64 == 0, K <= 4096) or else the GEMV
-// (R % 16 == 0), larger M the tiled MFMA GEMM (R % 128 == 0); other shapes the reference-order kernel.
+// exact): a bf16 [M, G, K], w e4m3 [G R, K], sw [ceil(G R / 128), K / 128], c bf16 [M, G, R]; K % 128 == 0. M <= 384
+// takes the row-tile kernel (M <= 16: R % 32 == 0, K <= 8192; else R % 64 == 0, K <= 4096), or else up to M = 160 the
+// GEMV (R % 16 == 0); larger M the tiled MFMA GEMM (R % 128 == 0); other shapes the reference-order kernel.
 void gemm_grouped_fp8w_wmma(const bf16* a, const uint8_t* w, const uint8_t* sw, bf16* c, int M, int G, int R, int K,
                             hipStream_t st);
 

@@ -7,7 +7,7 @@
 // Three entry points, as the reference has them:
 //   gemm_grouped_fp8w       the reference order (ref_gemm.hip:116-125, :198-202 at G = K: one fp32 fmaf chain over k
 //                           in order), a thread per output: bit-exact against the CPU oracle, not a fast path;
-//   gemm_grouped_fp8w_wmma  the fast path: the row-tile kernel for M <= 160 (M <= 16: R % 32 == 0, K <= 8192;
+//   gemm_grouped_fp8w_wmma  the fast path: the row-tile kernel for M <= 384 (M <= 16: R % 32 == 0, K <= 8192;
 //                           else R % 64 == 0, K <= 4096), the GEMV for other shapes up to M = 160, else the tiled
 //                           MFMA GEMM;
 //   gemv_grouped_fp8w       M <= 32 as the fast path, optionally followed by act_quant_fp8 of its outputs (GemvQuant).
@@ -16,7 +16,7 @@
 // its 8 waves splitting K in 128-input blocks, every load of a chunk issued before its first use; bf16 MFMA
 // 16x16x32 on the activations as they are and the weights dequantized with the block scale folded in; the 8
 // partial tiles added in LDS in wave order.
-// Row tiles (M <= 160): a workgroup per 64 columns x 32 rows (M <= 16: 32 columns x 16 rows) over the whole of K, the
+// Row tiles (M <= 384): a workgroup per 64 columns x 32 rows (M <= 16: 32 columns x 16 rows) over the whole of K, the
 // activation rows staged once per workgroup in LDS (the GEMV reads them once per 16 columns), the weights held in
 // registers up to four chunks ahead.
 // GEMM (bound: MFMA at M = 4096): 128-row tiles of one group, 4 waves, 64-input stages in an LDS ring filled by direct
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(64 * GV_W) void grouped_fp8w_gemv_kernel(const bf16
   }
 }
 
-// ---- row tiles, M <= 160 -----------------------------------------------------------------------------------------
+// ---- row tiles, M <= 384 -----------------------------------------------------------------------------------------
 // A workgroup per 64 columns (one group: R % 64 == 0) x 32 rows, the whole of K (<= 4,096), bf16 C written directly
 // (M <= 16: 32 columns x 16 rows, K <= 8,192, 16 K parts of 2,048-input chunks; the parameters below):
 // - 16 waves = 2 column halves x 8 K parts, 32 x 32 output tiles (bf16 MFMA 32x32x16); part p takes block p of every
@@ -290,9 +290,12 @@ __global__ __launch_bounds__(1024) void grouped_fp8w_rows_kernel(const bf16* a, 
 }
 
 // M <= 16: 32-column workgroups of 16 staged rows (256 workgroups at the DSV4 shape, every wave's weights in flight at
-// once); 16 < M <= 160: 64-column workgroups of 32-row tiles.
+// once); 16 < M <= GR_MAXM: 64-column workgroups of 32-row tiles. At the DSV4 shape the row tiles ran 44 / 58 / 86 us
+// at M = 192 / 256 / 384 against 100-106 us for the tiled GEMM (128 workgroups or fewer there), which wins from
+// M = 512 on (107 against 116 us).
+constexpr int GR_MAXM = 384;
 bool rows_fits(int M, int G, int R, int K) {
-  if (M < 1 || M > 160 || size_t(M) * G * K * 2 >= (size_t(1) << 32)) return false;
+  if (M < 1 || M > GR_MAXM || size_t(M) * G * K * 2 >= (size_t(1) << 32)) return false;
   return M <= 16 ? R % 32 == 0 && K <= GR_MAXCH * GroupedRows<1, 16>::KR
                  : R % 64 == 0 && K <= GR_MAXCH * GroupedRows<2, 32>::KR;
 }
