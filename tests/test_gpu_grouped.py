@@ -39,14 +39,15 @@ def test_grouped_fp8w_reference_order_bit_exact(M, G, R, K):
 # M <= 16: the row-tile kernel's 32-column form (R % 32 == 0, K <= 8192: one to four 2,048-input chunks, ragged K);
 # 16 < M <= 384: its 64-column form (R % 64 == 0, K <= 4096: one to four 1,024-input chunks, a ragged last chunk at
 # K = 640 and 1,152, 1 to 12 row tiles, the DSV4 shape); other shapes up to M = 160 the GEMV in 32-row chunks (R = 200
-# is the reference-order kernel; K = 9,216 the GEMV); larger M: the tiled GEMM (256-column tiles for R % 256 == 0,
-# else 128-column ones for R % 128 == 0: M = 385, 400, 520).
+# is the reference-order kernel; K = 9,216 the GEMV); larger M: the tiled GEMM (128-column tiles, M = 385, 400, 520;
+# 256-column ones for R % 256 == 0 once they make more than 256 workgroups: M = 400, G R = 16,896).
 @pytest.mark.parametrize("M,G,R,K", [(1, 8, 1024, 4096), (16, 2, 512, 1024), (32, 3, 256, 640), (7, 2, 200, 256),
                                      (33, 2, 256, 512), (100, 2, 256, 512), (200, 3, 128, 384), (300, 2, 384, 1024),
                                      (257, 2, 256, 512), (200, 3, 512, 384), (65, 2, 200, 256), (64, 8, 1024, 4096),
                                      (17, 2, 128, 768), (160, 2, 192, 3072), (48, 3, 64, 1152), (95, 1, 64, 9216),
                                      (4, 3, 96, 640), (16, 1, 32, 8192), (9, 2, 160, 5120), (1, 2, 64, 128),
-                                     (384, 1, 64, 256), (385, 1, 128, 384), (400, 2, 256, 512), (520, 2, 384, 1024)])
+                                     (384, 1, 64, 256), (385, 1, 128, 384), (400, 2, 256, 512), (520, 2, 384, 1024),
+                                     (400, 1, 16896, 128)])
 def test_grouped_fp8w_fast_path(M, G, R, K):
     rng = np.random.default_rng(M * 7 + G * R + K)
     a, w, sw = _case(rng, M, G, R, K)
