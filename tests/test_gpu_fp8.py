@@ -101,7 +101,10 @@ def test_fp8_f32s_row_tiles_ldc(M, N, K, pad):
     assert mr <= 1e-2
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (8, 1024, 512), (33, 256, 1024), (200, 512, 512), (17, 200, 640), (1000, 768, 1024)])
+# M > 64 takes the tiled GEMM: 64-column tiles while 128-column ones would make fewer than 256 workgroups
+# (M = 200, 1000), else 128 columns (M = 1024, N = 4096).
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (8, 1024, 512), (33, 256, 1024), (200, 512, 512), (17, 200, 640),
+                                   (1000, 768, 1024), (1024, 4096, 256)])
 def test_fp8_e8m0_scales(M, N, K):
     """The reference's W8A8 contract (gemm_w8a8 / gemv_w8a8 / gemm_w8a8_wmma): e8m0 scales on both sides."""
     rng = np.random.default_rng(M * 3 + K)

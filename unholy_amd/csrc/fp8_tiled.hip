@@ -2,10 +2,11 @@
 // gemm_w8a8, the reference's ref_gemm.hip:130-137 / gemm_wmma.hip:51-183; fp32 for the 1x128 / 128x128 format of
 // tools/ref/oracle/kernel.py:81-118).
 //
-// Workgroup = 256 threads, 128 rows x 128 columns; wave w owns rows 64 (w & 1) .. + 63 and columns 64 (w >> 1) .. + 63.
+// Workgroup = 256 threads, 128 rows x TN columns (TN = 128, or 64 while 128-column tiles would make fewer than 256
+// workgroups); wave w owns rows 64 (w & 1) .. + 63 and columns TN / 2 (w >> 1) .. + TN / 2 - 1.
 // Per 128-input stage a 2-slot LDS ring holds
 //   A 16 KB: row r's 16-byte piece p at slot r * 8 + (p ^ lds_swz(r)),
-//   B 16 KB: column n's 16-byte piece p at slot n * 8 + (p ^ lds_swz(n)) (W is row-major like A),
+//   B TN x 128 B: column n's 16-byte piece p at slot n * 8 + (p ^ lds_swz(n)) (W is row-major like A),
 //   S 512 B: fp32 activation scales of the 128 rows (fp32 form only, one gathered dword per row),
 // filled by direct global -> LDS loads: stage s + 1 is issued right after stage s's barrier. A workgroup stays under
 // 80 KB of LDS, so two share a CU and one's barriers and operand waits overlap the other's MFMAs.
@@ -26,22 +27,28 @@ using namespace pipe;
 
 namespace {
 
-constexpr int FT_S = 2, FT_A = 128 * 128, FT_B = 128 * 128, FT_SA = 128 * 4;
-constexpr int FT_STAGE = FT_A + FT_B + FT_SA;
-constexpr int FT_RING = FT_S * FT_STAGE;
-constexpr int FT_LDC = 128 + 8;
-static_assert(128 * FT_LDC * 2 <= FT_RING, "the bf16 C tile reuses the ring");
-size_t tiled_lds(int K, bool f32s) { return size_t(FT_RING) + size_t(4 + (f32s ? 0 : 128)) * (K / 128); }
+// TN output columns per workgroup: 128, or 64 where 128-column tiles would leave too few workgroups (each wave then
+// owns 64 rows x 32 columns).
+template <int TN>
+struct FpTile {
+  static constexpr int S = 2, A = 128 * 128, B = TN * 128, SA = 128 * 4, STAGE = A + B + SA, RING = S * STAGE;
+  static constexpr int LDC = TN + 8, CB = TN / 64, BL = TN / 32;  // column blocks per wave, B loads per wave
+  static_assert(128 * LDC * 2 <= RING, "the bf16 C tile reuses the ring");
+  static size_t lds(int K, bool f32s) { return size_t(RING) + size_t(4 + (f32s ? 0 : 128)) * (K / 128); }
+};
 
-template <bool F32S>
+template <bool F32S, int TN>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void fp8_tiled_kernel(Fp8GemmArgs a) {
+  using T = FpTile<TN>;
+  constexpr int FT_S = T::S, FT_A = T::A, FT_B = T::B, FT_STAGE = T::STAGE, FT_RING = T::RING, FT_LDC = T::LDC;
+  constexpr int CB = T::CB;
   extern __shared__ __align__(16) uint8_t smem[];
   int bx, by;
   tile_block(gridDim.x, bx, by);
   const int K = a.K, KS = K / 128, M = a.M;
   const int row0 = by * 128;
   if (row0 >= M) return;  // padding of the grid's row-tile count
-  const int Mt = min(128, M - row0), col0 = bx * 128;
+  const int Mt = min(128, M - row0), col0 = bx * TN;
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int rh = wave & 1, ch = wave >> 1;
@@ -52,12 +59,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   uint8_t* const sa_lds = smem + FT_RING + 4 * KS;
 
   // Per-lane load offsets (constant over the stages). Rows past the tile repeat its last row (never stored).
-  uint32_t aoff[4], boff[4];
+  uint32_t aoff[4], boff[T::BL];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int slot = (wave * 4 + i) * 64 + lane, r = slot >> 3, p = (slot & 7) ^ lds_swz(r);
     aoff[i] = uint32_t(min(r, Mt - 1)) * uint32_t(K) + uint32_t(p * 16);
-    boff[i] = uint32_t(r) * uint32_t(K) + uint32_t(p * 16);  // columns: the same slot geometry
+  }
+#pragma unroll
+  for (int i = 0; i < T::BL; ++i) {  // columns: the same slot geometry
+    const int slot = (wave * T::BL + i) * 64 + lane, r = slot >> 3, p = (slot & 7) ^ lds_swz(r);
+    boff[i] = uint32_t(r) * uint32_t(K) + uint32_t(p * 16);
   }
   // fp32 activation scales: waves 0 and 1 gather rows 64 w + lane.
   const uint32_t saoff = uint32_t(min((wave & 1) * 64 + lane, Mt - 1)) * uint32_t(KS) * 4u;
@@ -69,14 +80,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 #pragma unroll
     for (int i = 0; i < 4; ++i) dma16(arow + s * 128, aoff[i], st + uint32_t(wave * 4 + i) * 1024);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(wcol + s * 128, boff[i], st + uint32_t(FT_A + (wave * 4 + i) * 1024));
+    for (int i = 0; i < T::BL; ++i) dma16(wcol + s * 128, boff[i], st + uint32_t(FT_A + (wave * T::BL + i) * 1024));
     if constexpr (F32S)
       if (wave < 2) dma4(a.sa32 + size_t(row0) * KS + s, saoff, st + uint32_t(FT_A + FT_B + wave * 256));
   };
   issue(0);
   // Scales, after stage 0 is in flight.
   for (int e = tid; e < KS; e += 256) {
-    const size_t i = size_t(col0 / 128) * KS + e;
+    const size_t i = size_t(col0 / 128) * KS + e;  // a TN-column block lies in one 128-row scale block
     sw_lds[e] = F32S ? a.sw32[i] : e8m0_to_f32(a.sw8[i]);
   }
   if constexpr (!F32S) {
@@ -85,11 +96,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   }
 
   const int rb_live = __builtin_amdgcn_readfirstlane(min(2, max(0, (Mt - rh * 64 + 31) / 32)));
-  v16f_t acc[2][2];
+  v16f_t acc[2][CB];
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = v16f_t{};
+    for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = v16f_t{};
 
   for (int s = 0; s < KS; ++s) {
     wait_vm<0>();     // this wave's part of stage s (the only stage in flight)
@@ -101,19 +112,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
       asc[rb] = F32S ? 1.0f : e8m0_to_f32(sa_lds[s * 128 + rh * 64 + rb * 32 + l32]);
-    v16f_t raw[2][2];
+    v16f_t raw[2][CB];
     if constexpr (F32S) {
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) raw[rb][cb] = v16f_t{};
+        for (int cb = 0; cb < CB; ++cb) raw[rb][cb] = v16f_t{};
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      v4i aq[2][2], bq[2][2];
+      v4i aq[2][2], bq[CB][2];
 #pragma unroll
-      for (int cb = 0; cb < 2; ++cb) {
-        const int n = ch * 64 + cb * 32 + l32;
+      for (int cb = 0; cb < CB; ++cb) {
+        const int n = ch * (TN / 2) + cb * 32 + l32;
 #pragma unroll
         for (int x = 0; x < 2; ++x)
           bq[cb][x] = *reinterpret_cast<const v4i*>(stb + FT_A + (n * 8 + ((4 * j + 2 * h + x) ^ lds_swz(n))) * 16);
@@ -127,9 +138,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       }
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        bf16x8 bf[2];
+        bf16x8 bf[CB];
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
+        for (int cb = 0; cb < CB; ++cb)
           bf[cb] = fp8x8_to_bf16(uint32_t(bq[cb][t >> 1][(t & 1) * 2]), uint32_t(bq[cb][t >> 1][(t & 1) * 2 + 1]),
                                  F32S ? 1.0f : swv);
 #pragma unroll
@@ -138,7 +149,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
           const bf16x8 af =
               fp8x8_to_bf16(uint32_t(aq[rb][t >> 1][(t & 1) * 2]), uint32_t(aq[rb][t >> 1][(t & 1) * 2 + 1]), asc[rb]);
 #pragma unroll
-          for (int cb = 0; cb < 2; ++cb) {
+          for (int cb = 0; cb < CB; ++cb) {
             if constexpr (F32S) raw[rb][cb] = mfma32_bf16(af, bf[cb], raw[rb][cb]);
             else acc[rb][cb] = mfma32_bf16(af, bf[cb], acc[rb][cb]);
           }
@@ -156,7 +167,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
           const float4 sa4 = *reinterpret_cast<const float4*>(sas + rh * 64 + rb * 32 + 8 * i4 + 4 * h);
           const float f[4] = {sa4.x * swv, sa4.y * swv, sa4.z * swv, sa4.w * swv};
 #pragma unroll
-          for (int cb = 0; cb < 2; ++cb)
+          for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
             for (int q = 0; q < 4; ++q) acc[rb][cb][4 * i4 + q] += raw[rb][cb][4 * i4 + q] * f[q];
         }
@@ -164,40 +175,50 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     }
   }
 
-  // ---- epilogue through LDS: 128 x 128 bf16, then 16-byte row stores
+  // ---- epilogue through LDS: 128 x TN bf16, then 16-byte row stores
   __syncthreads();
   uint16_t* sc = reinterpret_cast<uint16_t*>(smem);
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
+    for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
       for (int i = 0; i < 16; ++i)
-        sc[(rh * 64 + rb * 32 + 8 * (i / 4) + 4 * h + (i % 4)) * FT_LDC + ch * 64 + cb * 32 + l32] =
+        sc[(rh * 64 + rb * 32 + 8 * (i / 4) + 4 * h + (i % 4)) * FT_LDC + ch * (TN / 2) + cb * 32 + l32] =
             f32_to_bf16(acc[rb][cb][i]);
   __syncthreads();
-  for (int e = tid; e < Mt * 16; e += 256) {
-    const int r = e / 16, c8 = (e % 16) * 8;
+  for (int e = tid; e < Mt * (TN / 8); e += 256) {
+    const int r = e / (TN / 8), c8 = (e % (TN / 8)) * 8;
     *reinterpret_cast<uint4*>(a.c + size_t(row0 + r) * a.ldc + col0 + c8) =
         *reinterpret_cast<const uint4*>(sc + r * FT_LDC + c8);
   }
 }
 
-template <bool F32S>
+template <bool F32S, int TN>
 void launch_tiled_t(const Fp8GemmArgs& a, hipStream_t st) {
-  const size_t lds = tiled_lds(a.K, F32S);
-  auto* kern = &fp8_tiled_kernel<F32S>;
+  const size_t lds = FpTile<TN>::lds(a.K, F32S);
+  auto* kern = &fp8_tiled_kernel<F32S, TN>;
   UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                int(lds)));
-  kern<<<tile_grid(a.N / 128, (a.M + 127) / 128), 256, lds, st>>>(a);
+  kern<<<tile_grid(a.N / TN, (a.M + 127) / 128), 256, lds, st>>>(a);
   UH_CHECK_LAUNCH();
+}
+// 64-column tiles while 128-column ones would leave fewer than 256 workgroups: twice the workgroups on the same
+// serial K loop each. 4096 x 4096 step, 128 / 64 columns: M = 384 55.9 / 52.7 us, 512 56.6 / 53.0, 768 57.4 / 55.6,
+// 1024 (256 workgroups of 128 columns) 61.0 / 60.1, 2048 96.1 / 112.5. (A 4-slot ring of 64-column stages, three in
+// flight, ran 80 us at M = 384-768: not kept.)
+bool tiled_narrow(const Fp8GemmArgs& a) { return size_t(a.N / 128) * ((a.M + 127) / 128) < 256; }
+template <bool F32S>
+void launch_tiled_f(const Fp8GemmArgs& a, hipStream_t st) {
+  if (tiled_narrow(a)) launch_tiled_t<F32S, 64>(a, st);
+  else launch_tiled_t<F32S, 128>(a, st);
 }
 
 }  // namespace
 
 bool fp8_tiled_fits(const Fp8GemmArgs& a) {
   // two workgroups per CU: 80 KB of LDS each
-  return a.N % 128 == 0 && a.K % 128 == 0 && a.ldc % 8 == 0 && tiled_lds(a.K, a.sa32 != nullptr) <= 80 * 1024;
+  return a.N % 128 == 0 && a.K % 128 == 0 && a.ldc % 8 == 0 && FpTile<128>::lds(a.K, a.sa32 != nullptr) <= 80 * 1024;
 }
 
 void launch_fp8_tiled(const Fp8GemmArgs& a, hipStream_t st) {
@@ -206,10 +227,10 @@ void launch_fp8_tiled(const Fp8GemmArgs& a, hipStream_t st) {
   if (!a.a || !a.w || !a.c) throw std::runtime_error("fp8 gemm: null operand");
   if (a.sa32) {
     if (!a.sw32) throw std::runtime_error("fp8 gemm: scales");
-    launch_tiled_t<true>(a, st);
+    launch_tiled_f<true>(a, st);
   } else {
     if (!a.sa8 || !a.sw8) throw std::runtime_error("fp8 gemm: scales");
-    launch_tiled_t<false>(a, st);
+    launch_tiled_f<false>(a, st);
   }
 }
 
