@@ -119,6 +119,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) raw[rb][cb] = v16f_t{};
     }
+    // The stage's operand reads, conversions and MFMAs at raised wave priority, so that a wave holding operands
+    // issues ahead of the other workgroup's waves still waiting for theirs (M = 4096 step: 172 against 181 us).
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       v4i aq[2][2], bq[CB][2];
@@ -156,6 +159,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
         }
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     if constexpr (F32S) {
       // Value i of a 32 x 32 block sits at row 8 (i / 4) + 4 h + i % 4: rows in runs of 4, one 16-byte read each.
       const float* sas = reinterpret_cast<const float*>(stb + FT_A + FT_B);
