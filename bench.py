@@ -175,20 +175,25 @@ def bench_moe(w, T, steps, warmup, rng, R=8, bias=0.0, stage=False):
 
 
 class DropinRunner:
-    """The reference's own call sequence for the native MXFP4 experts (src/model/forward_ref.hip:455-470) through the
-    drop-in entry points: routing (uh_route_softmax), dispatch (uh_moe_dispatch_small for T <= 32, else count / plan /
-    scatter), mx_xform_in (the pair rows gathered and fake-quantized to bf16), the w1 / w3 launch with the SwiGLU
-    epilogue writing hh (mx_grouped_gemv with MxGlu, or mx_grouped_gemm_glu for T > 64), the w2 launch on hh
-    (mx_grouped_gemv / mx_grouped_gemm), then moe_combine."""
+    """The reference's own call sequence for the native MXFP4 experts (src/model/forward_ref.hip:455-470, with
+    UNHOLY_MX_GEMV_TOKENS unset: a GEMV step for T <= 8 tokens) through the drop-in entry points: routing
+    (uh_route_softmax), dispatch (uh_moe_dispatch_small for T <= 32, else count / plan / scatter; tiles of
+    kMxGemvTileRows = 8 rows for a GEMV step, else 128), mx_xform_in (the pair rows gathered and fake-quantized to
+    bf16), then
+      - T <= 8: mx_grouped_gemv for w1 / w3 with the SwiGLU epilogue writing hh (MxGlu), mx_grouped_gemv for w2;
+      - larger T, glu (the reference's gfx11 order): mx_grouped_gemm_glu, then mx_grouped_gemm for w2;
+      - larger T, not glu (its gfx12 order): mx_grouped_gemm for w1 and w3 (two outputs), mx_swiglu, mx_grouped_gemm
+        for w2;
+    each grouped call with max_rows = min(T, 128) (an expert has at most one row per token); then moe_combine."""
 
-    def __init__(self, w, sets):
+    def __init__(self, w, sets, glu=True):
         from unholy_amd import call
         from unholy_amd.device import DeviceBuffer, pointer_table
         self.call, self.w = call, w
         T = self.T = sets[0][0].shape[0]
         P = self.P = T * TOPK
-        self.gemv = T <= 64
-        self.tile_rows = 16 if self.gemv else 128
+        self.gemv, self.glu = T <= 8, glu
+        self.tile_rows = 8 if self.gemv else 128
         self.max_tiles = min(P, E + P // self.tile_rows + 1)
         self.dev = [(DeviceBuffer.from_array(x), DeviceBuffer.from_array(l)) for x, l in sets]
         self.U = [distinct_experts(l)[0] for _, l in sets]
@@ -198,6 +203,7 @@ class DropinRunner:
         self.eidx, self.ewt, self.row_expert, self.pidx = B(P * 4), B(P * 4), B(P * 4), B(P * 4)
         self.count, self.off, self.fill = B(E * 4), B(E * 4), B(E * 4)
         self.xa, self.hh, self.pair = B(P * D * 2), B(P * I * 2), B(P * D * 2)
+        self.g, self.u = (B(P * I * 2), B(P * I * 2)) if not (self.gemv or glu) else (None, None)
         self.out = B(T * D * 2)
         t = w.ptrs
         self.tab = [pointer_table(t[i]) for i in range(6)]
@@ -220,25 +226,30 @@ class DropinRunner:
             c("uh_moe_scatter", self.sel, self.wt, T, TOPK, self.off, self.fill, self.eidx, self.ewt, self.row_expert,
               self.pidx, st)
         c("uh_mx_xform_in", x, D, self.row_expert, s1, self.xa, P, D, st, self.eidx)
-        rows = min(T, self.tile_rows)
+        rows = min(T, 128)
         if self.gemv:
             c("uh_mx_grouped_gemv", self.xa, D, self.tiles, self.max_tiles, w1, s1, None, I, I, st, ntd, w3, s3, None,
               rows, self.ewt, self.row_expert, s2, self.hh, LIMIT, None)
             c("uh_mx_grouped_gemv", self.hh, I, self.tiles, self.max_tiles, w2, s2, self.pair, D, D, st, ntd, None,
               None, None, rows, None, None, None, None, 0.0, None)
         else:
-            c("uh_mx_grouped_gemm_glu", self.xa, D, self.tiles, self.max_tiles, w1, s1, w3, s3, I, self.ewt,
-              self.row_expert, s2, self.hh, LIMIT, st, ntd)
+            if self.glu:
+                c("uh_mx_grouped_gemm_glu", self.xa, D, self.tiles, self.max_tiles, w1, s1, w3, s3, I, self.ewt,
+                  self.row_expert, s2, self.hh, LIMIT, st, ntd)
+            else:
+                c("uh_mx_grouped_gemm", self.xa, D, self.tiles, self.max_tiles, w1, s1, self.g, I, I, st, ntd, w3, s3,
+                  self.u, rows)
+                c("uh_mx_swiglu", self.g, self.u, self.ewt, self.row_expert, s2, self.hh, P, I, LIMIT, st)
             c("uh_mx_grouped_gemm", self.hh, I, self.tiles, self.max_tiles, w2, s2, self.pair, D, D, st, ntd, None,
               None, None, rows)
         c("uh_moe_combine", self.pair, self.pidx, None, self.out, T, TOPK, D, st)
 
 
-def bench_dropin(w, T, steps, warmup, rng, R=8):
+def bench_dropin(w, T, steps, warmup, rng, R=8, bias=0.0, glu=True):
     """ms per step of the reference's call sequence (DropinRunner); T <= 32 as HIP-graph replays (the GPU's time, not
     the host's launch rate of seven ctypes calls), larger T eagerly (memsets are not captured)."""
-    sets = routing_sets(rng, T, R, disjoint=T <= 8)
-    r = DropinRunner(w, sets)
+    sets = routing_sets(rng, T, R, bias, disjoint=T <= 8)
+    r = DropinRunner(w, sets, glu)
     if T <= 32:
         return dict(ms=time_graph(lambda i, st: r.step(i, st), steps, warmup, per_graph=R), U=float(np.mean(r.U)))
     return dict(ms=time_steps(lambda i: r.step(i), steps, warmup) / steps, U=float(np.mean(r.U)))
@@ -604,8 +615,9 @@ def run_only(name, args, rng):
         return {"moe_decode_T8_ms": d["ms"], "distinct_experts": d["U"]}
     if name == "dropin":
         d8 = bench_dropin(w, 8, args.steps, args.warmup, rng)
+        d64 = bench_dropin(w, 64, 50, 5, rng, bias=0.5, glu=False)
         d4 = bench_dropin(w, 4096, 5, 1, rng)
-        return {"dropin_T8_ms": d8["ms"], "dropin_T4096_ms": d4["ms"]}
+        return {"dropin_T8_ms": d8["ms"], "dropin_T64_ms": d64["ms"], "dropin_T4096_ms": d4["ms"]}
     if name == "verify":
         d = bench_moe(w, 64, 50, 5, rng, bias=0.5)
         return {"moe_verify_T64_ms": d["ms"], "distinct_experts": d["U"]}
@@ -671,10 +683,15 @@ def main():
     if not args.no_sweep:
         wl = {}
         s0 = bench_single_gemv(w, 500, 50, rng)
-        wl["single_gemv_M1 (configs[0])"] = {"ms": s0, "GBps": (MAT_BYTES + D + D // 128 + I * 2) / (s0 * 1e-3) / 1e9}
+        b0 = MAT_BYTES + D + D // 128 + I * 2  # weights (codes + scales), the row's codes + scales in, bf16 out
+        wl["single_gemv_M1 (configs[0])"] = {"ms": s0, "algorithmic_bytes": b0, "GBps": b0 / (s0 * 1e-3) / 1e9,
+                                             "bound": "hbm", "frac_hbm_peak": b0 / (s0 * 1e-3) / 1e9 / HBM_PEAK_GBS}
         v = bench_moe(w, 64, 50, 5, rng, bias=0.5)
+        bv = v["U"] * EXPERT_BYTES + 64 * D * 2 * 2  # touched experts' w1 + w3 + w2, x in and out (bf16)
         wl["moe_verify_T64 (configs[2])"] = {"ms": v["ms"], "tokens_per_s": 64 / (v["ms"] * 1e-3),
-                                              "distinct_experts": v["U"],
+                                              "distinct_experts": v["U"], "step_algorithmic_bytes": bv,
+                                              "GBps": bv / (v["ms"] * 1e-3) / 1e9, "bound": "hbm",
+                                              "frac_hbm_peak": bv / (v["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS,
                                               "GBps_weights": v["U"] * EXPERT_BYTES / (v["ms"] * 1e-3) / 1e9}
         from unholy_amd import call
         flops = 4096 * TOPK * 3 * 2 * D * I
@@ -697,13 +714,15 @@ def main():
                 "mfma": "v_mfma_scale_f32_16x16x128_f8f6f4 (e4m3 x e2m1, e8m0 block scales); sums below fp32 "
                         "precision, outside the per-element tolerance",
                 "frac_fp8_mfma_peak": flops / (ps["ms"] * 1e-3) / 1e12 / FP8_PEAK_TFLOPS}}
-        for T, stp, wu in ((8, 200, 16), (4096, 5, 1)):
-            dr = bench_dropin(w, T, stp, wu, rng)
+        for T, stp, wu, bias, glu in ((8, 200, 16, 0.0, True), (64, 50, 5, 0.5, False), (4096, 5, 1, 0.0, True)):
+            dr = bench_dropin(w, T, stp, wu, rng, bias=bias, glu=glu)
             wl[f"dropin_sequence_T{T}"] = {
                 "ms": dr["ms"], "tokens_per_s": T / (dr["ms"] * 1e-3), "distinct_experts": dr["U"],
                 "sequence": "route_softmax, dispatch, mx_xform_in, " + (
-                    "mx_grouped_gemv (MxGlu hh), mx_grouped_gemv" if T <= 64 else
-                    "mx_grouped_gemm_glu, mx_grouped_gemm") + ", moe_combine (forward_ref.hip:455-470)"}
+                    "mx_grouped_gemv (MxGlu hh), mx_grouped_gemv (tiles of 8 rows)" if T <= 8 else
+                    "mx_grouped_gemm (w1 and w3, max_rows = T), mx_swiglu, mx_grouped_gemm (w2, max_rows = T)"
+                    if not glu else "mx_grouped_gemm_glu, mx_grouped_gemm") +
+                ", moe_combine (forward_ref.hip:455-470; UNHOLY_MX_GEMV_TOKENS unset)"}
         for M, copies in ((1, 64), (64, 64), (4096, 4)):
             t = bench_fp8_dense(M, 100 if M < 4096 else 10, 10 if M < 4096 else 2, rng, copies)
             wl[f"fp8_dense_M{M} (configs[4])"] = {"ms": t, "tokens_per_s": M / (t * 1e-3),

@@ -54,7 +54,7 @@ _SIGS = {
     "or_remote_combine": (None, [_P, _P, _I, _I, _I, _P]),
     "or_hc_post": (None, [_P, _P, _P, _P, _P, _I, _I, _I]),
     "or_moe_combine_partial": (None, [_P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _I]),
-    "or_moe_forward": (None, [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _F, _P, _P, _I, _P, _I]),
+    "or_moe_forward": (None, [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _F, _P, _P, _I, _P, _I, _P, _P]),
 }
 
 _lib = None
@@ -421,9 +421,10 @@ def hc_post(x, res, post, comb):
     return out
 
 
-def moe_forward(x, sel, wt, experts, D, I, limit, tiled=True, threads=8, subset=None):
+def moe_forward(x, sel, wt, experts, D, I, limit, tiled=True, threads=8, subset=None, with_h=False):
     """experts: list of E dicts with w1, s1, w3, s3, w2, s2 (uint8 arrays, tile-major when tiled) or None.
-    Returns (out bf16 [T, D] or None when subset is given, pair_out bf16 [T*K, D])."""
+    Returns (out bf16 [T, D] or None when subset is given, pair_out bf16 [T*K, D]), and with with_h also the codes
+    [T*K, I] and e8m0 scales [T*K, I/128] of h (act_quant of the SwiGLU output) per pair row."""
     x = _c(x, np.uint16)
     sel = _c(sel, np.int32)
     wt = _c(wt, np.float32)
@@ -442,8 +443,11 @@ def moe_forward(x, sel, wt, experts, D, I, limit, tiled=True, threads=8, subset=
     pair_out = np.zeros((T * K, D), np.uint16)
     out = None if subset is not None else np.empty((T, D), np.uint16)
     sub = None if subset is None else _c(subset, np.int32)
+    hq = np.zeros((T * K, I), np.uint8) if with_h else None
+    hs = np.zeros((T * K, I // 128), np.uint8) if with_h else None
     lib().or_moe_forward(_p(x), _p(sel), _p(wt), T, K, E, D, I,
                          ctypes.cast(tabs["w1"], _P), ctypes.cast(tabs["s1"], _P), ctypes.cast(tabs["w3"], _P),
                          ctypes.cast(tabs["s3"], _P), ctypes.cast(tabs["w2"], _P), ctypes.cast(tabs["s2"], _P),
-                         int(tiled), limit, _p(pair_out), _p(out), threads, _p(sub), 0 if sub is None else len(sub))
-    return out, pair_out
+                         int(tiled), limit, _p(pair_out), _p(out), threads, _p(sub), 0 if sub is None else len(sub),
+                         _p(hq), _p(hs))
+    return (out, pair_out, hq, hs) if with_h else (out, pair_out)

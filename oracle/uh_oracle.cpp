@@ -739,7 +739,7 @@ void or_moe_forward(const uint16_t* x, const int32_t* sel, const float* wt, int 
                     const uint8_t* const* w1, const uint8_t* const* s1, const uint8_t* const* w3,
                     const uint8_t* const* s3, const uint8_t* const* w2, const uint8_t* const* s2, int tiled,
                     float limit, uint16_t* pair_out, uint16_t* out, int nthreads, const int32_t* experts_subset,
-                    int n_subset) {
+                    int n_subset, uint8_t* hq_out, uint8_t* hs_out) {
   const int P = T * K;
   std::vector<int32_t> count(static_cast<size_t>(E)), off(static_cast<size_t>(E)), eidx(static_cast<size_t>(P)), row_expert(static_cast<size_t>(P)), pidx(static_cast<size_t>(P));
   std::vector<float> ewt(static_cast<size_t>(P));
@@ -772,6 +772,8 @@ void or_moe_forward(const uint16_t* x, const int32_t* sel, const float* wt, int 
     or_gemm_a8w4(q.data(), qs.data(), w3[e], s3[e], h3.data(), nullptr, I, cnt, I, D, tiled, inner);
     or_swiglu(h1.data(), h3.data(), &ewt[size_t(r0)], hh.data(), cnt, I, limit);
     or_act_quant_fp8(hh.data(), I, q.data(), qs.data(), cnt, I, 128);
+    if (hq_out) std::memcpy(hq_out + size_t(r0) * I, q.data(), size_t(cnt) * I);  // h's codes and scales, optional
+    if (hs_out) std::memcpy(hs_out + size_t(r0) * (I / 128), qs.data(), size_t(cnt) * (I / 128));
     or_gemm_a8w4(q.data(), qs.data(), w2[e], s2[e], pair_out + size_t(r0) * D, nullptr, D, cnt, D, I, tiled, inner);
   });
   if (out) or_moe_combine(pair_out, pidx.data(), nullptr, out, T, K, D);

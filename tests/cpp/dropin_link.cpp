@@ -68,7 +68,11 @@ T* dev_zero(size_t n) {
   return p;
 }
 
-int run_case(int T, int K, int E, int D, int I, uint64_t seed) {
+// seq: 0 = the grouped GEMV with the SwiGLU epilogue (decode: tiles of 16 rows), 1 = the grouped GEMM with the
+// SwiGLU epilogue (mx_grouped_gemm_glu, 128-row tiles), 2 = the gfx12 order of forward_ref.hip:459-470 for a verify
+// step (UNHOLY_MX_GEMV_TOKENS unset, so T > 8 is not a GEMV step): w1 and w3 through mx_grouped_gemm with
+// max_rows = T on 128-row tiles, mx_swiglu, then w2 through mx_grouped_gemm with max_rows = T.
+int run_case(int T, int K, int E, int D, int I, uint64_t seed, int seq) {
   Lcg rng{seed};
   const float limit = 10.0f;
   const int P = T * K;
@@ -102,7 +106,7 @@ int run_case(int T, int K, int E, int D, int I, uint64_t seed) {
   int32_t* sel = dev_zero<int32_t>(P);
   float* wt = dev_zero<float>(P);
   k::route_softmax(dl, sel, wt, T, E, K, nullptr);
-  const bool gemv = T <= 64;
+  const bool gemv = seq == 0;
   const int tile_rows = gemv ? 16 : k::kExl3TileRows, max_tiles = P + E;
   int32_t* count = dev_zero<int32_t>(E);
   int32_t* off = dev_zero<int32_t>(E);
@@ -119,6 +123,8 @@ int run_case(int T, int K, int E, int D, int I, uint64_t seed) {
   const int* ntd = &plan->n_local_tiles;
   uint16_t* xa = dev_zero<uint16_t>(size_t(P) * D);
   uint16_t* hh = dev_zero<uint16_t>(size_t(P) * I);
+  uint16_t* gbuf = dev_zero<uint16_t>(size_t(P) * I);
+  uint16_t* ubuf = dev_zero<uint16_t>(size_t(P) * I);
   uint16_t* pair = dev_zero<uint16_t>(size_t(P) * D);
   uint16_t* out = dev_zero<uint16_t>(size_t(T) * D);
   k::mx_xform_in(dx, D, row_expert, t(0, 1), xa, P, D, nullptr, eidx);
@@ -129,9 +135,16 @@ int run_case(int T, int K, int E, int D, int I, uint64_t seed) {
                        rows, glu);
     k::mx_grouped_gemv(hh, I, tiles, max_tiles, t(2, 0), t(2, 1), pair, D, D, nullptr, ntd, nullptr, nullptr, nullptr,
                        rows);
-  } else {
+  } else if (seq == 1) {
     k::mx_grouped_gemm_glu(xa, D, tiles, max_tiles, t(0, 0), t(0, 1), t(1, 0), t(1, 1), I, glu, nullptr, ntd);
     k::mx_grouped_gemm(hh, I, tiles, max_tiles, t(2, 0), t(2, 1), pair, D, D, nullptr, ntd);
+  } else {
+    const int vrows = std::min(T, k::kExl3TileRows);  // an expert has at most one row per token
+    k::mx_grouped_gemm(xa, D, tiles, max_tiles, t(0, 0), t(0, 1), gbuf, I, I, nullptr, ntd, t(1, 0), t(1, 1), ubuf,
+                       vrows);
+    k::mx_swiglu(gbuf, ubuf, ewt, row_expert, t(2, 1), hh, P, I, limit, nullptr);
+    k::mx_grouped_gemm(hh, I, tiles, max_tiles, t(2, 0), t(2, 1), pair, D, D, nullptr, ntd, nullptr, nullptr, nullptr,
+                       vrows);
   }
   k::moe_combine(pair, pidx, nullptr, out, T, K, D, nullptr);
 
@@ -152,8 +165,9 @@ int run_case(int T, int K, int E, int D, int I, uint64_t seed) {
     diff += a[i] != b[i];
     nonzero += (a[i] & 0x7fff) != 0;
   }
+  static const char* const names[3] = {"grouped GEMV", "grouped GEMM", "grouped GEMM, max_rows = T"};
   std::printf("dropin_link: T=%d K=%d E=%d D=%d I=%d (%s): %zu of %zu outputs differ, %zu nonzero\n", T, K, E, D, I,
-              gemv ? "grouped GEMV" : "grouped GEMM", diff, a.size(), nonzero);
+              names[seq], diff, a.size(), nonzero);
   return diff == 0 && nonzero > a.size() / 2 ? 0 : 1;
 }
 
@@ -161,8 +175,9 @@ int run_case(int T, int K, int E, int D, int I, uint64_t seed) {
 
 int main() {
   int bad = 0;
-  bad |= run_case(8, 6, 32, 512, 256, 1);
-  bad |= run_case(200, 4, 16, 512, 256, 2);
+  bad |= run_case(8, 6, 32, 512, 256, 1, 0);
+  bad |= run_case(200, 4, 16, 512, 256, 2, 1);
+  bad |= run_case(64, 6, 32, 512, 256, 3, 2);
   std::printf("dropin_link: %s\n", bad ? "MISMATCH" : "OK");
   return bad;
 }

@@ -397,3 +397,68 @@ def test_grouped_gemm_prefill_tiles(amode, gemm_arith):
         codes, scales = hq.download((P, N), np.uint8), hs.download((P, N // 128), np.uint8)
         deq = oracle.e4m3_to_f32(codes) * np.ldexp(1.0, scales.astype(np.int32) - 127).repeat(128, axis=1)
         assert np.array_equal(deq.astype(np.float32), from_bf16(hgot))
+
+
+@pytest.mark.parametrize("K,N", [(1024, 384), (512, 256)])
+def test_grouped_gemm_max_rows_routes_to_gemv(K, N):
+    """mx_grouped_gemm with max_rows <= 64 (the reference's verify steps pass the step's token count,
+    forward_ref.hip:455-470) runs the grouped GEMV over 128-row tiles of up to 64 rows; the outputs must equal the
+    128-row GEMM's (max_rows = 128) bit for bit, with one and with two projections, and match the oracle (max-rel <=
+    1e-2 per element). N = 384 also runs the GEMM's half column block (N % 256 == 128)."""
+    rng = np.random.default_rng(71)
+    E = 5
+    rows = [1, 17, 64, 0, 40]
+    tiles, row_expert, P = _gemm_case(rng, rows, E, K, N)
+    x = randn_bf16(rng, (P, K), 1.5)
+    xa = oracle.fake_quant_fp8(x)
+    q, qs = oracle.act_quant_fp8(x)
+    w1, w3 = _make_experts(rng, E, N, K), _make_experts(rng, E, N, K)
+    b1, t1 = _expert_tables(w1, ("w", "s"))
+    b3, t3 = _expert_tables(w3, ("w", "s"))
+    g_ref = np.zeros((P, N), np.uint16)
+    for e, a0, c in tiles:
+        w, s_ = oracle.unrepack(w1[e]["w"], w1[e]["s"], N, K)
+        g_ref[a0:a0 + c] = oracle.gemm_a8w4(q[a0:a0 + c], qs[a0:a0 + c], w, s_, N)[0]
+    dxa, dt = dev(xa), dev(tiles)
+    ntd = dev(np.array([len(tiles)], np.int32))
+    outs = {}
+    for max_rows in (128, 64, 40):
+        g, u, g1 = DeviceBuffer(P * N * 2), DeviceBuffer(P * N * 2), DeviceBuffer(P * N * 2)
+        call("uh_mx_grouped_gemm", dxa, K, dt, len(tiles) + 3, t1["w"], t1["s"], g, N, N, None, ntd, t3["w"], t3["s"],
+             u, max_rows)
+        call("uh_mx_grouped_gemm", dxa, K, dt, len(tiles), t1["w"], t1["s"], g1, N, N, None, None, None, None, None,
+             max_rows)
+        synchronize()
+        outs[max_rows] = [b.download((P, N), np.uint16) for b in (g, u, g1)]
+    mr = max_rel(from_bf16(outs[128][0]), from_bf16(g_ref))
+    print(f"K={K} N={N}: GEMM vs oracle max_rel {mr:.3e}, bit-identical {np.mean(outs[128][0] == g_ref):.5f}")
+    assert mr <= 1e-2 and np.array_equal(outs[128][0], outs[128][2])
+    for max_rows in (64, 40):  # 40: tiles of up to 64 rows still run whole (16-row groups)
+        for a, b in zip(outs[max_rows], outs[128]):
+            assert np.array_equal(a, b), max_rows
+
+
+def test_grouped_gemm_k64_half_block():
+    """K % 64 == 0 with K % 128 != 0 (the reference's bound, mx_moe.hip:1045) and N % 256 == 128 on plain bf16 rows:
+    the 64-input-stage GEMM against an fp64 product of the bf16 rows and the decoded weights (max-rel <= 1e-2 per
+    element; the rows are not fake-quantized here, so each 32-block's sum rounds once in fp32)."""
+    rng = np.random.default_rng(72)
+    E, K, N = 3, 192, 384
+    rows = [5, 130, 33]
+    tiles, row_expert, P = _gemm_case(rng, rows, E, K, N)
+    x = randn_bf16(rng, (P, K))
+    w1 = _make_experts(rng, E, N, K)
+    b1, t1 = _expert_tables(w1, ("w", "s"))
+    ref = np.zeros((P, N))
+    xf = from_bf16(x).astype(np.float64)
+    for e, a0, c in tiles:
+        wd = oracle.mx_dequant(w1[e]["w"], w1[e]["s"], N, K, tiled=True).astype(np.float64)
+        ref[a0:a0 + c] = xf[a0:a0 + c] @ wd.T
+    g = DeviceBuffer(P * N * 2)
+    call("uh_mx_grouped_gemm", dev(x), K, dev(tiles), len(tiles), t1["w"], t1["s"], g, N, N, None, None, None, None,
+         None, 128)
+    synchronize()
+    got = from_bf16(g.download((P, N), np.uint16))
+    mr = max_rel(got, ref)
+    print(f"K={K} N={N} bf16 rows: max_rel {mr:.3e} vs fp64")
+    assert mr <= 1e-2

@@ -361,7 +361,6 @@ def test_dispatch_invariants(tile_rows):
     # resident experts first, each group in ascending id
     order = [e for e in range(E) if resident[e]] + [e for e in range(E) if not resident[e]]
     assert d["plan"][1] == sum(d["count"][e] for e in range(E) if resident[e])
-    assert list(np.argsort(d["off"], kind="stable")) == [e for e in order] or True
     pos = 0
     for e in order:
         assert d["off"][e] == pos

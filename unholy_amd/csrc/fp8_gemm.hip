@@ -6,6 +6,7 @@
 // On gfx950 raw_kb is four bf16 MFMAs (16x16x32) per 16 x 16 output tile on operands dequantized exactly in
 // registers (the block-scaled f8f6f4 MFMA's internal sums are not fp32-accurate; see common.hpp).
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 #include "numerics.hpp"
@@ -486,14 +487,16 @@ struct Fp8Rows {
   }
 };
 
-template <int CH>
+// NCH = the chunk count, ceil((K / 128) / KP) (1..FR_MAXCH): a template parameter, so that the issue order and every
+// counted wait are fixed at compile time and no branch depends on how many loads are outstanding.
+template <int CH, int NCH>
 __global__ __launch_bounds__(1024) void fp8_rows_kernel(Fp8GemmArgs p) {
   using namespace pipe;
   using T = Fp8Rows<CH>;
   constexpr int KP = T::KP, KR = T::KR, SLOT = T::SLOT, NA = T::NA;
   extern __shared__ __align__(16) uint8_t smem[];
-  const int M = p.M, N = p.N, K = p.K, KS = K / 128, nch = (KS + KP - 1) / KP;  // nch <= FR_MAXCH
-  if (nch < 1) return;  // (the host requires K >= 128) no load is ever left pending past the chunk loop
+  static_assert(NCH >= 1 && NCH <= FR_MAXCH);
+  const int M = p.M, N = p.N, K = p.K, KS = K / 128;  // the host launches NCH = ceil(KS / KP)
   const int nw = gridDim.x, lin = blockIdx.x;
   const int wi = nw % 8 ? lin : (lin & 7) * (nw >> 3) + (lin >> 3);
   const int RT = (M + 31) / 32, rt = wi % RT, bx = wi / RT, row0 = rt * 32;
@@ -518,7 +521,7 @@ __global__ __launch_bounds__(1024) void fp8_rows_kernel(Fp8GemmArgs p) {
       dma16(p.a, rowoff[i] + uint32_t(min(ch * KR + pin[i], K - 16)),
             lds0 + uint32_t((ch & 1) * SLOT + (wave * NA + i) * 1024));
   };
-  v4i b[FR_MAXCH][4];
+  v4i b[NCH][4];
   const auto load_w = [&](int u) {
     const uint8_t* q = wld + min(u * KP + kh, KS - 1) * 128;
 #pragma unroll
@@ -535,35 +538,24 @@ __global__ __launch_bounds__(1024) void fp8_rows_kernel(Fp8GemmArgs p) {
   }
   load_w(0);
   issue_a(0);
-  if (nch > 1) {
+  if constexpr (NCH > 1) {
     load_w(1);
     issue_a(1);
   }
-  if (nch > 2) load_w(2);
-  if (nch > 3) load_w(3);
+  if constexpr (NCH > 2) load_w(2);
+  if constexpr (NCH > 3) load_w(3);
   const int r = l32;
   v16f_t acc = v16f_t{};
-#pragma unroll
-  for (int ch = 0; ch < FR_MAXCH; ++ch) {
-    if (ch >= nch) break;
+  const auto chunk = [&](auto ich) {
+    constexpr int ch = decltype(ich)::value;
     // Chunk ch, its weights and the scales have landed when only the loads issued after A(ch) are pending (4 per
     // weight group, NA per activation group): ch = 0: W1 A1 W2 W3; ch = 1: W2 W3 A2; ch = 2: A3; each where it
     // exists.
-    const int later = ch == 0   ? 4 * ((1 < nch) + (2 < nch) + (3 < nch)) + NA * (1 < nch)
-                      : ch == 1 ? 4 * ((2 < nch) + (3 < nch)) + NA * (2 < nch)
-                      : ch == 2 ? NA * (3 < nch)
-                                : 0;
-    switch (later) {
-      case 16: wait_vm<16>(); break;
-      case 14: wait_vm<14>(); break;
-      case 12: wait_vm<12>(); break;
-      case 10: wait_vm<10>(); break;
-      case 8: wait_vm<8>(); break;
-      case 6: wait_vm<6>(); break;
-      case 4: wait_vm<4>(); break;
-      case 2: wait_vm<2>(); break;
-      default: wait_vm<0>();
-    }
+    constexpr int later = ch == 0   ? 4 * ((1 < NCH) + (2 < NCH) + (3 < NCH)) + NA * (1 < NCH)
+                          : ch == 1 ? 4 * ((2 < NCH) + (3 < NCH)) + NA * (2 < NCH)
+                          : ch == 2 ? NA * (3 < NCH)
+                                    : 0;
+    wait_vm<later>();
     vlanded(b[ch]);
     if (ch == 0) {
       vlanded(swv);
@@ -604,11 +596,15 @@ __global__ __launch_bounds__(1024) void fp8_rows_kernel(Fp8GemmArgs p) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[i] += raw[i] * (ssa[(8 * (i / 4) + 4 * h + (i % 4)) * KS + kb] * sw);
     }
-    if (ch + 2 < nch) {
+    if constexpr (ch + 2 < NCH) {
       __syncthreads();  // every wave is done with slot ch & 1
       issue_a(ch + 2);
     }
-  }
+  };
+  chunk(std::integral_constant<int, 0>{});
+  if constexpr (NCH > 1) chunk(std::integral_constant<int, 1>{});
+  if constexpr (NCH > 2) chunk(std::integral_constant<int, 2>{});
+  if constexpr (NCH > 3) chunk(std::integral_constant<int, 3>{});
   // The KP parts added in part order through LDS: wave (chh, kh) adds elements CH kh .. CH kh + CH - 1 of its column
   // half's lanes (lane stride 17 floats for 4-byte reads, 18 for 8-byte ones: a half-wave's reads cover the 64 banks
   // once).
@@ -657,7 +653,11 @@ bool fp8_rows_fits(const Fp8GemmArgs& a) {
 template <int CH>
 static void launch_fp8_rows_t(const Fp8GemmArgs& a, hipStream_t st) {
   const size_t lds = Fp8Rows<CH>::lds(a.K);
-  auto* kern = &fp8_rows_kernel<CH>;
+  const int nch = (a.K / 128 + Fp8Rows<CH>::KP - 1) / Fp8Rows<CH>::KP;  // 1..FR_MAXCH (fp8_rows_fits)
+  auto* kern = nch == 1   ? &fp8_rows_kernel<CH, 1>
+               : nch == 2 ? &fp8_rows_kernel<CH, 2>
+               : nch == 3 ? &fp8_rows_kernel<CH, 3>
+                          : &fp8_rows_kernel<CH, 4>;
   UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                int(lds)));
   kern<<<dim3(unsigned(a.N / Fp8Rows<CH>::W * ((a.M + 31) / 32))), 1024, lds, st>>>(a);

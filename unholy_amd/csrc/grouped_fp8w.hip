@@ -23,6 +23,7 @@
 // global -> LDS loads (two workgroups per CU); bf16 MFMA 32x32x16. A wave's columns lie in one 128-row weight block
 // and a stage in one 128-input block, so the weight scale is one value per stage, folded into the dequantization.
 #include <stdexcept>
+#include <type_traits>
 #include <string>
 
 #include "common.hpp"
@@ -157,14 +158,16 @@ struct GroupedRows {
   static_assert(TR * KR * 2 == GR_SLOT, "one chunk fills a slot");
 };
 
-template <int CH, int TR>
+// NCH = the chunk count, ceil((K / 128) / KP) (1..GR_MAXCH): a template parameter, so that the issue order and every
+// counted wait are fixed at compile time and no branch depends on how many loads are outstanding.
+template <int CH, int TR, int NCH>
 __global__ __launch_bounds__(1024) void grouped_fp8w_rows_kernel(const bf16* a, const uint8_t* w, const uint8_t* sw,
                                                                  bf16* c, int M, int G, int R, int K) {
   using T = GroupedRows<CH, TR>;
   constexpr int KP = T::KP, KR = T::KR, PPR = T::PPR;
   extern __shared__ __align__(16) uint8_t smem[];
-  const int N = G * R, KS = K / 128, nch = (KS + KP - 1) / KP;  // nch <= GR_MAXCH
-  if (nch < 1) return;  // (K % 128 == 0, K > 0 on the host) no load is ever left pending past the chunk loop
+  static_assert(NCH >= 1 && NCH <= GR_MAXCH);
+  const int N = G * R, KS = K / 128;  // the host launches NCH = ceil(KS / KP)
   const int nw = gridDim.x, lin = blockIdx.x;
   const int wi = nw % 8 ? lin : (lin & 7) * (nw >> 3) + (lin >> 3);
   const int RT = (M + TR - 1) / TR, rt = wi % RT, bx = wi / RT, row0 = rt * TR;
@@ -194,7 +197,7 @@ __global__ __launch_bounds__(1024) void grouped_fp8w_rows_kernel(const bf16* a, 
       dma16(a, rowoff[i] + uint32_t(min(ch * KR + pin[i], K - 8)) * 2u,
             lds0 + uint32_t((ch & 1) * GR_SLOT + (wave * 4 + i) * 1024));
   };
-  v4i b[GR_MAXCH][4];
+  v4i b[NCH][4];
   const auto load_w = [&](int u) {
     const uint8_t* p = wld + min(u * KP + kh, KS - 1) * 128;
 #pragma unroll
@@ -205,30 +208,23 @@ __global__ __launch_bounds__(1024) void grouped_fp8w_rows_kernel(const bf16* a, 
   uint32_t sv = vload_u8(swrow + min(min(lane, GR_MAXCH - 1) * KP + kh, KS - 1));
   load_w(0);
   issue_a(0);
-  if (nch > 1) {
+  if constexpr (NCH > 1) {
     load_w(1);
     issue_a(1);
   }
-  if (nch > 2) load_w(2);
-  if (nch > 3) load_w(3);
+  if constexpr (NCH > 2) load_w(2);
+  if constexpr (NCH > 3) load_w(3);
   const int r = l32 & (TR - 1);
   v16f_t acc = v16f_t{};
-#pragma unroll
-  for (int ch = 0; ch < GR_MAXCH; ++ch) {
-    if (ch >= nch) break;
+  const auto chunk = [&](auto ich) {
+    constexpr int ch = decltype(ich)::value;
     // Chunk ch, its weights and the scales have landed when only the loads issued after A(ch) are pending (4 per
     // group): ch = 0: W1 A1 W2 W3; ch = 1: W2 W3 A2; ch = 2: A3; each where it exists.
-    const int later = ch == 0 ? (1 < nch) * 2 + (2 < nch) + (3 < nch)
-                      : ch == 1 ? (2 < nch) * 2 + (3 < nch)
-                      : ch == 2 ? (3 < nch)
-                                : 0;
-    switch (later) {
-      case 4: wait_vm<16>(); break;
-      case 3: wait_vm<12>(); break;
-      case 2: wait_vm<8>(); break;
-      case 1: wait_vm<4>(); break;
-      default: wait_vm<0>();
-    }
+    constexpr int later = 4 * (ch == 0   ? (1 < NCH) * 2 + (2 < NCH) + (3 < NCH)
+                               : ch == 1 ? (2 < NCH) * 2 + (3 < NCH)
+                               : ch == 2 ? (3 < NCH)
+                                         : 0);
+    wait_vm<later>();
     vlanded(b[ch]);
     vlanded(sv);
     __syncthreads();  // every wave's part of chunk ch has landed
@@ -254,11 +250,15 @@ __global__ __launch_bounds__(1024) void grouped_fp8w_rows_kernel(const bf16* a, 
         acc = mfma32_bf16(af, bf, acc);
       }
     }
-    if (ch + 2 < nch) {
+    if constexpr (ch + 2 < NCH) {
       __syncthreads();  // every wave is done with slot ch & 1
       issue_a(ch + 2);
     }
-  }
+  };
+  chunk(std::integral_constant<int, 0>{});
+  if constexpr (NCH > 1) chunk(std::integral_constant<int, 1>{});
+  if constexpr (NCH > 2) chunk(std::integral_constant<int, 2>{});
+  if constexpr (NCH > 3) chunk(std::integral_constant<int, 3>{});
   // The KP parts added in part order through LDS, shared by all waves: wave (chh, kh) adds elements CH kh ..
   // CH kh + CH - 1 of its column half's lanes. Lane stride 18 floats for 8-byte reads (CH 2), 17 for 4-byte ones
   // (CH 1): a half-wave's reads cover the 64 banks once.
@@ -303,7 +303,11 @@ template <int CH, int TR>
 void launch_rows_t(const bf16* a, const uint8_t* w, const uint8_t* sw, bf16* c, int M, int G, int R, int K,
                    hipStream_t st) {
   const size_t lds = 2 * size_t(GR_SLOT);
-  auto* kern = &grouped_fp8w_rows_kernel<CH, TR>;
+  const int nch = (K / 128 + GroupedRows<CH, TR>::KP - 1) / GroupedRows<CH, TR>::KP;  // 1..GR_MAXCH (rows_fits)
+  auto* kern = nch == 1   ? &grouped_fp8w_rows_kernel<CH, TR, 1>
+               : nch == 2 ? &grouped_fp8w_rows_kernel<CH, TR, 2>
+               : nch == 3 ? &grouped_fp8w_rows_kernel<CH, TR, 3>
+                          : &grouped_fp8w_rows_kernel<CH, TR, 4>;
   UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                int(lds)));
   kern<<<dim3(unsigned(G * R / GroupedRows<CH, TR>::W * ((M + TR - 1) / TR))), 1024, lds, st>>>(a, w, sw, c, M, G, R,

@@ -37,26 +37,31 @@ struct AStage {
 
   // No branches around the loads (rows past the tile re-read its last row and are zeroed in store()): divergent
   // control flow here would make the compiler drain every outstanding load, the weight prefetch included.
-  uint32_t rowoff[CH];  // element offset of each item's row (loop-invariant: no dependent loads in the stage loop)
+  // Element offset of each item's row (loop-invariant: no dependent loads in the stage loop). Gathered rows (AM 2)
+  // keep 64-bit offsets (row index x ldx can pass 2^32); the others are relative to the tile's first row (row0 K).
+  std::conditional_t<AM == 2, size_t, uint32_t> rowoff[CH];
+  size_t base = 0;
 
   __device__ __forceinline__ void rows(const MxGemvArgs& a, size_t row0, int M, int tid) {
+    if constexpr (AM != 2) base = row0 * size_t(a.K);
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int r = min((tid + i * NT) / 8, M - 1);
-      rowoff[i] = AM == 2 ? uint32_t(a.x_rows ? a.x_rows[row0 + r] : int(row0 + r)) * uint32_t(a.ldx)
-                          : uint32_t(row0 + r) * uint32_t(a.K);
+      if constexpr (AM == 2) rowoff[i] = size_t(a.x_rows ? a.x_rows[row0 + r] : int(row0 + r)) * size_t(a.ldx);
+      else rowoff[i] = uint32_t(r) * uint32_t(a.K);
     }
   }
 
   __device__ __forceinline__ void load(const MxGemvArgs& a, int s, int tid) {
-    const auto qbase = as_global(a.aq + size_t(s) * GM_KS);  // AM 0 (uniform per stage)
-    const auto xbase = as_global(a.xa + size_t(s) * GM_KS);  // AM 1, 2
+    const auto qbase = as_global(a.aq + base + size_t(s) * GM_KS);  // AM 0 (uniform per stage)
+    const auto xbase = as_global(a.xa + base + size_t(s) * GM_KS);  // AM 1, 2
+    const auto sbase = as_global(a.as + base / 128 + size_t(s));    // AM 0: (row * K) / 128 = row * K/128
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const uint32_t part = uint32_t((tid + i * NT) % 8);
       if constexpr (AM == 0) {
         raw[i][0] = *reinterpret_cast<gptr<v4i>>(qbase + (rowoff[i] + part * 16));
-        sc[i] = *(as_global(a.as) + (rowoff[i] / uint32_t(128) + uint32_t(s)));  // (row * K) / 128 = row * K/128
+        sc[i] = *(sbase + rowoff[i] / uint32_t(128));
       } else {
         raw[i][0] = *reinterpret_cast<gptr<v4i>>(xbase + (rowoff[i] + part * 16));
         raw[i][1] = *reinterpret_cast<gptr<v4i>>(xbase + (rowoff[i] + part * 16 + 8));
@@ -383,8 +388,10 @@ __device__ __forceinline__ void gp_epilogue(const MxGemvArgs& a, uint8_t* smem, 
       uint16_t* sc = reinterpret_cast<uint16_t*>(smem);
       each([&](int row, int col, float v) { sc[row * GP_LDC1 + c0 + col] = f32_to_bf16(v); });
       __syncthreads();
-      for (int e = tid; e < M * 32; e += 256) {
-        const int r = e / 32, c8 = (e % 32) * 8;
+      // 256 columns, or 128 in the last block of a matrix with N % 256 == 128 (bf16-row kernel only)
+      const int p8 = min(256, N - bx * 256) / 8;
+      for (int e = tid; e < M * p8; e += 256) {
+        const int r = e / p8, c8 = (e % p8) * 8;
         *reinterpret_cast<uint4*>(a.out[0] + (row0 + r) * a.ldo + bx * 256 + c8) =
             *reinterpret_cast<const uint4*>(sc + r * GP_LDC1 + c8);
       }
@@ -462,18 +469,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     const int M = min(128, tile.rows - rg);
     const size_t row0 = size_t(tile.row0) + rg;
     __syncthreads();  // the previous row group's LDS use is over
-    uint32_t aoff[4];
+    // Each lane's A source in 16-byte units from a.aq (a gathered row's byte offset can pass 4 GiB).
+    uint32_t a16[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int slot = (wave * 4 + i) * 64 + lane, r = slot >> 3, p = (slot & 7) ^ lds_swz(r);
       const int rr = min(r, M - 1);  // rows past the tile repeat its last
-      aoff[i] = (a.x_rows ? uint32_t(a.x_rows[row0 + rr]) : uint32_t(rr)) * uint32_t(K) + uint32_t(p * 16);
+      a16[i] = uint32_t(a.x_rows ? a.x_rows[row0 + rr] : int(row0 + rr)) * uint32_t(K / 16) + uint32_t(p);
     }
-    const uint8_t* arow = a.x_rows ? a.aq : a.aq + row0 * size_t(K);
     const auto issue = [&](int s) {
       const uint32_t st = __builtin_amdgcn_readfirstlane(lds0 + uint32_t((s % GP_S) * GP_STAGE));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dma16(arow + s * 128, aoff[i], st + uint32_t(wave * 4 + i) * 1024);
+      for (int i = 0; i < 4; ++i) dma16_g(a.aq + s * 128, a16[i], st + uint32_t(wave * 4 + i) * 1024);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int u = wave * 4 + i, q = u >> 3, j = (u >> 2) & 1, c = u & 3;
@@ -647,6 +654,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
 //   B   8 KB: 8 blocks of 1 KB = (projection or column half q, 32-column block c), slot h * 32 + n <- piece 2n + h;
 //   Bs 512 B: the e8m0 weight scales of projection q at q * 256 in their global order.
 // Every wave issues 4 A, 2 B and 1 scale load per stage (7 vm operations).
+constexpr int kSkinnyMaxRows = 64;  // mx_grouped_gemm's max_rows bound for the GEMV route
 constexpr int GB_KS = 64, GB_A = 128 * 128, GB_B = 8 * 1024, GB_BS = 512;
 constexpr int GB_STAGE = GB_A + GB_B + GB_BS;
 constexpr int GB_S = 3, GB_RING = GB_S * GB_STAGE;
@@ -672,7 +680,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // column quarter
   const int cq = wave, q_own = cq >> 1;
-  const int colq0 = NP == 2 ? bx * 128 : bx * 256, colq_step = NP == 2 ? 0 : 128;
+  // NP 1: columns bx 256 .. + 255 as two 128-column halves; the last block of a matrix with N % 256 == 128 has only
+  // the first half, and its second-half waves stream that half again (their results are not stored).
+  const int colq0 = NP == 2 ? bx * 128 : bx * 256, colq_step = NP == 2 || colq0 + 128 >= N ? 0 : 128;
   const size_t cslab = size_t(ntn) * 512, sslab = size_t(ntn) * 32;
   const uint32_t lds0 = lds_addr(smem);
   const uint32_t boff = uint32_t((l32 * 2 + h) * 16);  // B block: slot h*32+n <- piece 2n+h
@@ -685,24 +695,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
   // of column block cb (b = 0, 1) the u16 at s_lane + cb * 32.
   const uint32_t b_lane = uint32_t(GB_A + q_own * 4096 + (cq & 1) * 2048 + m16 * 16 + 4 * g);
   const uint32_t s_lane = uint32_t(GB_A + GB_B + q_own * 256 + (cq & 1) * 128 + m16 * 2);
-  const uint32_t row_bytes = uint32_t(K) * 2u;
 
   for (int rg = 0; rg < tile.rows; rg += 128) {
     const int M = min(128, tile.rows - rg);
     const size_t row0 = size_t(tile.row0) + rg;
     __syncthreads();  // the previous row group's LDS use is over
-    uint32_t aoff[4];
+    // Each lane's A source in 16-byte units from a.xa (a gathered row's byte offset can pass 4 GiB).
+    uint32_t a16[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int slot = (wave * 4 + i) * 64 + lane, r = slot >> 3, p = (slot & 7) ^ lds_swz(r);
       const int rr = min(r, M - 1);  // rows past the tile repeat its last
-      aoff[i] = (a.x_rows ? uint32_t(a.x_rows[row0 + rr]) : uint32_t(rr)) * row_bytes + uint32_t(p * 16);
+      a16[i] = uint32_t(a.x_rows ? a.x_rows[row0 + rr] : int(row0 + rr)) * uint32_t(K / 8) + uint32_t(p);
     }
-    const uint8_t* arow = reinterpret_cast<const uint8_t*>(a.x_rows ? a.xa : a.xa + row0 * size_t(K));
     const auto issue = [&](int s) {
       const uint32_t st = __builtin_amdgcn_readfirstlane(lds0 + uint32_t((s % GB_S) * GB_STAGE));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dma16(arow + s * 128, aoff[i], st + uint32_t(wave * 4 + i) * 1024);
+      for (int i = 0; i < 4; ++i) dma16_g(a.xa + s * 64, a16[i], st + uint32_t(wave * 4 + i) * 1024);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int u = wave * 2 + i, q = u >> 2, c = u & 3;
@@ -801,7 +810,7 @@ void launch_pipe_bf16_t(const MxGemvArgs& a, int ntiles, hipStream_t st) {
                                int(lds)));
   MxGemvArgs b = a;
   b.ntiles = ntiles;
-  kern<<<tile_grid(a.N / (NP == 2 ? 128 : 256), ntiles), 256, lds, st>>>(b);
+  kern<<<tile_grid(NP == 2 ? a.N / 128 : (a.N + 255) / 256, ntiles), 256, lds, st>>>(b);
   UH_CHECK_LAUNCH();
 }
 
@@ -833,9 +842,7 @@ void launch_mx_gemm(const MxGemvArgs& a, int ntiles, int amode, hipStream_t st) 
   if (ntiles <= 0) return;
   // bf16 activation rows (amode 1) take the 64-input-stage pipelined kernel: K % 64 as the reference asks
   // (mx_moe.hip:1045); the other kernels stage 128 inputs at a time.
-  const bool glu_ = a.hh || a.hq;  // (two projections without the epilogue run as two one-projection launches)
-  const bool pipe16 = amode == 1 && !pipe_disabled() && a.N % 128 == 0 && (glu_ || a.N % 256 == 0) &&
-                      a.K % GB_KS == 0;
+  const bool pipe16 = amode == 1 && !pipe_disabled() && a.N % 128 == 0 && a.K % GB_KS == 0 && !a.out32;
   if (a.K <= 0 || a.N <= 0 || a.N % 128 || (!pipe16 && a.K % GM_KS))
     throw std::runtime_error("mx_grouped_gemm: K % 128 (K % 64 for bf16 rows) or N % 128");
   const bool np2 = a.w_tab[1] != nullptr, glu = a.hh || a.hq;
@@ -922,12 +929,22 @@ MxGemvArgs gemm_args(const bf16* xa, const uint8_t* q, const uint8_t* qs, int K,
 }
 }  // namespace
 
+// max_rows: the caller's bound on any tile's rows (the reference's verify steps pass the step's token count, an expert
+// having at most one row per token). Up to 64 rows (and K % 128) the tiles take the grouped GEMV in groups of up to
+// 16 rows, each group streaming the tile's weights once, instead of a 128-row GEMM tile that is mostly padding: the
+// same per-output arithmetic (every 32-input block's exact sum added to the fp32 accumulator in input order), so the
+// outputs are the GEMM's bit for bit. Larger bounds, or K % 128 != 0, take the GEMM.
 void mx_grouped_gemm(const bf16* xa, int K, const Exl3Tile* tiles, int ntiles, const uint8_t* const* w_tab,
                      const uint8_t* const* s_tab, bf16* out, int ldo, int N, hipStream_t st, const int* ntiles_dev,
-                     const uint8_t* const* w_tab2, const uint8_t* const* s_tab2, bf16* out2, int) {
-  launch_mx_gemm(gemm_args(xa, nullptr, nullptr, K, tiles, w_tab, s_tab, out, ldo, N, ntiles_dev, w_tab2, s_tab2, out2,
-                           MxGlu{}),
-                 ntiles, 1, st);
+                     const uint8_t* const* w_tab2, const uint8_t* const* s_tab2, bf16* out2, int max_rows) {
+  MxGemvArgs a = gemm_args(xa, nullptr, nullptr, K, tiles, w_tab, s_tab, out, ldo, N, ntiles_dev, w_tab2, s_tab2, out2,
+                           MxGlu{});
+  if (max_rows >= 1 && max_rows <= kSkinnyMaxRows && K % 128 == 0 && K > 0 && N % 16 == 0) {
+    a.rows_cap = std::min(max_rows, 16);
+    launch_mx_gemv(a, ntiles, 1, st);
+    return;
+  }
+  launch_mx_gemm(a, ntiles, 1, st);
 }
 
 void mx_grouped_gemm_q(const uint8_t* q, const uint8_t* qs, int K, const Exl3Tile* tiles, int ntiles,
@@ -985,9 +1002,8 @@ void mx_grouped_gemm_rows(const bf16* xa, const int32_t* x_rows, int K, const Ex
   MxGemvArgs a = gemm_args(xa, nullptr, nullptr, K, tiles, w_tab, s_tab, out, ldo, N, ntiles_dev, w_tab2, s_tab2, out2,
                            glu);
   a.x_rows = x_rows;
-  if (x_rows && (pipe_disabled() || K % GB_KS || N % 128 || (!(glu.hh || glu.hq) && N % 256)))
-    throw std::runtime_error("mx_grouped_gemm_rows: x_rows needs the pipelined kernel (K % 64, N % 128; N % 256 "
-                             "without the SwiGLU epilogue)");
+  if (x_rows && (pipe_disabled() || K % GB_KS || N % 128))
+    throw std::runtime_error("mx_grouped_gemm_rows: x_rows needs the pipelined kernel (K % 64, N % 128)");
   launch_mx_gemm(a, ntiles, 1, st);
 }
 

@@ -226,7 +226,15 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
       for (int i = 0; i < GV_PF; ++i) load_step(min(sb + i, se - 1), i);  // fewer than GV_PF steps: re-read the last
     }
     __syncthreads();
-    if constexpr (AM != 0) {
+    if constexpr (AM == 1 && ABF) {
+      // bf16 rows held as they are: for fake-quantized rows (mx_xform_in's) these are exactly the values the codes
+      // and scales recovered below would give back, and other bf16 rows are used as given.
+      const int total = M * (K / 8);
+      for (int i = tid; i < total; i += NT) {
+        const int m = i / (K / 8), c = (i % (K / 8)) * 8;
+        *reinterpret_cast<uint4*>(sAb + m * ldAb + c) = *reinterpret_cast<const uint4*>(a.xa + (row0 + m) * size_t(K) + c);
+      }
+    } else if constexpr (AM != 0) {
       // 8 values per thread; 16 consecutive threads hold one 128-block (K / 8 is a multiple of 16).
       const int total = M * (K / 8);
       for (int base = 0; base < total; base += NT) {

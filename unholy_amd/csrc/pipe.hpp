@@ -47,6 +47,16 @@ __device__ __forceinline__ void dma16_nt(const void* base, uint32_t voff, uint32
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase), "s"(lds)
                : "memory", "m0");
 }
+// dma16 of a row gather: lane source base + 16 * off16 (64-bit arithmetic, so a gathered row's byte offset may pass
+// 4 GiB, where the 32-bit per-lane offset of dma16 would wrap). off16 passes through an empty asm statement at each
+// call, so the compiler rebuilds the 64-bit address in two temporary registers per load instead of keeping one
+// register pair per lane live across the K loop.
+__device__ __forceinline__ void dma16_g(const void* base, uint32_t off16, uint32_t lds) {
+  asm volatile("" : "+v"(off16));
+  const uint8_t* addr = static_cast<const uint8_t*>(base) + (size_t(off16) << 4);
+  lds = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(addr), "s"(lds) : "memory", "m0");
+}
 // The same with 4 bytes per lane (to LDS lds + 4 * lane): a gather of one dword per lane.
 __device__ __forceinline__ void dma4(const void* base, uint32_t voff, uint32_t lds) {
   const uint64_t sbase = uniform_ptr(base);
