@@ -356,6 +356,7 @@ constexpr int GP_MAX_KS = (80 * 1024 - GP_RING) / 128;  // activation scales [KS
 constexpr int GP_LDC1 = 256 + 8, GP_LDC2 = 128 + 8;
 constexpr int GP_C1 = 128 * GP_LDC1 * 2, GP_C2 = 2 * 128 * GP_LDC2 * 2;
 static_assert(GP_C1 <= GP_RING, "the bf16 C tile reuses the ring");
+constexpr int GP_ROWS = 1024;  // the SwiGLU epilogue's per-row weights and flags, after the C tiles
 
 // The bf16 / fp32 / SwiGLU epilogue of the pipelined kernels. each(f) calls f(row, column within the wave's 64, value)
 // for every accumulator element; the ring is reused as the C tile.
@@ -399,11 +400,26 @@ __device__ __forceinline__ void gp_epilogue(const MxGemvArgs& a, uint8_t* smem, 
   } else {
     // bf16 g (w1) and u (w3) tiles in LDS, then 8 consecutive outputs of one row per thread: h = bf16(SwiGLU(g, u)),
     // the row's amax over its 128 outputs (16 threads: a DPP row max), fake quantization, 16-byte stores.
+    // Each row's routing weight and whether its expert's w2 is here, loaded once per row (threads 0..127) into LDS
+    // beside the tiles, so that the loop below has no dependent global loads.
     uint16_t* const tg = reinterpret_cast<uint16_t*>(smem);
     uint16_t* const tu = tg + 128 * GP_LDC2;
     uint16_t* const mine = q_own ? tu : tg;
+    float* const rw_lds = reinterpret_cast<float*>(smem + GP_C2);
+    int* const live_lds = reinterpret_cast<int*>(smem + GP_C2 + 512);
+    float rw_t = 0.0f;
+    int live_t = 1;
+    if (tid < M) {
+      const size_t row = row0 + tid;
+      if (a.gw) rw_t = a.gw[row];
+      if (a.gs_tab) live_t = a.gs_tab[a.grow_expert[row]] != nullptr;
+    }
     const int chh = cq & 1;
     each([&](int row, int col, float v) { mine[row * GP_LDC2 + chh * 64 + col] = f32_to_bf16(v); });
+    if (tid < 128) {
+      rw_lds[tid] = rw_t;
+      live_lds[tid] = live_t;
+    }
     __syncthreads();
     for (int e0 = 0; e0 < M * 16; e0 += 256) {  // uniform bound: every 16-lane group is whole
       const int e = e0 + tid, r = min(e / 16, M - 1), c8 = (e % 16) * 8;
@@ -411,7 +427,7 @@ __device__ __forceinline__ void gp_epilogue(const MxGemvArgs& a, uint8_t* smem, 
       const uint4 gv4 = *reinterpret_cast<const uint4*>(tg + r * GP_LDC2 + c8);
       const uint4 uv4 = *reinterpret_cast<const uint4*>(tu + r * GP_LDC2 + c8);
       const uint32_t gw4[4] = {gv4.x, gv4.y, gv4.z, gv4.w}, uw4[4] = {uv4.x, uv4.y, uv4.z, uv4.w};
-      const float w = a.gw ? a.gw[row] : 0.0f;
+      const float w = rw_lds[r];
       float hv[8], am = 0.0f;
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
@@ -425,7 +441,7 @@ __device__ __forceinline__ void gp_epilogue(const MxGemvArgs& a, uint8_t* smem, 
       const size_t oc = row * a.ldo + size_t(bx) * 128 + c8;
       if (a.out[0]) *reinterpret_cast<uint4*>(a.out[0] + oc) = gv4;
       if (a.out[1]) *reinterpret_cast<uint4*>(a.out[1] + oc) = uv4;
-      if (a.gs_tab && !a.gs_tab[a.grow_expert[row]]) continue;
+      if (!live_lds[r]) continue;
       const Fp8Block blk = fp8_block_scale(am);
       uint32_t qb[2];
       fp8_codes8(hv, blk, qb[0], qb[1]);
@@ -658,7 +674,8 @@ constexpr int kSkinnyMaxRows = 64;  // mx_grouped_gemm's max_rows bound for the 
 constexpr int GB_KS = 64, GB_A = 128 * 128, GB_B = 8 * 1024, GB_BS = 512;
 constexpr int GB_STAGE = GB_A + GB_B + GB_BS;
 constexpr int GB_S = 3, GB_RING = GB_S * GB_STAGE;
-static_assert(GP_C1 <= GB_RING && GP_C2 <= GB_RING && 64 * (256 + 4) * 4 <= GB_RING, "the C tiles reuse the ring");
+static_assert(GP_C1 <= GB_RING && GP_C2 + GP_ROWS <= GB_RING && 64 * (256 + 4) * 4 <= GB_RING,
+              "the C tiles reuse the ring");
 
 template <int NP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mx_gemm_pipe_bf16_kernel(MxGemvArgs a) {
@@ -792,7 +809,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
 
 template <int NP>
 void launch_pipe_t(const MxGemvArgs& a, int ntiles, hipStream_t st) {
-  const size_t lds = std::max<size_t>(size_t(GP_RING) + size_t(128) * (a.K / 128), NP == 2 ? GP_C2 : GP_C1);
+  const size_t lds = std::max<size_t>(size_t(GP_RING) + size_t(128) * (a.K / 128), NP == 2 ? GP_C2 + GP_ROWS : GP_C1);
   auto* kern = mx_gemm_exact() ? &mx_gemm_pipe_kernel<NP, false> : &mx_gemm_pipe_kernel<NP, true>;
   UH_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                int(lds)));
