@@ -46,8 +46,9 @@ void mx_swiglu(const bf16* g, const bf16* u, const float* w, const int32_t* row_
                bf16* hh, int P, int I, float limit, hipStream_t st);
 
 // out[r] = xa[r] @ W[e]^T over each tile's rows; second projection (w3) of the same rows with w_tab2/s_tab2/out2.
-// Ref mx_moe.hpp:49-52. Preconditions: K % 64 == 0 and N % 128 == 0, the reference's (mx_moe.hip:1045), when N % 256
-// == 0 (the 64-input-stage kernel for bf16 rows); otherwise K % 128 == 0 (the register-staged kernel).
+// Ref mx_moe.hpp:49-52. Preconditions: K % 64 == 0 and N % 128 == 0, the reference's (mx_moe.hip:1045). max_rows:
+// the caller's bound on any tile's rows; <= 64 with K % 128 == 0 runs the tiles on the grouped GEMV 16 rows at a time
+// (the reference's skinny route, mx_moe.hip:1054), with the same outputs.
 void mx_grouped_gemm(const bf16* xa, int K, const Exl3Tile* tiles, int ntiles, const uint8_t* const* w_tab,
                      const uint8_t* const* s_tab, bf16* out, int ldo, int N, hipStream_t st,
                      const int* ntiles_dev = nullptr, const uint8_t* const* w_tab2 = nullptr,

@@ -956,7 +956,7 @@ void mx_grouped_gemm(const bf16* xa, int K, const Exl3Tile* tiles, int ntiles, c
                      const uint8_t* const* w_tab2, const uint8_t* const* s_tab2, bf16* out2, int max_rows) {
   MxGemvArgs a = gemm_args(xa, nullptr, nullptr, K, tiles, w_tab, s_tab, out, ldo, N, ntiles_dev, w_tab2, s_tab2, out2,
                            MxGlu{});
-  if (max_rows >= 1 && max_rows <= kSkinnyMaxRows && K % 128 == 0 && K > 0 && N % 16 == 0) {
+  if (max_rows >= 1 && max_rows <= kSkinnyMaxRows && K % 128 == 0 && K > 0 && N % 16 == 0 && mx_skinny_enabled()) {
     a.rows_cap = std::min(max_rows, 16);
     launch_mx_gemv(a, ntiles, 1, st);
     return;

@@ -798,7 +798,15 @@ int mx_gemv_max_tokens() {
   }();
   return v;
 }
-bool mx_skinny_enabled() { return true; }
+// mx_grouped_gemm's small-tile route (max_rows <= 64 on the grouped GEMV); UNHOLY_MX_SKINNY=0 turns it off, as in the
+// reference (mx_moe.hip:1033-1039).
+bool mx_skinny_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("UNHOLY_MX_SKINNY");
+    return !(v && v[0] == '0' && v[1] == 0);
+  }();
+  return on;
+}
 bool mx_gemm_rb() { return false; }
 void mx_gemm_force_rb(int) {}
 void mx_gemm_rb_double_buffer(int) {}
