@@ -16,6 +16,9 @@ using bf16 = uint16_t;
 void act_quant_fp8(const bf16* x, int ldx, uint8_t* q, uint8_t* s, int rows, int cols, int block, hipStream_t st);
 // In-place quantize + dequantize to bf16. Ref ref.hpp:130.
 void fake_quant_fp8(bf16* x, int ldx, int rows, int cols, int block, hipStream_t st);
+// In-place e2m1 quantize + dequantize per block (the attention indexer's query operand; block 32 there). Ref
+// ref.hpp:25. block % 8 == 0 (the reference's block is 32 or a multiple), cols % block == 0.
+void fake_quant_fp4(bf16* x, int ldx, int rows, int cols, int block, hipStream_t st);
 // act_quant with fp32 scales (kernel.py act_quant, scale_fmt=None): s = max(amax, 1e-4) * fp32(1/448).
 void act_quant_fp8_f32s(const bf16* x, int ldx, uint8_t* q, float* s, int rows, int cols, int block, hipStream_t st);
 

@@ -214,6 +214,8 @@ int uh_moe_combine(const uint16_t* pair_out, const int32_t* pidx, const uint16_t
 int uh_act_quant_fp8(const uint16_t* x, int ldx, uint8_t* q, uint8_t* s, int rows, int cols, int block, void* stream);
 /* ref.hpp:130 */
 int uh_fake_quant_fp8(uint16_t* x, int ldx, int rows, int cols, int block, void* stream);
+/* ref.hpp:25 */
+int uh_fake_quant_fp4(uint16_t* x, int ldx, int rows, int cols, int block, void* stream);
 /* tools/ref/oracle/kernel.py:43-55 with scale_fmt=None (fp32 scales) */
 int uh_act_quant_fp8_f32s(const uint16_t* x, int ldx, uint8_t* q, float* s, int rows, int cols, int block,
                           void* stream);

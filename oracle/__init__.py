@@ -33,6 +33,7 @@ _SIGS = {
     "or_f32_to_e4m3_array": (None, [_P, _P, ctypes.c_size_t]),
     "or_act_quant_fp8": (None, [_P, _I, _P, _P, _I, _I, _I]),
     "or_fake_quant_fp8": (None, [_P, _I, _I, _I, _I]),
+    "or_fake_quant_fp4": (None, [_P, _I, _I, _I, _I]),
     "or_act_quant_fp8_f32s": (None, [_P, _I, _P, _P, _I, _I, _I]),
     "or_repack": (None, [_P, _P, _P, _P, _I, _I]),
     "or_unrepack": (None, [_P, _P, _P, _P, _I, _I]),
@@ -149,6 +150,14 @@ def act_quant_fp8(x_bf16, block=128):
     s = np.empty((rows, cols // block), np.uint8)
     lib().or_act_quant_fp8(_p(x), cols, _p(q), _p(s), rows, cols, block)
     return q, s
+
+
+def fake_quant_fp4(x_bf16, block=32):
+    """bf16 [rows, cols] -> bf16 [rows, cols]: e2m1 fake quantization per block (ref_elem.hip:43-59)."""
+    x = np.array(x_bf16, dtype=np.uint16, copy=True, order="C")
+    rows, cols = x.shape
+    lib().or_fake_quant_fp4(_p(x), cols, rows, cols, block)
+    return x
 
 
 def fake_quant_fp8(x_bf16, block=128):

@@ -9,6 +9,8 @@
 //   numerics            src/kernels/dev.hip.hpp:40-127 (device codecs), src/core/half.hpp:68-96 (host twins)
 //   act_quant_fp8       src/kernels/ref_elem.hip:18-41 (e8m0 scales); tools/ref/oracle/kernel.py:43-55
 //                       (scale_fmt=None: fp32 scales amax/448)
+//   fake_quant_fp4      src/kernels/ref_elem.hip:43-59 (e2m1 per block, amax floor 6 * 2^-126), round_e2m1
+//                       dev.hip.hpp:107-119
 //   gemm_a8w4(_tiled)   src/kernels/ref_gemm.hip:15-67 (K-block partial sums), :77-99, :138-155, :180-188
 //   gemm_w8a8           src/kernels/ref_gemm.hip:130-137, :175-178; fp32-scale form: gemm_wmma.hip:89-100
 //                       (raw per-128 chain folded with acc += raw * (sa * sw))
@@ -103,6 +105,22 @@ inline uint8_t pow2_ceil_e8m0(float v) {
   const uint32_t b = f2u(v);
   const int e = int((b >> 23) & 0xff) - 127 + ((b & 0x7fffff) != 0 ? 1 : 0);
   return uint8_t(e + 127);
+}
+
+// e2m1 rounding of a scaled value, to nearest with ties to the even code (dev.hip.hpp:107-119: the midpoints 0.25,
+// 1.25, 2.5 and 5 go down, 0.75, 1.75 and 3.5 go up).
+inline float round_e2m1(float x) {
+  const float a = std::fabs(x);
+  float r;
+  if (a <= 0.25f) r = 0.0f;
+  else if (a < 0.75f) r = 0.5f;
+  else if (a <= 1.25f) r = 1.0f;
+  else if (a < 1.75f) r = 1.5f;
+  else if (a <= 2.5f) r = 2.0f;
+  else if (a < 3.5f) r = 3.0f;
+  else if (a <= 5.0f) r = 4.0f;
+  else r = 6.0f;
+  return x < 0 ? -r : r;
 }
 
 // e^x as the library computes it (IEEE operations only, so both sides produce the same bits; the reference's device
@@ -200,6 +218,21 @@ void or_act_quant_fp8(const uint16_t* x, int ldx, uint8_t* q, uint8_t* s, int ro
         q[size_t(r) * cols + size_t(b) * block + i] =
             f32_to_e4m3(std::fmin(std::fmax(bf16_to_f32(xr[i]) / sc, -448.0f), 448.0f));
       s[size_t(r) * nb + b] = se;
+    }
+}
+// In-place e2m1 fake quantization per block (ref_elem.hip:43-59): amax floored at 6 * 2^-126, sc = 2^ceil(log2(amax /
+// 6)), x = bf16(e2m1(clamp(x / sc, +-6)) * sc).
+void or_fake_quant_fp4(uint16_t* x, int ldx, int rows, int cols, int block) {
+  const int nb = cols / block;
+  for (int r = 0; r < rows; ++r)
+    for (int b = 0; b < nb; ++b) {
+      uint16_t* xr = x + size_t(r) * ldx + size_t(b) * block;
+      float amax = 0.0f;
+      for (int i = 0; i < block; ++i) amax = std::fmax(amax, std::fabs(bf16_to_f32(xr[i])));
+      amax = std::fmax(amax, 6.0f * 1.1754943508222875e-38f);
+      const float sc = e8m0_to_f32(pow2_ceil_e8m0(amax * (1.0f / 6.0f)));
+      for (int i = 0; i < block; ++i)
+        xr[i] = f32_to_bf16(round_e2m1(std::fmin(std::fmax(bf16_to_f32(xr[i]) / sc, -6.0f), 6.0f)) * sc);
     }
 }
 // In-place fake quantization: x = bf16(e4m3(x / sc) * sc) per block (ref_elem.hip:37).

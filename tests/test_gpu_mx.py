@@ -10,8 +10,9 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.helpers import from_bf16, max_abs_rms, max_rel, mx_weights, randn_bf16, rel_l2
+from tests.helpers import from_bf16, max_abs_rms, max_rel, mx_weights, randn_bf16, rel_l2, to_bf16
 from unholy_amd import call
+from unholy_amd._lib import UhError
 from unholy_amd.device import DeviceBuffer, pointer_table, synchronize
 
 pytestmark = pytest.mark.gpu
@@ -105,6 +106,30 @@ def test_act_quant_bit_exact(block):
     call("uh_act_quant_fp8_f32s", dx.ptr, 1024, q.ptr, s32.ptr, 37, 1024, block, None)
     assert np.array_equal(q.download(q32_ref.shape, np.uint8), q32_ref)
     assert np.array_equal(s32.download(s32_ref.shape, np.float32), s32_ref)
+
+
+@pytest.mark.parametrize("block,ldx", [(32, 1024), (64, 1024), (128, 1024), (32, 1029)])
+def test_fake_quant_fp4_bit_exact(block, ldx):
+    """e2m1 fake quantization in place (ref_elem.hip:43-59) against the oracle, bit for bit: random rows, an all-zero
+    and a sub-floor block, every rounding midpoint, values clamped at +-6 x scale; 16-byte rows and an odd stride (the
+    2-byte path). Columns past `cols` in the strided rows stay untouched."""
+    rng = np.random.default_rng(block + ldx)
+    rows, cols = 37, 1024
+    full = randn_bf16(rng, (rows, ldx), 3.0)
+    x = full[:, :cols]
+    x[0, :block] = 0
+    x[1, :block] = to_bf16(np.full(block, 1e-39, np.float32))
+    ties = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, -0.25, -2.5, -5.0, 6.0, -6.0], np.float32)
+    x[2, :len(ties)] = to_bf16(ties)
+    x[3, :block] = to_bf16(np.linspace(-70, 70, block, dtype=np.float32))
+    ref = oracle.fake_quant_fp4(np.ascontiguousarray(x), block)
+    dx = dev(full)
+    call("uh_fake_quant_fp4", dx.ptr, ldx, rows, cols, block, None)
+    got = dx.download(full.shape, np.uint16)
+    assert np.array_equal(got[:, :cols], ref)
+    assert np.array_equal(got[:, cols:], full[:, cols:])
+    with pytest.raises(UhError, match="block % 8"):
+        call("uh_fake_quant_fp4", dx.ptr, ldx, rows, cols, 12, None)
 
 
 def test_xform_in_gathered_rows():

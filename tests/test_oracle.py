@@ -423,3 +423,45 @@ def test_moe_forward_composition():
     got = from_bf16(out).astype(np.float64)
     rel = np.linalg.norm(got - want) / np.linalg.norm(want)
     assert rel < 5e-3, rel  # bf16 pair rows and output (2^-9 each) and the rare fp8 code flip they cause
+
+
+def _fake_quant_fp4_closed(x_bf16, block):
+    """An independent statement of e2m1 fake quantization (ref_elem.hip:43-59): per block, sc = the smallest power of
+    two >= max(amax, 6 * 2^-126) / 6 (from frexp, no logarithms), each value clamped to +-6 after division by sc and
+    moved to the nearest e2m1 grid value, a tie going to the even code (codes 0..7 = 0, .5, 1, 1.5, 2, 3, 4, 6)."""
+    grid = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0])
+    xf = from_bf16(x_bf16).astype(np.float64)
+    rows, cols = xf.shape
+    out = np.empty_like(xf)
+    for r in range(rows):
+        for b in range(cols // block):
+            v = xf[r, b * block:(b + 1) * block]
+            amax = max(np.abs(v).max(), 6.0 * 2.0 ** -126)
+            m, e = np.frexp(np.float32(amax) * np.float32(1 / 6))  # the kernel's fp32 product, then 2^ceil(log2)
+            sc = 2.0 ** (e - 1) if m == 0.5 else 2.0 ** e
+            y = np.clip(v / sc, -6.0, 6.0)
+            d = np.abs(np.abs(y)[:, None] - grid[None, :])
+            best = d.min(axis=1, keepdims=True)
+            cand = d == best
+            # a tie is between neighbouring codes, exactly one of them even
+            even = np.argmax(cand & (np.arange(8) % 2 == 0), axis=1)
+            code = np.where(cand.sum(axis=1) > 1, even, np.argmax(cand, axis=1))
+            out[r, b * block:(b + 1) * block] = np.copysign(grid[code], y) * sc
+    return out.astype(np.float32)
+
+
+@pytest.mark.parametrize("block", [32, 64, 128])
+def test_fake_quant_fp4_closed_form(block):
+    rng = np.random.default_rng(40 + block)
+    x = randn_bf16(rng, (7, 256), 3.0)
+    x[0, :block] = 0                                    # all-zero block: the amax floor
+    x[1, :block] = to_bf16(np.full(block, 1e-39, np.float32))  # below the floor
+    ties = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, -0.25, -2.5, -5.0, 6.0, -6.0], np.float32)
+    x[2, :len(ties)] = to_bf16(ties)                  # amax 6 -> sc = 1: every tie at its midpoint
+    x[3, :block] = to_bf16(np.linspace(-70, 70, block, dtype=np.float32))
+    got = from_bf16(oracle.fake_quant_fp4(x, block))
+    want = _fake_quant_fp4_closed(x, block)
+    assert np.array_equal(got.view(np.uint32) & 0x7FFFFFFF, want.view(np.uint32) & 0x7FFFFFFF)
+    assert np.array_equal(np.signbit(got) & (got != 0), np.signbit(want) & (want != 0))
+    # the ties row: midpoints to the even code
+    assert got[2, :len(ties)].tolist() == [0.0, 1.0, 1.0, 2.0, 2.0, 4.0, 4.0, -0.0, -2.0, -4.0, 6.0, -6.0]

@@ -512,6 +512,9 @@ int uh_act_quant_fp8(const uint16_t* x, int ldx, uint8_t* q, uint8_t* s, int row
 int uh_fake_quant_fp8(uint16_t* x, int ldx, int rows, int cols, int block, void* st) {
   return guard([&] { k::fake_quant_fp8(x, ldx, rows, cols, block, S(st)); });
 }
+int uh_fake_quant_fp4(uint16_t* x, int ldx, int rows, int cols, int block, void* st) {
+  return guard([&] { k::fake_quant_fp4(x, ldx, rows, cols, block, S(st)); });
+}
 int uh_act_quant_fp8_f32s(const uint16_t* x, int ldx, uint8_t* q, float* s, int rows, int cols, int block, void* st) {
   return guard([&] { k::act_quant_fp8_f32s(x, ldx, q, s, rows, cols, block, S(st)); });
 }

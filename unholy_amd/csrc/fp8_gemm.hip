@@ -717,7 +717,70 @@ void launch_fp8_gemv(const Fp8GemmArgs& a, hipStream_t st, const Fp8Parts* parts
   else launch_fp8_gemv_t<false>(a, st, pp);
 }
 
+// e2m1 fake quantization in place (the reference's ref_elem.hip:43-59): per block of `block` values, amax floored at
+// 6 * 2^-126, sc = 2^ceil(log2(amax / 6)), x = bf16(e2m1(clamp(x / sc, +-6)) * sc) with the e2m1 rounding to nearest,
+// ties to the even code. A thread per block, 8 values per 16-byte access (ldx % 8 == 0 on the host; other strides use
+// 2-byte accesses); not a hot path (the attention indexer's operand).
+__device__ __forceinline__ float round_e2m1_dev(float x) {
+  const float a = fabsf(x);
+  float r;
+  if (a <= 0.25f) r = 0.0f;
+  else if (a < 0.75f) r = 0.5f;
+  else if (a <= 1.25f) r = 1.0f;
+  else if (a < 1.75f) r = 1.5f;
+  else if (a <= 2.5f) r = 2.0f;
+  else if (a < 3.5f) r = 3.0f;
+  else if (a <= 5.0f) r = 4.0f;
+  else r = 6.0f;
+  return x < 0.0f ? -r : r;
+}
+template <bool VEC>
+__global__ __launch_bounds__(256) void fake_quant_fp4_kernel(bf16* x, int ldx, int rows, int cols, int block) {
+  const int nb = cols / block;
+  const size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (i >= size_t(rows) * nb) return;
+  bf16* xr = x + (i / nb) * size_t(ldx) + (i % nb) * size_t(block);
+  float amax = 0.0f;
+  if constexpr (VEC) {
+    for (int c = 0; c < block; c += 8) {
+      const uint4 v = *reinterpret_cast<const uint4*>(xr + c);
+      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int t = 0; t < 8; ++t) amax = fmaxf(amax, fabsf(bf16_to_f32(uint16_t(w4[t / 2] >> (16 * (t % 2))))));
+    }
+  } else {
+    for (int c = 0; c < block; ++c) amax = fmaxf(amax, fabsf(bf16_to_f32(xr[c])));
+  }
+  amax = fmaxf(amax, 6.0f * 1.1754943508222875e-38f);  // 6 * 2^-126
+  const float sc = e8m0_to_f32(pow2_ceil_e8m0(amax * (1.0f / 6.0f)));
+  const auto q = [&](uint16_t v) {
+    return f32_to_bf16(round_e2m1_dev(fminf(fmaxf(bf16_to_f32(v) / sc, -6.0f), 6.0f)) * sc);
+  };
+  if constexpr (VEC) {
+    for (int c = 0; c < block; c += 8) {
+      const uint4 v = *reinterpret_cast<const uint4*>(xr + c);
+      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) o[t] = uint32_t(q(uint16_t(w4[t]))) | (uint32_t(q(uint16_t(w4[t] >> 16))) << 16);
+      *reinterpret_cast<uint4*>(xr + c) = uint4{o[0], o[1], o[2], o[3]};
+    }
+  } else {
+    for (int c = 0; c < block; ++c) xr[c] = q(xr[c]);
+  }
+}
+
 // ---- entry points ---------------------------------------------------------------------------------------------------
+void fake_quant_fp4(bf16* x, int ldx, int rows, int cols, int block, hipStream_t st) {
+  if (rows <= 0 || cols <= 0) return;
+  if (block <= 0 || block % 8 || cols % block || ldx < cols || !x)
+    throw std::runtime_error("fake_quant_fp4: block % 8, cols % block, ldx >= cols");
+  const size_t n = size_t(rows) * (cols / block);
+  const bool vec = ldx % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  if (vec) fake_quant_fp4_kernel<true><<<cdiv(n, 256), 256, 0, st>>>(x, ldx, rows, cols, block);
+  else fake_quant_fp4_kernel<false><<<cdiv(n, 256), 256, 0, st>>>(x, ldx, rows, cols, block);
+  UH_CHECK_LAUNCH();
+}
 void act_quant_fp8(const bf16* x, int ldx, uint8_t* q, uint8_t* s, int rows, int cols, int block, hipStream_t st) {
   launch_act_quant<0>(x, ldx, q, s, rows, cols, block, st);
 }
