@@ -125,6 +125,20 @@ class MoeRunner:
                   self.out, None, None, None, self.evarr if stage_events else None)
 
 
+def bench_moe_graph(w, T, steps, warmup, rng, R=8, bias=0.0):
+    """ms per step of the same routed-expert FFN with the R rotating steps captured as one HIP graph and replayed
+    (the serving loop's form: every kernel of every step runs, the host enqueues one graph per R steps)."""
+    sets = routing_sets(rng, T, R, bias, disjoint=T <= 8)
+    r = MoeRunner(w, sets)
+
+    def fn(i, stream):
+        x, l = r.dev[i % len(r.dev)]
+        r.call("uh_mx_moe_forward", x, l, r.T, TOPK, E, D, I, r.w.table, LIMIT, r.ws, r.ws_bytes, r.out, None, None,
+               stream.handle)
+
+    return dict(ms=time_graph(fn, steps, warmup, per_graph=R), U=float(np.mean(r.U)))
+
+
 def time_steps(fn, steps, warmup, timed_fn=None):
     """Total ms of `steps` calls after `warmup` (timed_fn, if given, is the form used inside the timed region)."""
     from unholy_amd.device import Event, synchronize
@@ -612,7 +626,8 @@ def run_only(name, args, rng):
         return {"single_gemv_M1_ms": bench_single_gemv(w, 500, 50, rng)}
     if name == "decode":
         d = bench_moe(w, 8, args.steps, args.warmup, rng)
-        return {"moe_decode_T8_ms": d["ms"], "distinct_experts": d["U"]}
+        g = bench_moe_graph(w, 8, args.steps, args.warmup, np.random.default_rng(0))
+        return {"moe_decode_T8_ms": d["ms"], "moe_decode_T8_graph_ms": g["ms"], "distinct_experts": d["U"]}
     if name == "dropin":
         d8 = bench_dropin(w, 8, args.steps, args.warmup, rng)
         d64 = bench_dropin(w, 64, 50, 5, rng, bias=0.5, glu=False)
