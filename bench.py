@@ -34,7 +34,7 @@ LIMIT = 10.0
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the dominant kernel (w1/w3 GEMV, this seeded workload): FETCH_SIZE + WRITE_SIZE from two
 # rocprofv3 --pmc runs, scaled by the same counters on a 1 GiB device copy (profiles/hbm_traffic_pmc.md).
-GEMV_TRAFFIC_BYTES = 385.0e6
+GEMV_TRAFFIC_BYTES = 383.9e6
 BF16_PEAK_TFLOPS = 2500.0
 GW_G, GW_R, GW_K = 8, 1024, 4096  # the DSV4 wo_a shape (o_groups, o_lora_rank, heads x head_dim / o_groups)
 FP8_PEAK_TFLOPS = 5000.0  # the block-scaled fp8 x fp4 MFMA runs at the fp8 rate (4.29 PFLOP/s sustained, measured)
