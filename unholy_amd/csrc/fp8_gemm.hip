@@ -454,9 +454,16 @@ void launch_fp8_gemv_t(const Fp8GemmArgs& a, hipStream_t st, const Fp8Parts& pp)
 // A workgroup per 32 columns x 32 rows over the whole of K (<= 8,192), bf16 C written directly, one launch:
 // - 16 waves = 16 K parts of one 32 x 32 output tile (bf16 MFMA 32x32x16); part p takes block p of every 2,048-input
 //   chunk;
-// - the tile's activation codes go through a 2-slot LDS ring of chunks (32 rows x 2,048 codes, 64 KB) by direct
-//   global -> LDS loads; piece p (16 bytes) of row r sits at p ^ (r & 15), so a 16-lane pass of 16-byte reads covers
-//   the 64 banks once; the fp32 row scales of the tile are staged beside them;
+// - CH = 1: each wave loads the activation codes of its own K part (32 rows x 128 codes a chunk, four 1 KB loads)
+//   into its own 2-slot LDS ring by direct global -> LDS loads, and its rows' fp32 scales into registers (lane r
+//   holds row r's; a lane-crossbar read hands each accumulator row its scale). No wave waits for another before the
+//   final reduction, so a wave computes its chunks as soon as its own loads land while the others still stream;
+//   piece q (16 bytes) of row r sits at q ^ ((r >> 1) & 7), so a 16-lane pass of 16-byte reads covers the 64 banks
+//   once. The waves of a 32-row tile share nothing but the reduction;
+// - CH = 2 (the two column halves of a K part read the same activations): the tile's activation codes go through a
+//   2-slot LDS ring of chunks (32 rows x 1,024 codes, 32 KB) by direct global -> LDS loads, filled by all 16 waves and
+//   read after a barrier; piece p (16 bytes) of row r sits at p ^ (r & 15), so a 16-lane pass of 16-byte reads
+//   covers the 64 banks once; the fp32 row scales of the tile are staged beside them;
 // - a wave's weights for all (<= 4) chunks are loaded into registers up front, interleaved with the first two
 //   activation chunks (issue order: scales, W0 A0 W1 A1 W2 W3, then A(c + 2) once chunk c is done); loads retire in
 //   order and each chunk waits for exactly the loads before its own. Weight load x (0..3) of a block: lane l reads
@@ -482,8 +489,11 @@ template <int CH>
 struct Fp8Rows {
   static constexpr int KP = 16 / CH, KR = 128 * KP, SLOT = 32 * KR, NA = SLOT / 1024 / 16, W = 32 * CH;
   static constexpr int LS = CH == 2 ? 18 : 17;  // reduction lane stride (floats)
+  // CH = 1: each wave's own 2-slot ring of its K part (32 rows x 128 codes, 4 KB a slot); CH = 2: the shared ring
+  // of chunks and the tile's row scales.
   static size_t lds(int K) {
-    return std::max(2 * size_t(SLOT) + size_t(32) * (K / 128) * 4, size_t(16) * 64 * LS * 4);
+    const size_t ring = CH == 1 ? size_t(16) * 2 * 4096 : 2 * size_t(SLOT) + size_t(32) * (K / 128) * 4;
+    return std::max(ring, size_t(16) * 64 * LS * 4);
   }
 };
 
@@ -496,6 +506,7 @@ __global__ __launch_bounds__(1024) void fp8_rows_kernel(Fp8GemmArgs p) {
   constexpr int KP = T::KP, KR = T::KR, SLOT = T::SLOT, NA = T::NA;
   extern __shared__ __align__(16) uint8_t smem[];
   static_assert(NCH >= 1 && NCH <= FR_MAXCH);
+  static_assert(CH == 2 || NA == 4, "CH = 1: four 1 KB activation loads per wave and chunk");
   const int M = p.M, N = p.N, K = p.K, KS = K / 128;  // the host launches NCH = ceil(KS / KP)
   const int nw = gridDim.x, lin = blockIdx.x;
   const int wi = nw % 8 ? lin : (lin & 7) * (nw >> 3) + (lin >> 3);
@@ -503,23 +514,35 @@ __global__ __launch_bounds__(1024) void fp8_rows_kernel(Fp8GemmArgs p) {
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), chh = wave % CH, kh = wave / CH;  // column half, K part
   const int col0 = bx * T::W, n = col0 + chh * 32 + l32;
-  float* const ssa = reinterpret_cast<float*>(smem + 2 * SLOT);  // row scales [32][KS]
   const uint8_t* wld = p.w + size_t(col0 + chh * 32 + (lane & 15)) * K + (lane >> 4) * 16;
   const float* swrow = p.sw32 + size_t((col0 + chh * 32) / 128) * KS;  // 32 columns lie in one 128-row block
   const uint32_t lds0 = lds_addr(smem);
+  // The activation loads. CH = 1: load i of the wave covers rows 8i .. 8i + 7 of its 4 KB slot, lane j row
+  // 8i + j / 8 at piece (j % 8) ^ swz(row) of the K part. CH = 2: load i covers 1 KB of the shared chunk slot.
   uint32_t rowoff[NA];
   int pin[NA];
 #pragma unroll
   for (int i = 0; i < NA; ++i) {
-    const int slot = (wave * NA + i) * 64 + lane, r = slot / (KR / 16);
-    rowoff[i] = uint32_t(min(row0 + r, M - 1)) * uint32_t(K);
-    pin[i] = ((slot % (KR / 16)) ^ (r & 15)) * 16;
+    if constexpr (CH == 1) {
+      const int r = 8 * i + (lane >> 3);
+      rowoff[i] = uint32_t(min(row0 + r, M - 1)) * uint32_t(K);
+      pin[i] = 16 * ((lane & 7) ^ ((r >> 1) & 7));
+    } else {
+      const int slot = (wave * NA + i) * 64 + lane, r = slot / (KR / 16);
+      rowoff[i] = uint32_t(min(row0 + r, M - 1)) * uint32_t(K);
+      pin[i] = ((slot % (KR / 16)) ^ (r & 15)) * 16;
+    }
   }
   const auto issue_a = [&](int ch) {
 #pragma unroll
-    for (int i = 0; i < NA; ++i)
-      dma16(p.a, rowoff[i] + uint32_t(min(ch * KR + pin[i], K - 16)),
-            lds0 + uint32_t((ch & 1) * SLOT + (wave * NA + i) * 1024));
+    for (int i = 0; i < NA; ++i) {
+      if constexpr (CH == 1)
+        dma16(p.a, rowoff[i] + uint32_t(min(ch * KP + kh, KS - 1)) * 128u + uint32_t(pin[i]),
+              lds0 + uint32_t((wave * 2 + (ch & 1)) * 4096 + i * 1024));
+      else
+        dma16(p.a, rowoff[i] + uint32_t(min(ch * KR + pin[i], K - 16)),
+              lds0 + uint32_t((ch & 1) * SLOT + (wave * NA + i) * 1024));
+    }
   };
   v4i b[NCH][4];
   const auto load_w = [&](int u) {
@@ -527,15 +550,21 @@ __global__ __launch_bounds__(1024) void fp8_rows_kernel(Fp8GemmArgs p) {
 #pragma unroll
     for (int x = 0; x < 4; ++x) b[u][x] = vload16(q + (x >> 1) * 16 * K + (x & 1) * 64);
   };
-  // Issue order: the scales (lane u < nch: the wave's weight scale of chunk u; thread t: row scales t, t + 1024 of
-  // the tile), W0 A0 W1 A1 W2 W3, then A(c + 2).
+  // Issue order: the scales (lane u < nch: the wave's weight scale of chunk u; CH = 1: lane r's row scale of each
+  // chunk's block; CH = 2: thread t's row scales t, t + 1024 of the tile), W0 A0 W1 A1 W2 W3, then A(c + 2).
   uint32_t swv = vload_u32(swrow + min(min(lane, FR_MAXCH - 1) * KP + kh, KS - 1));
-  uint32_t sav[2];
+  constexpr int NSA = CH == 1 ? NCH : 2;
+  uint32_t sav[NSA];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int e = min(tid + 1024 * j, 32 * KS - 1);
-    sav[j] = vload_u32(p.sa32 + size_t(min(row0 + e / KS, M - 1)) * KS + e % KS);
+  for (int j = 0; j < NSA; ++j) {
+    if constexpr (CH == 1) {
+      sav[j] = vload_u32(p.sa32 + size_t(min(row0 + l32, M - 1)) * KS + min(j * KP + kh, KS - 1));
+    } else {
+      const int e = min(tid + 1024 * j, 32 * KS - 1);
+      sav[j] = vload_u32(p.sa32 + size_t(min(row0 + e / KS, M - 1)) * KS + e % KS);
+    }
   }
+  float* const ssa = reinterpret_cast<float*>(smem + 2 * SLOT);  // CH = 2: row scales [32][KS]
   load_w(0);
   issue_a(0);
   if constexpr (NCH > 1) {
@@ -559,16 +588,18 @@ __global__ __launch_bounds__(1024) void fp8_rows_kernel(Fp8GemmArgs p) {
     vlanded(b[ch]);
     if (ch == 0) {
       vlanded(swv);
-      vlanded(sav[0]);
-      vlanded(sav[1]);
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        if (tid + 1024 * j < 32 * KS) ssa[tid + 1024 * j] = __uint_as_float(sav[j]);
+      for (int j = 0; j < NSA; ++j) vlanded(sav[j]);
+      if constexpr (CH == 2)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          if (tid + 1024 * j < 32 * KS) ssa[tid + 1024 * j] = __uint_as_float(sav[j]);
     }
-    __syncthreads();  // every wave's part of chunk ch (and the row scales) has landed
+    if constexpr (CH == 1) asm volatile("" ::: "memory");  // the wave's own activation pieces have landed in LDS
+    else __syncthreads();                                    // every wave's part of chunk ch (and the row scales)
     const int kb = ch * KP + kh;
     if (kb < KS) {
-      const uint8_t* sl = smem + (ch & 1) * SLOT;
+      const uint8_t* sl = CH == 1 ? smem + (wave * 2 + (ch & 1)) * 4096 : smem + (ch & 1) * SLOT;
       const float sw = __uint_as_float(uint32_t(__builtin_amdgcn_readlane(int(swv), ch)));
 #pragma unroll
       for (int x = 0; x < 2; ++x)
@@ -583,8 +614,9 @@ __global__ __launch_bounds__(1024) void fp8_rows_kernel(Fp8GemmArgs p) {
       v16f_t raw = v16f_t{};
 #pragma unroll
       for (int x = 0; x < 4; ++x) {
-        const int pc = (kh * 8 + 2 * h + (x >> 1) + 4 * (x & 1)) ^ (r & 15);
-        const v4i av = *reinterpret_cast<const v4i*>(sl + r * KR + pc * 16);
+        const int q = 2 * h + (x >> 1) + 4 * (x & 1);  // the piece of the block this load holds
+        const v4i av = CH == 1 ? *reinterpret_cast<const v4i*>(sl + r * 128 + (q ^ ((r >> 1) & 7)) * 16)
+                               : *reinterpret_cast<const v4i*>(sl + r * KR + ((kh * 8 + q) ^ (r & 15)) * 16);
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const bf16x8 af = fp8x8_to_bf16(uint32_t(av[2 * e]), uint32_t(av[2 * e + 1]), 1.0f);
@@ -594,11 +626,19 @@ __global__ __launch_bounds__(1024) void fp8_rows_kernel(Fp8GemmArgs p) {
       }
       // Element i of lane (l32, h) is row 8 (i / 4) + 4 h + i % 4 of the tile.
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[i] += raw[i] * (ssa[(8 * (i / 4) + 4 * h + (i % 4)) * KS + kb] * sw);
+      for (int i = 0; i < 16; ++i) {
+        const int row = 8 * (i / 4) + 4 * h + (i % 4);
+        float sa;
+        if constexpr (CH == 1)
+          sa = __uint_as_float(uint32_t(__builtin_amdgcn_ds_bpermute(row * 4, int(sav[ch]))));
+        else
+          sa = ssa[row * KS + kb];
+        acc[i] += raw[i] * (sa * sw);
+      }
     }
     if constexpr (ch + 2 < NCH) {
-      __syncthreads();  // every wave is done with slot ch & 1
-      issue_a(ch + 2);
+      if constexpr (CH == 2) __syncthreads();  // every wave is done with slot ch & 1
+      issue_a(ch + 2);  // CH = 1: the wave's own slot, whose reads above have returned
     }
   };
   chunk(std::integral_constant<int, 0>{});
