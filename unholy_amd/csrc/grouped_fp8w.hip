@@ -167,6 +167,7 @@ __global__ __launch_bounds__(1024) void grouped_fp8w_rows_kernel(const bf16* a, 
   constexpr int KP = T::KP, KR = T::KR, PPR = T::PPR;
   extern __shared__ __align__(16) uint8_t smem[];
   static_assert(NCH >= 1 && NCH <= GR_MAXCH);
+  static_assert(CH == 2 || TR == 16, "the per-wave activation loads cover 16 rows");
   const int N = G * R, KS = K / 128;  // the host launches NCH = ceil(KS / KP)
   const int nw = gridDim.x, lin = blockIdx.x;
   const int wi = nw % 8 ? lin : (lin & 7) * (nw >> 3) + (lin >> 3);
@@ -181,21 +182,38 @@ __global__ __launch_bounds__(1024) void grouped_fp8w_rows_kernel(const bf16* a, 
   const uint8_t* wld = w + size_t(col0 + chh * 32 + (lane & 15)) * K + (lane >> 4) * 16;
   const uint8_t* swrow = sw + size_t((col0 + chh * 32) / 128) * KS;  // 32 columns lie in one 128-row block
   const uint32_t lds0 = lds_addr(smem);
-  // This wave's 4 direct loads of a chunk: 1 KB pieces q = 4 wave + i of the 64 KB slot (rows past M repeat row M - 1,
-  // inputs past K repeat the row's last 8; neither is used).
+  // This wave's 4 direct loads of a chunk (rows past M repeat row M - 1; neither they nor the clamped inputs are
+  // used).
+  // - CH = 1 (16 rows): the wave's own K part, 16 rows x 128 inputs (4 KB), into its own 2-slot ring: load i covers
+  //   rows 4i .. 4i + 3, lane j row 4i + j / 16 at piece (j % 16) ^ row, so a 16-lane pass of the MFMA's 16-byte
+  //   reads (16 rows, one piece) covers the 64 banks once. No wave waits for another before the reduction: a wave
+  //   computes its chunks as soon as its own loads land while the others still stream.
+  // - CH = 2 (32 rows, the two column halves of a K part read the same activations): 1 KB pieces q = 4 wave + i of
+  //   the shared 64 KB chunk slot, read after a barrier.
   uint32_t rowoff[4];
   int pin[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int slot = (wave * 4 + i) * 64 + lane, r = slot / PPR;
-    rowoff[i] = uint32_t(min(row0 + r, M - 1) * G + grp) * uint32_t(K) * 2u;
-    pin[i] = ((slot % PPR) ^ (r & 15)) * 8;
+    if constexpr (CH == 1) {
+      const int r = 4 * i + (lane >> 4);
+      rowoff[i] = uint32_t(min(row0 + r, M - 1) * G + grp) * uint32_t(K) * 2u;
+      pin[i] = ((lane & 15) ^ r) * 8;
+    } else {
+      const int slot = (wave * 4 + i) * 64 + lane, r = slot / PPR;
+      rowoff[i] = uint32_t(min(row0 + r, M - 1) * G + grp) * uint32_t(K) * 2u;
+      pin[i] = ((slot % PPR) ^ (r & 15)) * 8;
+    }
   }
   const auto issue_a = [&](int ch) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dma16(a, rowoff[i] + uint32_t(min(ch * KR + pin[i], K - 8)) * 2u,
-            lds0 + uint32_t((ch & 1) * GR_SLOT + (wave * 4 + i) * 1024));
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (CH == 1)
+        dma16(a, rowoff[i] + uint32_t(min(ch * KP + kh, KS - 1) * 128 + pin[i]) * 2u,
+              lds0 + uint32_t((wave * 2 + (ch & 1)) * 4096 + i * 1024));
+      else
+        dma16(a, rowoff[i] + uint32_t(min(ch * KR + pin[i], K - 8)) * 2u,
+              lds0 + uint32_t((ch & 1) * GR_SLOT + (wave * 4 + i) * 1024));
+    }
   };
   v4i b[NCH][4];
   const auto load_w = [&](int u) {
@@ -227,9 +245,10 @@ __global__ __launch_bounds__(1024) void grouped_fp8w_rows_kernel(const bf16* a, 
     wait_vm<later>();
     vlanded(b[ch]);
     vlanded(sv);
-    __syncthreads();  // every wave's part of chunk ch has landed
+    if constexpr (CH == 1) asm volatile("" ::: "memory");  // the wave's own activation pieces have landed in LDS
+    else __syncthreads();                                    // every wave's part of chunk ch has landed
     if (ch * KP + kh < KS) {
-      const uint8_t* sl = smem + (ch & 1) * GR_SLOT;
+      const uint8_t* sl = CH == 1 ? smem + (wave * 2 + (ch & 1)) * 4096 : smem + (ch & 1) * GR_SLOT;
       const float swc = __uint_as_float(uint32_t(__builtin_amdgcn_readlane(int(sv), ch)) << 23);
 #pragma unroll
       for (int x = 0; x < 2; ++x)
@@ -245,14 +264,16 @@ __global__ __launch_bounds__(1024) void grouped_fp8w_rows_kernel(const bf16* a, 
       for (int j = 0; j < 8; ++j) {
         const int x = j >> 1;
         const bf16x8 bf = fp8x8_to_bf16(uint32_t(b[ch][x][2 * (j & 1)]), uint32_t(b[ch][x][2 * (j & 1) + 1]), swc);
-        const int pc = (kh * 16 + 2 * (2 * h + (x >> 1) + 4 * (x & 1)) + (j & 1)) ^ (r & 15);
-        const bf16x8 af = __builtin_bit_cast(bf16x8, *reinterpret_cast<const v4i*>(sl + (r * PPR + pc) * 16));
+        const int q = 2 * (2 * h + (x >> 1) + 4 * (x & 1)) + (j & 1);  // the block's piece of this MFMA
+        const bf16x8 af = CH == 1
+            ? __builtin_bit_cast(bf16x8, *reinterpret_cast<const v4i*>(sl + (r * 16 + (q ^ r)) * 16))
+            : __builtin_bit_cast(bf16x8, *reinterpret_cast<const v4i*>(sl + (r * PPR + ((kh * 16 + q) ^ (r & 15))) * 16));
         acc = mfma32_bf16(af, bf, acc);
       }
     }
     if constexpr (ch + 2 < NCH) {
-      __syncthreads();  // every wave is done with slot ch & 1
-      issue_a(ch + 2);
+      if constexpr (CH == 2) __syncthreads();  // every wave is done with slot ch & 1
+      issue_a(ch + 2);  // CH = 1: the wave's own slot, whose reads above have returned
     }
   };
   chunk(std::integral_constant<int, 0>{});
