@@ -140,14 +140,15 @@ __global__ __launch_bounds__(64 * GV_W) void grouped_fp8w_gemv_kernel(const bf16
 //   while the later weights stream; loads retire in order and each chunk waits for exactly the loads before its own;
 // - the tile's activation rows go through a 2-slot LDS ring of chunks (32 rows x 1,024 bf16, 64 KB) by direct
 //   global -> LDS loads; piece p (16 bytes) of row r sits at p ^ (r & 15), so the 16 rows of an MFMA operand pass
-//   cover the 64 banks once;
+//   cover the 64 banks once (the 32-column form: each wave stages its own K part's 16 rows in its own ring and waits
+//   for no other wave until the reduction);
 // - the weights dequantize with the block scale folded in (exact); the 8 parts (16 in the 32-column form) are added
 //   in LDS in part order by all 16 waves;
 // - work item wi = column block x row tiles + row tile; XCD x takes the x-th eighth of the items, so the row tiles of
 //   a column block share one L2 (the second reads the weights from it) and a group's activation rows sit in one L2.
 // Against the GEMV (one 16-column tile per workgroup, every workgroup reading its rows from L2): the activation rows
-// leave L2 once per 64 columns. DSV4 shape: 17.6 us against 45 us at M = 64; 10.0 / 11.5 / 12.0 us against 10.8 / 13.4 /
-// 14.9 us at M = 1 / 8 / 16 (the 32-column form: 256 workgroups, each wave's weights in flight at once).
+// leave L2 once per 64 columns. DSV4 shape: 17.6 us against 45 us at M = 64; at M = 1 8.9 us against 10.8 us (the
+// 32-column form: 256 workgroups, each wave's weights in flight at once).
 constexpr int GR_SLOT = 64 * 1024, GR_MAXCH = 4;
 
 // CH column halves of 32 (workgroup width 32 CH), TR staged rows (32, or 16 for M <= 16: the MFMA's rows 16-31 then
