@@ -13,6 +13,7 @@
 // Both operands are dequantized exactly to bf16 at the LDS read and multiplied on the 32x32x16 bf16 MFMA. e8m0
 // scales are folded into the conversions (exact) and the MFMA accumulates across blocks; with fp32 scales each
 // block's MFMA chain starts from zero and is folded as acc += raw * (sa * sw), the reference's order of scaling.
+#include <type_traits>
 #include <stdexcept>
 
 #include "common.hpp"
@@ -70,8 +71,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     const int slot = (wave * T::BL + i) * 64 + lane, r = slot >> 3, p = (slot & 7) ^ lds_swz(r);
     boff[i] = uint32_t(r) * uint32_t(K) + uint32_t(p * 16);
   }
-  // fp32 activation scales: waves 0 and 1 gather rows 64 w + lane.
-  const uint32_t saoff = uint32_t(min((wave & 1) * 64 + lane, Mt - 1)) * uint32_t(KS) * 4u;
+  // fp32 scales: the fold's factor sa[row] * sw (the reference's order, raw * (sa * sw)) for each stage's 128 rows is
+  // formed once, by waves 0 and 1 (rows 64 w + lane) one stage ahead: the next stage's sa is loaded into a register
+  // and, at the end of the current stage, multiplied and written into that stage's slot; the fold of every wave then
+  // reads the products instead of forming 32 of them per lane.
+  const float* sarow = F32S ? a.sa32 + size_t(row0 + min((wave & 1) * 64 + lane, Mt - 1)) * KS : nullptr;
+  const float* swcol = F32S ? a.sw32 + size_t(col0 / 128) * KS : nullptr;  // a TN-column block lies in one 128-row block
+  const auto put_products = [&](int s, float sa_v, float sw_v) {
+    float* dst = reinterpret_cast<float*>(smem + (s % FT_S) * FT_STAGE + FT_A + FT_B);
+    dst[wave * 64 + lane] = sa_v * sw_v;
+  };
 
   const uint8_t* arow = a.a + size_t(row0) * K;
   const uint8_t* wcol = a.w + size_t(col0) * K;
@@ -81,10 +90,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     for (int i = 0; i < 4; ++i) dma16(arow + s * 128, aoff[i], st + uint32_t(wave * 4 + i) * 1024);
 #pragma unroll
     for (int i = 0; i < T::BL; ++i) dma16(wcol + s * 128, boff[i], st + uint32_t(FT_A + (wave * T::BL + i) * 1024));
-    if constexpr (F32S)
-      if (wave < 2) dma4(a.sa32 + size_t(row0) * KS + s, saoff, st + uint32_t(FT_A + FT_B + wave * 256));
   };
   issue(0);
+  if constexpr (F32S)
+    if (wave < 2) put_products(0, sarow[0], swcol[0]);
   // Scales, after stage 0 is in flight.
   for (int e = tid; e < KS; e += 256) {
     const size_t i = size_t(col0 / 128) * KS + e;  // a TN-column block lies in one 128-row scale block
@@ -95,89 +104,113 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     for (int e = tid; e < 128 * KS; e += 256) sa_lds[e] = a.sa8[size_t(row0 + r) * KS + (e >> 7)];
   }
 
+  // The wave's live 32-row blocks (2 but in a partial last row tile) as a compile-time count: the stage loop then
+  // has no branches, and each block's raw MFMA chain starts from a zero operand instead of zeroed registers.
   const int rb_live = __builtin_amdgcn_readfirstlane(min(2, max(0, (Mt - rh * 64 + 31) / 32)));
   v16f_t acc[2][CB];
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = v16f_t{};
-
-  for (int s = 0; s < KS; ++s) {
-    wait_vm<0>();     // this wave's part of stage s (the only stage in flight)
-    __syncthreads();  // every wave's part has landed; the other slot (stage s - 1) is free
-    if (s + 1 < KS) issue(s + 1);
-    const uint8_t* stb = smem + (s % FT_S) * FT_STAGE;
-    const float swv = sw_lds[s];
-    float asc[2];
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-      asc[rb] = F32S ? 1.0f : e8m0_to_f32(sa_lds[s * 128 + rh * 64 + rb * 32 + l32]);
-    v16f_t raw[2][CB];
-    if constexpr (F32S) {
+  // One stage; NEXT: a stage follows (its ring loads and scale go out here). The last stage is peeled off, so no
+  // branch separates the counted scale load from its wait.
+  const auto stages = [&](auto rbl) {
+    constexpr int RBL = decltype(rbl)::value;
+    const auto stage = [&](int s, auto next_c) {
+      constexpr bool NEXT = decltype(next_c)::value;
+      wait_vm<0>();     // this wave's part of stage s (the only stage in flight)
+      __syncthreads();  // every wave's part has landed; the other slot (stage s - 1) is free
+      // The next stage's sa goes out before its ring loads, as a counted load (every wave: an unconditional load keeps
+      // the count exact; waves 2 and 3 read rows they do not use): the wait for it at the end of this stage leaves
+      // those 4 + BL loads in flight (loads retire in order).
+      uint32_t sa_next = 0u;
+      if constexpr (NEXT) {
+        if constexpr (F32S) sa_next = vload_u32(sarow + s + 1);
+        issue(s + 1);
+      }
+      const uint8_t* stb = smem + (s % FT_S) * FT_STAGE;
+      const float swv = sw_lds[s];
+      float asc[2];
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb)
+        asc[rb] = F32S ? 1.0f : e8m0_to_f32(sa_lds[s * 128 + rh * 64 + rb * 32 + l32]);
+      v16f_t raw[2][CB];
+      if constexpr (F32S) {
 #pragma unroll
-        for (int cb = 0; cb < CB; ++cb) raw[rb][cb] = v16f_t{};
-    }
-    // The stage's operand reads, conversions and MFMAs at raised wave priority, so that a wave holding operands
-    // issues ahead of the other workgroup's waves still waiting for theirs (M = 4096 step: 172 against 181 us).
-    __builtin_amdgcn_s_setprio(1);
+        for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      v4i aq[2][2], bq[CB][2];
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        const int n = ch * (TN / 2) + cb * 32 + l32;
-#pragma unroll
-        for (int x = 0; x < 2; ++x)
-          bq[cb][x] = *reinterpret_cast<const v4i*>(stb + FT_A + (n * 8 + ((4 * j + 2 * h + x) ^ lds_swz(n))) * 16);
+          for (int cb = 0; cb < CB; ++cb) raw[rb][cb] = v16f_t{};
       }
+      // The stage's operand reads, conversions and MFMAs at raised wave priority, so that a wave holding operands
+      // issues ahead of the other workgroup's waves still waiting for theirs (M = 4096 step: 172 against 181 us).
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        const int r = rh * 64 + rb * 32 + l32;
+      for (int j = 0; j < 2; ++j) {
+        v4i aq[2][2], bq[CB][2];
 #pragma unroll
-        for (int x = 0; x < 2; ++x)
-          aq[rb][x] = *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 * j + 2 * h + x) ^ lds_swz(r))) * 16);
-      }
+        for (int cb = 0; cb < CB; ++cb) {
+          const int n = ch * (TN / 2) + cb * 32 + l32;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        bf16x8 bf[CB];
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb)
-          bf[cb] = fp8x8_to_bf16(uint32_t(bq[cb][t >> 1][(t & 1) * 2]), uint32_t(bq[cb][t >> 1][(t & 1) * 2 + 1]),
-                                 F32S ? 1.0f : swv);
+          for (int x = 0; x < 2; ++x)
+            bq[cb][x] = *reinterpret_cast<const v4i*>(stb + FT_A + (n * 8 + ((4 * j + 2 * h + x) ^ lds_swz(n))) * 16);
+        }
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb) {
-          if (rb >= rb_live) break;
-          const bf16x8 af =
-              fp8x8_to_bf16(uint32_t(aq[rb][t >> 1][(t & 1) * 2]), uint32_t(aq[rb][t >> 1][(t & 1) * 2 + 1]), asc[rb]);
+          const int r = rh * 64 + rb * 32 + l32;
 #pragma unroll
-          for (int cb = 0; cb < CB; ++cb) {
-            if constexpr (F32S) raw[rb][cb] = mfma32_bf16(af, bf[cb], raw[rb][cb]);
-            else acc[rb][cb] = mfma32_bf16(af, bf[cb], acc[rb][cb]);
+          for (int x = 0; x < 2; ++x)
+            aq[rb][x] = *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 * j + 2 * h + x) ^ lds_swz(r))) * 16);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          bf16x8 bf[CB];
+#pragma unroll
+          for (int cb = 0; cb < CB; ++cb)
+            bf[cb] = fp8x8_to_bf16(uint32_t(bq[cb][t >> 1][(t & 1) * 2]), uint32_t(bq[cb][t >> 1][(t & 1) * 2 + 1]),
+                                   F32S ? 1.0f : swv);
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb) {
+            if (rb >= RBL) break;
+            const bf16x8 af =
+                fp8x8_to_bf16(uint32_t(aq[rb][t >> 1][(t & 1) * 2]), uint32_t(aq[rb][t >> 1][(t & 1) * 2 + 1]), asc[rb]);
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+              if constexpr (F32S) raw[rb][cb] = mfma32_bf16(af, bf[cb], raw[rb][cb]);
+              else acc[rb][cb] = mfma32_bf16(af, bf[cb], acc[rb][cb]);
+            }
           }
         }
       }
-    }
-    __builtin_amdgcn_s_setprio(0);
-    if constexpr (F32S) {
-      // Value i of a 32 x 32 block sits at row 8 (i / 4) + 4 h + i % 4: rows in runs of 4, one 16-byte read each.
-      const float* sas = reinterpret_cast<const float*>(stb + FT_A + FT_B);
+      __builtin_amdgcn_s_setprio(0);
+      if constexpr (F32S) {
+        // Value i of a 32 x 32 block sits at row 8 (i / 4) + 4 h + i % 4: rows in runs of 4, one 16-byte read each.
+        const float* sas = reinterpret_cast<const float*>(stb + FT_A + FT_B);
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        if (rb >= rb_live) break;
+        for (int rb = 0; rb < 2; ++rb) {
+          if (rb >= RBL) break;
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-          const float4 sa4 = *reinterpret_cast<const float4*>(sas + rh * 64 + rb * 32 + 8 * i4 + 4 * h);
-          const float f[4] = {sa4.x * swv, sa4.y * swv, sa4.z * swv, sa4.w * swv};
+          for (int i4 = 0; i4 < 4; ++i4) {
+            const float4 f4 = *reinterpret_cast<const float4*>(sas + rh * 64 + rb * 32 + 8 * i4 + 4 * h);
+            const float f[4] = {f4.x, f4.y, f4.z, f4.w};
 #pragma unroll
-          for (int cb = 0; cb < CB; ++cb)
+            for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) acc[rb][cb][4 * i4 + q] += raw[rb][cb][4 * i4 + q] * f[q];
+              for (int q = 0; q < 4; ++q) acc[rb][cb][4 * i4 + q] += raw[rb][cb][4 * i4 + q] * f[q];
+          }
+        }
+        if constexpr (NEXT) {  // into stage s - 1's slot, now free
+          wait_vm<4 + T::BL>();
+          vlanded(sa_next);
+          if (wave < 2) put_products(s + 1, __uint_as_float(sa_next), sw_lds[s + 1]);
         }
       }
-    }
-  }
+    };
+    for (int s = 0; s + 1 < KS; ++s) stage(s, std::true_type{});
+    stage(KS - 1, std::false_type{});
+  };
+  if (rb_live == 2) stages(std::integral_constant<int, 2>{});
+  else if (rb_live == 1) stages(std::integral_constant<int, 1>{});
+  else stages(std::integral_constant<int, 0>{});
 
   // ---- epilogue through LDS: 128 x TN bf16, then 16-byte row stores
   __syncthreads();
