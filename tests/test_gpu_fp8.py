@@ -24,11 +24,12 @@ def _weights_f32s(rng, N, K):
 
 # 16 < M <= 256 with N % 32 == 0 takes the row-tile kernel: one to four 2,048-input chunks, ragged last chunks (K = 640,
 # 2,176), one 32-column block (N = 32), a weight-scale row shared by fewer than 128 columns (N = 96), 1 to 8 row tiles;
-# (200, 4096, 1024): the 64-column form over 7 row tiles.
+# (200, 4096, 1024): the 64-column form over 7 row tiles. Past 256 rows the tiled GEMM, whose last row tile leaves a
+# wave one or no live 32-row block: 300 (44 rows), 400 (16 rows), 480 (96 rows).
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (5, 384, 1024), (64, 512, 1024), (300, 256, 512), (3, 136, 384),
                                    (1000, 768, 1024), (129, 200, 256), (17, 32, 640), (33, 1024, 8192), (64, 96, 6144),
                                    (48, 256, 2176), (40, 200, 512), (200, 128, 1024), (256, 96, 2176), (129, 64, 384),
-                                   (200, 4096, 1024)])
+                                   (200, 4096, 1024), (400, 256, 512), (480, 384, 768)])
 def test_fp8_f32_scales(M, N, K):
     """BASELINE config 4 form: A bf16 -> e4m3 per 1x128 with fp32 scales; W e4m3 with fp32 128x128 scales."""
     rng = np.random.default_rng(M + N)
@@ -104,7 +105,7 @@ def test_fp8_f32s_row_tiles_ldc(M, N, K, pad):
 # M > 64 takes the tiled GEMM: 64-column tiles while 128-column ones would make fewer than 256 workgroups
 # (M = 200, 1000), else 128 columns (M = 1024, N = 4096).
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (8, 1024, 512), (33, 256, 1024), (200, 512, 512), (17, 200, 640),
-                                   (1000, 768, 1024), (1024, 4096, 256)])
+                                   (1000, 768, 1024), (1024, 4096, 256), (400, 256, 512)])
 def test_fp8_e8m0_scales(M, N, K):
     """The reference's W8A8 contract (gemm_w8a8 / gemv_w8a8 / gemm_w8a8_wmma): e8m0 scales on both sides."""
     rng = np.random.default_rng(M * 3 + K)
