@@ -334,7 +334,10 @@ int uh_quant_weight_fp8_f32s(const float* w, uint8_t* q, float* s, int N, int K,
  * :1052-1156 + moe_combine): router logits [T, E] -> softmax top-K -> dispatch -> xform (fp8) -> w1/w3 + SwiGLU ->
  * w2 -> combine into out [T, D]. tab: device table of 6 * E pointers {w1 codes, w1 scales, w3 codes, w3 scales,
  * w2 codes, w2 scales} x E (tile-major), the layout of the reference's exl3_ptrs(m, f, E). ws: device workspace of
- * uh_mx_moe_workspace_size bytes. sel / wt (may be NULL): the routing is also written there. ---- */
+ * uh_mx_moe_workspace_size bytes. sel / wt (may be NULL): the routing is also written there. Every expert the routing
+ * can pick must have all six pointers: a NULL entry's rows are skipped by the GEMVs / GEMMs (the kernels' contract)
+ * and their pair rows are then undefined in the combine; an engine holding only some experts uses the remote entry
+ * points (uh_moe_dispatch_small_remote, uh_remote_combine, uh_moe_combine_partial_link) instead. ---- */
 size_t uh_mx_moe_workspace_size(int T, int K, int E, int D, int I);
 int uh_mx_moe_forward(const uint16_t* x, const float* logits, int T, int K, int E, int D, int I,
                       const uint8_t* const* tab, float limit, void* ws, size_t ws_bytes, uint16_t* out, int32_t* sel,
