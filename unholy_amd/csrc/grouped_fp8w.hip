@@ -406,41 +406,49 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 #pragma unroll
     for (int cb = 0; cb < T::CB; ++cb) acc[rb][cb] = v16f_t{};
 
-  for (int s = 0; s < KS; ++s) {
-    // This wave's part of stage s has landed when at most its loads of the later stages issued (S - 2 at most) are
-    // pending.
-    if (T::S == 3 && s + 1 < KS) wait_vm<T::OPS>();
-    else wait_vm<0>();
-    __syncthreads();  // every wave's part has landed; slot (s - 1) % S is free
-    if (s + T::S - 1 < KS) issue(s + T::S - 1);
-    const uint8_t* stb = smem + (s % T::S) * T::STAGE;
-    const float swv = e8m0_to_f32(swrow[s >> 1]);
-    // MFMA step t (16 inputs): lane half h supplies inputs 32 h + 8 t .. + 7 of the stage, on both sides.
-    v4i bq[T::CB][2];
+  // The wave's live 32-row blocks as a compile-time count (2 but in a partial last row tile): no branch in the stage
+  // loop.
+  const auto stages = [&](auto rbl) {
+    constexpr int RBL = decltype(rbl)::value;
+    for (int s = 0; s < KS; ++s) {
+      // This wave's part of stage s has landed when at most its loads of the later stages issued (S - 2 at most) are
+      // pending.
+      if (T::S == 3 && s + 1 < KS) wait_vm<T::OPS>();
+      else wait_vm<0>();
+      __syncthreads();  // every wave's part has landed; slot (s - 1) % S is free
+      if (s + T::S - 1 < KS) issue(s + T::S - 1);
+      const uint8_t* stb = smem + (s % T::S) * T::STAGE;
+      const float swv = e8m0_to_f32(swrow[s >> 1]);
+      // MFMA step t (16 inputs): lane half h supplies inputs 32 h + 8 t .. + 7 of the stage, on both sides.
+      v4i bq[T::CB][2];
 #pragma unroll
-    for (int cb = 0; cb < T::CB; ++cb) {
-      const int n = ch * (TN / 2) + cb * 32 + l32;
+      for (int cb = 0; cb < T::CB; ++cb) {
+        const int n = ch * (TN / 2) + cb * 32 + l32;
 #pragma unroll
-      for (int x = 0; x < 2; ++x)
-        bq[cb][x] = *reinterpret_cast<const v4i*>(stb + T::A + (n * 4 + ((2 * h + x) ^ swz64(n))) * 16);
-    }
+        for (int x = 0; x < 2; ++x)
+          bq[cb][x] = *reinterpret_cast<const v4i*>(stb + T::A + (n * 4 + ((2 * h + x) ^ swz64(n))) * 16);
+      }
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      bf16x8 bf[T::CB];
+      for (int t = 0; t < 4; ++t) {
+        bf16x8 bf[T::CB];
 #pragma unroll
-      for (int cb = 0; cb < T::CB; ++cb)
-        bf[cb] = fp8x8_to_bf16(uint32_t(bq[cb][t >> 1][(t & 1) * 2]), uint32_t(bq[cb][t >> 1][(t & 1) * 2 + 1]), swv);
+        for (int cb = 0; cb < T::CB; ++cb)
+          bf[cb] = fp8x8_to_bf16(uint32_t(bq[cb][t >> 1][(t & 1) * 2]), uint32_t(bq[cb][t >> 1][(t & 1) * 2 + 1]), swv);
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        if (rb >= rb_live) break;
-        const int r = rh * 64 + rb * 32 + l32;
-        const bf16x8 af =
-            __builtin_bit_cast(bf16x8, *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 * h + t) ^ lds_swz(r))) * 16));
+        for (int rb = 0; rb < 2; ++rb) {
+          if (rb >= RBL) break;
+          const int r = rh * 64 + rb * 32 + l32;
+          const bf16x8 af =
+              __builtin_bit_cast(bf16x8, *reinterpret_cast<const v4i*>(stb + (r * 8 + ((4 * h + t) ^ lds_swz(r))) * 16));
 #pragma unroll
-        for (int cb = 0; cb < T::CB; ++cb) acc[rb][cb] = mfma32_bf16(af, bf[cb], acc[rb][cb]);
+          for (int cb = 0; cb < T::CB; ++cb) acc[rb][cb] = mfma32_bf16(af, bf[cb], acc[rb][cb]);
+        }
       }
     }
-  }
+  };
+  if (rb_live == 2) stages(std::integral_constant<int, 2>{});
+  else if (rb_live == 1) stages(std::integral_constant<int, 1>{});
+  else stages(std::integral_constant<int, 0>{});
 
   // ---- epilogue through LDS: 128 x TN bf16, then 16-byte row stores
   __syncthreads();
