@@ -141,6 +141,8 @@ unsigned transform_blocks(int P, int K) { return unsigned(std::min<size_t>((size
 // the matching activation inputs. The MFMA accumulates in fp32 with exact products; no cross-lane reductions.
 // GV_PF: weight steps in flight per wave (8 measured slower: the larger ring costs occupancy).
 constexpr int GV_WAVES = 8, GV_PAD = 16, GV_MAXROWS = 16, GV_PF = 4;
+// The live tile count of a launch without a device-side count.
+__device__ const int g_no_tile_limit = 0x7fffffff;
 
 // AM: activation source -- 0: e4m3 codes + e8m0 scales (aq, as); 1: fake-quantized bf16 rows (xa), codes recovered
 // exactly; 2: raw bf16 token rows x[x_rows[r]] quantized here with the reference's act_quant (mx_xform_in_fp8 fused).
@@ -158,9 +160,16 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
   static_assert(!(KSPLIT && ABF), "the K split stages codes");
   constexpr int NT = 64 * W;
   extern __shared__ __align__(16) uint8_t smem[];
-  if (a.ntiles_dev && int(blockIdx.y) >= *a.ntiles_dev) return;
+  // The tile and the live tile count are loaded together (the tile slot is in bounds: the grid has one row per
+  // slot), then the expert's table entries, then the weights: three dependent loads before the first weight byte
+  // instead of five.
   const Exl3Tile tile = a.tiles[blockIdx.y];
-  if (tile.rows <= 0) return;
+  const int live = *(a.ntiles_dev ? a.ntiles_dev : &g_no_tile_limit);
+  // The arguments the weight stream's first addresses need, read with the tile rather than one after another
+  // behind the table entries.
+  asm volatile("" ::"s"(a.K), "s"(a.N), "s"(a.ldo), "s"(a.rows_cap), "s"(a.split), "s"(a.w_tab[0]), "s"(a.s_tab[0]),
+               "s"(a.w_tab[1]), "s"(a.s_tab[1]), "s"(a.aq), "s"(a.as), "s"(a.xa), "s"(a.out[0]), "s"(a.out32));
+  if (int(blockIdx.y) >= live || tile.rows <= 0 || tile.expert < 0) return;  // all three fields in one load
   const uint8_t* wp[NP];
   const uint8_t* sp[NP];
   wp[0] = a.w_tab[0][tile.expert];
