@@ -192,15 +192,17 @@ __device__ __forceinline__ void quant_token_item(const uint16_t* __restrict__ x,
 // compute the same bits everywhere e^x decides a stored value (the SwiGLU's silu, the softmax and sigmoid routers'
 // weights). Cody-Waite reduction x = n ln2 + r with ln2 split into a 16-significant-bit high part (n ln2_hi is
 // exact for |n| <= 150) and the rest, |r| <= ln2 / 2; e^r by its degree-7 Taylor polynomial in Horner form with
-// fused multiply-adds (truncation below 2^-27 relative); 2^n applied as two exact power-of-two factors so that
-// results down to the subnormal range are one rounding of p 2^n. Within 2 ulp of e^x (tests/test_oracle.py).
-__device__ __forceinline__ float pow2_f32(int e) { return __uint_as_float(uint32_t(e + 127) << 23); }  // -126..127
+// fused multiply-adds (truncation below 2^-27 relative); results down to the subnormal range are one rounding of
+// p 2^n (the oracle applies 2^n as two exact power-of-two factors, here v_ldexp_f32 rounds p 2^n once: the same
+// value). Within 2 ulp of e^x (tests/test_oracle.py).
+// Branch-free: the polynomial path runs for every x, on x clamped into [-103.972084, 88.7228394] (unchanged inside
+// it), and the results past the cut-offs are selected at the end, so a wave of mixed inputs takes no divergent
+// branch.
 __device__ __forceinline__ float exp_f32(float x) {
 #pragma clang fp contract(off)  // every rounding as written (no multiply-add fused into the caller's add)
-  if (!(x < 88.7228394f)) return x != x ? x : __builtin_inff();
-  if (x < -103.972084f) return 0.0f;
-  const float n = rintf(x * 1.44269504f);
-  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+  const float xc = __builtin_amdgcn_fmed3f(x, -103.972084f, 88.7228394f);  // NaN: replaced below
+  const float n = rintf(xc * 1.44269504f);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, xc);
   r = __builtin_fmaf(-n, 1.42860677e-06f, r);
   float p = 1.0f / 5040.0f;
   p = __builtin_fmaf(p, r, 1.0f / 720.0f);
@@ -210,8 +212,10 @@ __device__ __forceinline__ float exp_f32(float x) {
   p = __builtin_fmaf(p, r, 0.5f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  const int ni = int(n), h = ni / 2;
-  return (p * pow2_f32(h)) * pow2_f32(ni - h);
+  float e = __builtin_amdgcn_ldexpf(p, int(n));
+  asm volatile("" : "+v"(e));  // computed on every path: the compiler would otherwise branch around it
+  // x >= 88.7228394: +inf, or x itself (quieted) when x is NaN
+  return !(x < 88.7228394f) ? x + __builtin_inff() : x < -103.972084f ? 0.0f : e;
 }
 
 // SwiGLU with the clamp and optional routing weight (ref_moe.hip:62-74): x = silu(min(g, l)) * clamp(u, +-l), then
