@@ -84,7 +84,9 @@ int uh_exp_f32_array(const float* x, float* y, size_t n, void* stream);
 /* mx_moe.hpp:61: exhaustive MFMA block-scaled decode check; *bad = mismatches among normal results. */
 int uh_mx_check_dequant(unsigned long long* bad, unsigned long long* total);
 
-/* ---- grouped expert GEMV / GEMM (src/kernels/mx_moe.hpp). tiles: int32 triples {expert, row0, rows}.
+/* ---- grouped expert GEMV / GEMM (src/kernels/mx_moe.hpp). tiles: int32 triples {expert, row0, rows}, ntiles of
+ * them (the grid's tile count, as the reference launches it); with ntiles_dev the tiles at or past the device count
+ * are read but not used, so the buffer holds ntiles entries either way.
  * glu_*: the MxGlu epilogue (glu_hh / glu_hq NULL: none); glu_hq + glu_hs: hh as e4m3 codes + e8m0 scales. ---- */
 /* mx_moe.hpp:100-104 */
 int uh_mx_grouped_gemv(const uint16_t* xa, int K, const int32_t* tiles, int ntiles, const uint8_t* const* w_tab,
